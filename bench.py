@@ -1,0 +1,248 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused causal GQA attention path on one MI355X.
+
+A step is one forward (zt_attn_forward) plus one backward (zt_attn_backward)
+over BASELINE.json's C3 workload: B=1, T=4096, 32 query / 8 kv heads,
+head_dim 128, f32, RoPE (theta 500000) pre-applied to Q and K, all inputs
+seeded N(0,1) on the device and resident in HBM before timing.  The headline
+value is fwd+bwd TFLOP/s with the causal-pair FLOP count
+(fwd 2*B*H*d*T(T+1), bwd 5*B*H*d*T(T+1)).  The same line also carries the
+decode step (C4: B=64, 8192 cached keys, GB/s of K/V/q/out) and RMSNorm
+([64,4096] and [4096,4096], GB/s over rotating buffers larger than the 256 MB
+MALL), per-kernel times from HIP events on the launch stream, the roofline of
+the dominant kernel, and the CPU restatement timed on a bounded sample.
+
+    python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--cpu-rows 64] [--no-cpu]
+"""
+import argparse
+import importlib.util
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+METRIC = "causal GQA attn fwd+bwd TFLOP/s f32 (T=4096,d=128); decode attn HBM GB/s"
+PEAK_MFMA_F32 = 157.3   # TFLOP/s, MI355X dense FP32 matrix
+PEAK_HBM = 8000.0       # GB/s, MI355X HBM3E
+SEEDS = {"q": 0x5EED0001, "k": 0x5EED0002, "v": 0x5EED0003, "do": 0x5EED0004, "kc": 0x5EED0005,
+         "vc": 0x5EED0006, "x": 0x5EED0007, "w": 0x5EED0008}
+
+
+def _load(name, rel):
+    spec = importlib.util.spec_from_file_location(name, os.path.join(ROOT, rel))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def event_time(torch, fn, n):
+    """Average ms per call of fn over n back-to-back calls, HIP events on the
+    current stream (the stream every launch here goes to)."""
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(n):
+        fn()
+    e.record()
+    e.synchronize()
+    return s.elapsed_time(e) / n
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--cpu-rows", type=int, default=48, help="query rows of the CPU baseline sample")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU: this build's path runs on one MI355X (per-head/batch sharding "
+              "across GPUs is described in DESIGN.md and not built). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    zt = _load("zt_attn", "z-transformer_amd/zt_attn.py")
+    torch.cuda.set_device(0)
+    dev = "cuda:0"
+    assert zt.lib().zt_attn_lds_limit() > 0, "libzt_attn found no usable gfx950 device"
+
+    def normal(n, seed, sigma=1.0):
+        t = torch.empty(n, device=dev, dtype=torch.float32)
+        zt.fill_normal(t, seed, 0.0, sigma)
+        return t
+
+    # ---------------- C3: fused causal GQA fwd + bwd ----------------
+    B, T, H, Hkv, D = 1, 4096, 32, 8, 128
+    q0, k0 = normal(B * T * H * D, SEEDS["q"]), normal(B * T * Hkv * D, SEEDS["k"])
+    q, k = torch.empty_like(q0), torch.empty_like(k0)
+    zt.rope(q0, q, B * T, H * D, 0, 500000.0, D)
+    zt.rope(k0, k, B * T, Hkv * D, 0, 500000.0, D)
+    del q0, k0
+    v, do = normal(B * T * Hkv * D, SEEDS["v"]), normal(B * T * H * D, SEEDS["do"])
+    out, dq = torch.empty_like(q), torch.empty_like(q)
+    dk, dv = torch.empty_like(k), torch.empty_like(v)
+    rm, rl, rd = (torch.empty(B * T * H, device=dev) for _ in range(3))
+
+    def fwd():
+        zt.forward(q, k, v, out, T, H, Hkv, D)
+
+    def bwd():
+        zt.backward(q, k, v, do, dq, dk, dv, rm, rl, rd, T, H, Hkv, D)
+
+    def bwd_dq():
+        zt.bwd_dq(q, k, v, do, dq, rm, rl, rd, T, H, Hkv, D)
+
+    def bwd_dkdv():
+        zt.bwd_dkdv(q, k, v, do, dk, dv, rm, rl, rd, T, H, Hkv, D)
+
+    def step():
+        fwd()
+        bwd()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t_wall = time.perf_counter()
+    s.record()
+    for _ in range(args.steps):
+        step()
+    e.record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t_wall) * 1e3 / args.steps
+    ms_step = s.elapsed_time(e) / args.steps
+    pairs = B * H * T * (T + 1) / 2          # causal (query, key) pairs over all heads
+    unit = 2 * D * pairs                      # FLOPs of one T x T x d causal matmul
+    fwd_flop, bwd_flop = 2 * unit, 5 * unit
+    value = (fwd_flop + bwd_flop) / (ms_step * 1e-3) / 1e12
+    log(f"C3 step: {ms_step:.3f} ms (wall {wall_ms:.3f} ms), {value:.2f} TFLOP/s fwd+bwd")
+
+    n_k = max(3, args.steps)
+    t_fwd = event_time(torch, fwd, n_k)
+    bwd_dq()
+    t_dq = event_time(torch, bwd_dq, n_k)
+    t_dkdv = event_time(torch, bwd_dkdv, n_k)
+    # Algorithmic FLOPs per launch: the forward's two matmuls; of the backward's
+    # five (S recompute, dP, dV, dK, dQ) the dk/dv kernel owns four and the dq
+    # kernel one -- the dq kernel's own recompute earns no credit.
+    kernels = [
+        {"kernel": f"zt_fwd_d128", "ms": t_fwd, "flop": fwd_flop},
+        {"kernel": f"zt_bwd_dq_d128", "ms": t_dq, "flop": unit},
+        {"kernel": f"zt_bwd_dkdv_d128_hs4", "ms": t_dkdv, "flop": 4 * unit},
+    ]
+    for kk in kernels:
+        kk["tflops"] = kk["flop"] / (kk["ms"] * 1e-3) / 1e12
+        kk["frac_mfma_f32"] = kk["tflops"] / PEAK_MFMA_F32
+        log(f"  {kk['kernel']}: {kk['ms']:.3f} ms, {kk['tflops']:.2f} TFLOP/s ({100 * kk['frac_mfma_f32']:.1f}% of "
+            f"FP32 MFMA peak)")
+    fwd_tflops = fwd_flop / (t_fwd * 1e-3) / 1e12
+    bwd_tflops = bwd_flop / ((t_dq + t_dkdv) * 1e-3) / 1e12
+    log(f"  forward {fwd_tflops:.2f} TFLOP/s ({100 * fwd_tflops / PEAK_MFMA_F32:.1f}%), backward "
+        f"{bwd_tflops:.2f} TFLOP/s ({100 * bwd_tflops / PEAK_MFMA_F32:.1f}%)")
+    dom = max(kernels, key=lambda x: x["ms"])
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get(dom["kernel"])
+    roofline = {"bound": "mfma", "achieved": round(dom["tflops"], 3), "peak": PEAK_MFMA_F32, "unit": "TFLOP/s",
+                "frac": round(dom["tflops"] / PEAK_MFMA_F32, 4), "traffic": traffic, "kernel": dom["kernel"]}
+    del out, dq, dk, dv, do, q, k, v, rm, rl, rd
+
+    # ---------------- C4: decode step ----------------
+    Bd, n_ctx = 64, 8192
+    qd = normal(Bd * H * D, SEEDS["q"])
+    kc = normal(Bd * n_ctx * Hkv * D, SEEDS["kc"])
+    vc = normal(Bd * n_ctx * Hkv * D, SEEDS["vc"])
+    od = torch.empty_like(qd)
+    ws = torch.empty(zt.decode_workspace_bytes(Bd, n_ctx, H, Hkv, D) // 4 + 1, device=dev)
+    n_keys = [n_ctx] * Bd
+
+    def dec():
+        zt.decode(qd, kc, vc, od, n_keys, Bd, n_ctx, H, Hkv, D, ws)
+
+    for _ in range(3):
+        dec()
+    t_dec = event_time(torch, dec, max(10, args.steps))
+    dec_bytes = 2 * Bd * n_ctx * Hkv * D * 4 + 2 * Bd * H * D * 4
+    dec_gbs = dec_bytes / (t_dec * 1e-3) / 1e9
+    log(f"C4 decode: {t_dec * 1e3:.1f} us, {dec_gbs:.0f} GB/s ({100 * dec_gbs / PEAK_HBM:.1f}% of HBM peak)")
+    del kc, vc, qd, od, ws
+
+    # ---------------- RMSNorm over rotating buffers ----------------
+    norm = {}
+    for rows, cols, sets in ((64, 4096, 256), (4096, 4096, 4)):
+        xs = normal(sets * rows * cols, SEEDS["x"]).view(sets, rows * cols)
+        ys = torch.empty_like(xs)
+        w = torch.empty(cols, device=dev)
+        zt.fill_uniform(w, SEEDS["w"], 0.5, 1.5)
+        it = [0]
+
+        def nrm():
+            i = it[0] % sets
+            it[0] += 1
+            zt.rmsnorm(xs[i], w, ys[i], rows, cols)
+
+        for _ in range(sets):
+            nrm()
+        t_n = event_time(torch, nrm, 4 * sets)
+        nb = (2 * rows * cols + cols) * 4
+        gbs = nb / (t_n * 1e-3) / 1e9
+        norm[f"{rows}x{cols}"] = {"us": round(t_n * 1e3, 3), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM, 4),
+                                  "bytes": nb, "rotating_sets": sets}
+        log(f"RMSNorm {rows}x{cols}: {t_n * 1e3:.2f} us, {gbs:.0f} GB/s")
+        del xs, ys
+
+    # ---------------- CPU baseline: the restatement on a bounded sample ----------------
+    cpu = None
+    if not args.no_cpu:
+        import numpy as np
+        oracle = _load("zt_oracle", "oracle/zt_oracle.py")
+        W = max(1, min(args.cpu_rows, T))
+        qh = oracle.fill_normal(B * T * H * D, SEEDS["q"])
+        kh = oracle.fill_normal(B * T * Hkv * D, SEEDS["k"])
+        qh = oracle.rope(qh, B * T, H * D, 0, 500000.0, D)
+        kh = oracle.rope(kh, B * T, Hkv * D, 0, 500000.0, D)
+        vh = oracle.fill_normal(B * T * Hkv * D, SEEDS["v"])
+        dh = oracle.fill_normal(B * T * H * D, SEEDS["do"])
+        t0 = time.perf_counter()
+        oracle.attention_forward(qh, kh, vh, B, T, H, Hkv, D, t_begin=T - W, threads=1)
+        oracle.attention_backward(qh, kh, vh, dh, B, T, H, Hkv, D, t_begin=T - W, threads=1)
+        secs = time.perf_counter() - t0
+        spairs = B * H * sum(t + 1 for t in range(T - W, T))
+        sflop = 14 * D * spairs    # fwd 4d + bwd 10d FLOPs per causal pair, as the GPU figure counts
+        cpu = {"value": round(sflop / secs / 1e12, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
+               "sample": f"C3 query rows {T - W}..{T - 1} ({W} of {T}, all {H} heads, full causal prefix), "
+                         f"forward+backward of the C restatement of attention.zig/autograd.zig, 1 thread, "
+                         f"{secs:.1f} s", "seconds": round(secs, 2)}
+        log(f"CPU baseline: {cpu['value'] * 1e3:.3f} GFLOP/s on {W} rows ({secs:.1f} s)")
+        del np
+
+    line = {
+        "metric": METRIC, "value": round(value, 3), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic: splitmix64/Box-Muller N(0,1) generated on the device, RoPE theta=500000 on Q/K",
+        "config": {"workload": "C3 causal GQA forward+backward, B=1 T=4096 Hq=32 Hkv=8 d=128 f32",
+                   "global_batch": B, "seq_len": T, "n_heads": H, "n_kv_heads": Hkv, "head_dim": D,
+                   "parallelism": "none (1 GPU)"},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "fwd_tflops": round(fwd_tflops, 3), "bwd_tflops": round(bwd_tflops, 3),
+        "kernels": [{k2: (round(v2, 4) if isinstance(v2, float) else v2) for k2, v2 in kk.items()} for kk in kernels],
+        "decode": {"workload": "C4 B=64 n_keys=8192 Hq=32 Hkv=8 d=128 f32", "us": round(t_dec * 1e3, 2),
+                   "GB/s": round(dec_gbs, 1), "bytes": dec_bytes, "frac_hbm": round(dec_gbs / PEAK_HBM, 4)},
+        "rmsnorm": norm,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

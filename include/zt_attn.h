@@ -1,0 +1,147 @@
+/*
+ * zt_attn.h -- C ABI of the MI355X (gfx950) fused causal GQA attention and
+ * RMSNorm library, libzt_attn.so.
+ *
+ * The first six entry points keep the names, argument meaning, return values
+ * and refusal order of the reference's C ABI in src/cuda/attn_kernels.cu
+ * (mirrored by the Zig FFI in src/cuda/device.zig:58-105), so the reference's
+ * device.Attn holder binds them unchanged once its three runtime externs
+ * (cudaMalloc/Free/Memcpy, device.zig:112-117) are renamed to their hip*
+ * twins.  The stream argument is a hipStream_t (NULL = the default stream).
+ *
+ * Conventions, as in the reference (attn_kernels.cu:18-54, 940-951):
+ *   - device pointers in; the CALLER owns all memory; nothing here allocates;
+ *   - return 0 = the launch was accepted (asynchronous: a device fault shows
+ *     only at the caller's next synchronising call);
+ *   - return 1 = refused, with the reason on stderr; never exit();
+ *   - outputs (out, dq, dk, dv) are assigned, never accumulated into.
+ * Layout: dense row-major f32 (src/tensor.zig:3-54): q/out/dout/dq are
+ * [T, n_heads*dim], k/v/dk/dv are [T, n_kv_heads*dim]; query head h reads kv
+ * head h / (n_heads / n_kv_heads) (src/attention.zig:111-112).
+ *
+ * Everything after the six is an extension with no reference counterpart and
+ * says so.
+ */
+#ifndef ZT_ATTN_H
+#define ZT_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Same type as HIP's own hipStream_t (hip_runtime_api.h). */
+typedef struct ihipStream_t *hipStream_t;
+
+/* ---- The reference's six entry points -------------------------------- */
+
+/* Replaces zt_attn_dim_ok, src/cuda/attn_kernels.cu:648-659.  1 iff dim is
+ * even and in [32, 256]; prints nothing. */
+int zt_attn_dim_ok(int dim);
+
+/* Replace zt_attn_forward_shmem / zt_attn_bwd_dq_shmem /
+ * zt_attn_bwd_dkdv_shmem, src/cuda/attn_kernels.cu:692-706.  Pure byte
+ * counts: the LDS bytes per workgroup THIS library's kernel asks at head width
+ * `dim` with its key tile capped at `tile` (a tile cap below 64 selects the
+ * 32-key tile; `group_q` does not change this library's schedule and is
+ * ignored here).  The dk/dv figure is the most that kernel asks at `dim`.
+ * 0 for a width zt_attn_dim_ok refuses. */
+size_t zt_attn_forward_shmem(int dim, int tile, int group_q);
+size_t zt_attn_bwd_dq_shmem(int dim, int tile);
+size_t zt_attn_bwd_dkdv_shmem(int dim);
+
+/* Replaces zt_attn_forward, src/cuda/attn_kernels.cu:833-938.
+ * out[t] for query rows t in [0, T) at absolute positions q_offset + t, over
+ * keys s <= q_offset + t, s < n_keys (k/v hold at least n_keys rows).
+ * Refusal order: T < 1; width; group; n_heads > 65535; group_q outside
+ * [1, 64] or dim*group_q > 1024; q_offset < 0 || n_keys < 1 ||
+ * q_offset > n_keys - T; max_tile < 1; device LDS ceiling unreadable; no
+ * tile fits.  group_q is validated exactly as the reference does and
+ * otherwise has no effect (every wave owns 16 query rows). */
+int zt_attn_forward(const float *q, const float *k, const float *v, float *out, int T, int n_heads,
+                    int n_kv_heads, int dim, int group_q, int max_tile, int q_offset, int n_keys,
+                    hipStream_t stream);
+
+/* Replaces zt_attn_backward, src/cuda/attn_kernels.cu:952-1036.
+ * dq [T, n_heads*dim], dk/dv [T, n_kv_heads*dim]; row_max/row_den/row_del are
+ * [T, n_heads] scratch that the first kernel writes (max score, softmax
+ * denominator exp-sum, and delta = sum_s p*dp) and the second reads on the
+ * same stream.  Refusal order: T < 1; width; group; n_heads > 65535;
+ * max_tile < 1; LDS ceiling unreadable; no tile fits. */
+int zt_attn_backward(const float *q, const float *k, const float *v, const float *dout, float *dq,
+                     float *dk, float *dv, float *row_max, float *row_den, float *row_del, int T,
+                     int n_heads, int n_kv_heads, int dim, int max_tile, hipStream_t stream);
+
+/* ---- Extensions (no reference counterpart) ---------------------------- */
+
+/* Batched forward: B independent sequences.  q/out [B, T, n_heads*dim];
+ * k/v [B, kv_rows, n_kv_heads*dim] (kv_rows >= n_keys rows per sequence, so a
+ * preallocated cache can be passed whole).  Same semantics and refusals as
+ * zt_attn_forward per sequence, plus B < 1 and kv_rows < n_keys. */
+int zt_attn_forward_batched(const float *q, const float *k, const float *v, float *out, int B, int T,
+                            int n_heads, int n_kv_heads, int dim, int group_q, int max_tile,
+                            int q_offset, int n_keys, int kv_rows, hipStream_t stream);
+
+/* Batched backward: q/dout/dq [B, T, n_heads*dim]; k/v/dk/dv
+ * [B, T, n_kv_heads*dim]; row_* [B, T, n_heads]. */
+int zt_attn_backward_batched(const float *q, const float *k, const float *v, const float *dout,
+                             float *dq, float *dk, float *dv, float *row_max, float *row_den,
+                             float *row_del, int B, int T, int n_heads, int n_kv_heads, int dim,
+                             int max_tile, hipStream_t stream);
+
+/* The two stages of zt_attn_backward_batched, for callers that schedule them
+ * apart (and for per-stage timing).  zt_attn_bwd_dq writes dq and the row
+ * statistics; zt_attn_bwd_dkdv reads those statistics and writes dk/dv, so on
+ * one stream dq must run first.  Same layouts and refusals as the batched
+ * backward (dkdv uses the default tile cap). */
+int zt_attn_bwd_dq(const float *q, const float *k, const float *v, const float *dout, float *dq, float *row_max,
+                   float *row_den, float *row_del, int B, int T, int n_heads, int n_kv_heads, int dim, int max_tile,
+                   hipStream_t stream);
+int zt_attn_bwd_dkdv(const float *q, const float *k, const float *v, const float *dout, float *dk, float *dv,
+                     const float *row_max, const float *row_den, const float *row_del, int B, int T, int n_heads,
+                     int n_kv_heads, int dim, hipStream_t stream);
+
+/* Decode step over a KV cache, split over the key axis.  q/out [B, n_heads*dim];
+ * k_cache/v_cache [B, n_ctx, n_kv_heads*dim] (the src/kv_cache.zig:58-63
+ * layout per sequence); sequence b attends its first n_keys[b] cached rows,
+ * its query sitting at position n_keys[b]-1 (src/decode.zig:326-392).
+ * n_keys is a HOST array of B ints in [1, n_ctx].  `workspace` is device
+ * memory of at least zt_attn_decode_workspace(...) bytes (chunk partials).
+ * Refuses B < 1, n_ctx < 1, a refused width or group, an n_keys outside
+ * [1, n_ctx], a null pointer, or a short workspace. */
+size_t zt_attn_decode_workspace(int B, int n_ctx, int n_heads, int n_kv_heads, int dim);
+int zt_attn_decode(const float *q, const float *k_cache, const float *v_cache, float *out,
+                   const int *n_keys, int B, int n_ctx, int n_heads, int n_kv_heads, int dim,
+                   void *workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* RMSNorm, src/norm.zig:18-47 on the device (the reference's src/cuda/norm.cu
+ * kernel has no C entry point).  x/y [rows, cols], w [cols]; eps is
+ * src/norm.zig:14's 1e-5 for the reference's behaviour.  rows == 0 launches
+ * nothing and returns 0 (norm.forward on zero rows is an empty result);
+ * refuses rows < 0, cols < 1, eps < 0, null pointers. */
+int zt_rmsnorm_forward(const float *x, const float *w, float *y, int rows, int cols, double eps,
+                       hipStream_t stream);
+
+/* RoPE, src/rope.zig:21-55 on the device (input preparation: Q/K rotated
+ * before attention).  x/y [rows, cols], row r at position pos + r.  Refuses
+ * an odd or non-positive head_dim (rope.zig:28) and cols % head_dim != 0
+ * (rope.zig:29). */
+int zt_rope_forward(const float *x, float *y, int rows, int cols, int pos, double theta,
+                    int head_dim, hipStream_t stream);
+
+/* Seeded synthetic inputs (splitmix64 counter stream + Box-Muller): element i
+ * depends only on (seed, i).  normal: mean + sigma*z; uniform: [lo, hi). */
+int zt_fill_normal(float *dst, size_t n, uint64_t seed, double mean, double sigma, hipStream_t stream);
+int zt_fill_uniform(float *dst, size_t n, uint64_t seed, double lo, double hi, hipStream_t stream);
+
+/* Library version string, and the LDS ceiling per workgroup the library read
+ * for the current device (0 = no usable device / code object). */
+const char *zt_attn_version(void);
+size_t zt_attn_lds_limit(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

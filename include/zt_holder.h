@@ -1,0 +1,67 @@
+/*
+ * zt_holder.h -- the host-side holder of the reference's Zig FFI
+ * (src/cuda/device.zig:119-501), restated in C++ over the zt_attn C ABI, plus
+ * a C face of it so foreign callers (and this repository's tests) can drive it.
+ *
+ * The holder owns the eleven device buffers a forward/backward pass at one
+ * shape needs (device.zig:185-212), sizes them once with overflow-checked
+ * arithmetic, validates every call before it reaches the device, and maps each
+ * failure to one of the reference's five errors (device.zig:119-141).
+ * Allocation goes through hipMalloc/hipFree/hipMemcpy, the HIP twins of the
+ * three runtime externs the reference binds (device.zig:112-117).
+ */
+#ifndef ZT_HOLDER_H
+#define ZT_HOLDER_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* device.zig:119-141.  0 is success. */
+enum zt_error {
+    ZT_OK = 0,
+    ZT_DEGENERATE_SHAPE = 1,
+    ZT_SHAPE_TOO_LARGE = 2,
+    ZT_CONFIG_REFUSED = 3,
+    ZT_DEVICE_ALLOC_FAILED = 4,
+    ZT_DEVICE_TRANSFER_FAILED = 5,
+};
+
+/* device.zig:143-160 (Kind). */
+enum zt_kind { ZT_QUERY_HEADED = 0, ZT_KV_HEADED = 1, ZT_PER_ROW = 2 };
+
+/* device.zig:162-171 (bytesFor): bytes of one buffer of `kind`. */
+int zt_bytes_for(int kind, size_t t, size_t n_heads, size_t n_kv_heads, size_t dim, size_t *out);
+/* device.zig:179-182 (toCInt). */
+int zt_to_cint(size_t x, int *out);
+/* device.zig:489-501 (forwardBounds): ZT_OK or ZT_SHAPE_TOO_LARGE. */
+int zt_forward_bounds(int c_t, int q_offset, int n_keys, int t);
+
+/* The buffers of a holder, in device.zig's field order (:186-196). */
+enum zt_buffer {
+    ZT_BUF_Q = 0, ZT_BUF_K, ZT_BUF_V, ZT_BUF_OUT, ZT_BUF_DOUT, ZT_BUF_DQ, ZT_BUF_DK, ZT_BUF_DV,
+    ZT_BUF_ROW_MAX, ZT_BUF_ROW_DEN, ZT_BUF_ROW_DEL, ZT_N_BUFFERS
+};
+
+typedef struct zt_holder zt_holder;
+
+/* device.zig:221-299 (Attn.init): refuses via zt_attn_dim_ok and the group
+ * check BEFORE allocating; on an allocation failure frees what it took. */
+int zt_holder_init(size_t t, size_t n_heads, size_t n_kv_heads, size_t dim, zt_holder **out);
+void zt_holder_deinit(zt_holder *h);                                   /* :328-330 */
+size_t zt_holder_total_bytes(const zt_holder *h);                     /* :332-341 */
+float *zt_holder_buffer(const zt_holder *h, int which);
+int zt_holder_forward(const zt_holder *h, int group_q, int max_tile); /* :376-379 */
+int zt_holder_forward_at(const zt_holder *h, int group_q, int max_tile, int q_offset, int n_keys,
+                         int t);                                      /* :381-398 */
+int zt_holder_backward(const zt_holder *h, int max_tile);             /* :400-406 */
+/* :412-431: bounds-checked against the target buffer's real byte count. */
+int zt_holder_upload(const zt_holder *h, int which, const float *src, size_t n_floats);
+int zt_holder_download(const zt_holder *h, float *dst, int which, size_t n_floats);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

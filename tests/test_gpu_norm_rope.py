@@ -1,0 +1,93 @@
+"""RMSNorm (src/norm.zig:18-47) and RoPE (src/rope.zig:21-55) on the GPU
+against the CPU restatement.  RMSNorm gate: the reference kernel's 1e-5
+absolute (src/cuda/norm.cu:56); the f64 sum of squares differs from the
+reference's sequential sum only in association, so nearly every element is
+bit-identical."""
+import numpy as np
+import pytest
+
+from gpuhelp import SEED_W, SEED_X, THETA, dev_normal, dev_uniform, host, max_abs
+
+pytestmark = pytest.mark.gpu
+
+
+def _norm(gpu, zt, x, w, rows, cols, eps=1e-5):
+    y = gpu.full((rows * cols,), float("nan"), device="cuda", dtype=gpu.float32)
+    zt.rmsnorm(x, w, y, rows, cols, eps)
+    gpu.cuda.synchronize()
+    return host(y)
+
+
+@pytest.mark.parametrize("rows,cols", [(64, 4096), (4096, 4096), (1, 1), (3, 3), (5, 4), (7, 100), (9, 1023),
+                                       (2, 4097), (4, 16384), (3, 20000), (256, 128), (1000, 2)])
+def test_rmsnorm_matches_twin(gpu, zt, oracle, rows, cols):
+    x = dev_normal(gpu, zt, rows * cols, SEED_X)
+    w = dev_uniform(gpu, zt, cols, SEED_W, 0.5, 1.5)
+    y = _norm(gpu, zt, x, w, rows, cols)
+    ref = oracle.rmsnorm(host(x), host(w), rows, cols)
+    assert max_abs(y, ref) <= 1e-5
+    assert np.mean(y.view(np.uint32) == ref.view(np.uint32)) >= 0.999
+
+
+def test_rmsnorm_reference_known_answers(gpu, zt, golden):
+    for c in golden["rmsnorm"]:
+        x = gpu.tensor(np.float32(c["x"]), device="cuda")
+        w = gpu.tensor(np.float32(c["w"]), device="cuda")
+        y = _norm(gpu, zt, x, w, c["rows"], c["cols"])
+        tol = 0.0 if c["tol"] is None else c["tol"]
+        assert max_abs(y, c["y"]) <= tol, c["src"]
+    c = golden["rmsnorm_f64_row"]
+    x = gpu.full((c["cols"],), np.float32(c["x"]).item(), device="cuda", dtype=gpu.float32)
+    y = _norm(gpu, zt, x, gpu.ones(c["cols"], device="cuda"), 1, c["cols"])
+    assert abs(float(y[0]) - c["exact"]) <= c["tol"]
+
+
+def test_rmsnorm_zero_rows_and_zero_values(gpu, zt):
+    w = gpu.ones(8, device="cuda")
+    y = gpu.empty(0, device="cuda")
+    zt.rmsnorm(gpu.empty(0, device="cuda"), w, y, 0, 8)
+    x = gpu.zeros(16, device="cuda")
+    out = _norm(gpu, zt, x, w, 2, 8)
+    assert np.all(out == 0)
+
+
+def test_rmsnorm_gate_catches_broken_references(gpu, zt, oracle):
+    # src/cuda/norm.cu:58-86 variants: weight + 1e-3, mean instead of mean of squares.
+    rows, cols = 16, 512
+    x = dev_normal(gpu, zt, rows * cols, SEED_X)
+    w = dev_uniform(gpu, zt, cols, SEED_W, 0.5, 1.5)
+    y = _norm(gpu, zt, x, w, rows, cols)
+    xh, wh = host(x), host(w)
+    assert max_abs(y, oracle.rmsnorm(xh, wh + np.float32(1e-3), rows, cols)) > 1e-5
+    xr = xh.reshape(rows, cols).astype(np.float64)
+    mean_not_sq = (xr / np.float32(np.sqrt(np.abs(xr.mean(1, keepdims=True)) + 1e-5)) * wh).ravel()
+    assert max_abs(y, mean_not_sq) > 1e-5
+
+
+@pytest.mark.parametrize("rows,heads,hd,pos", [(4096, 32, 128, 0), (17, 3, 6, 5), (8, 2, 256, 1000), (1, 1, 2, 1)])
+def test_rope_matches_twin(gpu, zt, oracle, rows, heads, hd, pos):
+    cols = heads * hd
+    x = dev_normal(gpu, zt, rows * cols, SEED_X)
+    y = gpu.empty_like(x)
+    zt.rope(x, y, rows, cols, pos, THETA, hd)
+    gpu.cuda.synchronize()
+    ref = oracle.rope(host(x), rows, cols, pos, THETA, hd)
+    assert max_abs(host(y), ref) <= 2e-6
+
+
+def test_rope_reference_known_answers(gpu, zt, golden):
+    for c in golden["rope"]:
+        x = gpu.tensor(np.float32(c["x"]), device="cuda")
+        y = gpu.empty_like(x)
+        zt.rope(x, y, c["rows"], c["cols"], c["pos"], THETA, c["head_dim"])
+        gpu.cuda.synchronize()
+        tol = 0.0 if c["tol"] is None else c["tol"]
+        assert max_abs(host(y), c["y"]) <= tol, c["src"]
+
+
+def test_device_fill_matches_host_generator(gpu, zt, oracle):
+    t = dev_normal(gpu, zt, 100_000, SEED_X)
+    ref = oracle.fill_normal(100_000, SEED_X)
+    assert max_abs(host(t), ref) <= 1e-6
+    u = dev_uniform(gpu, zt, 10_000, SEED_W, 0.5, 1.5)
+    assert max_abs(host(u), oracle.fill_uniform(10_000, SEED_W, 0.5, 1.5)) <= 1e-7

@@ -1,0 +1,64 @@
+// Kernel argument blocks, shared by the device code (kernels/*.hip) and the
+// host launcher (zt_attn.cpp), which passes each one as the single argument of
+// hipModuleLaunchKernel.  Plain C layout: no HIP types.
+#pragma once
+
+struct FwdArgs {
+    const float *q;    // [B, T, H*dim]
+    const float *k;    // [B, kv_rows, Hkv*dim]
+    const float *v;    // [B, kv_rows, Hkv*dim]
+    float *out;        // [B, T, H*dim]
+    int B, T, H, Hkv, dim;
+    int q_offset, n_keys, kv_rows;
+    int HW;            // query heads per workgroup (1, 2 or 4; divides H/Hkv)
+    int n_row_tiles;   // ceil(T / (16 * 4 / HW))
+    int n_head_blocks; // H / HW
+    float scale_log2e; // log2(e) / sqrt(dim)
+};
+
+struct BwdArgs {
+    const float *q, *k, *v, *dout;       // q/dout [B,T,H*dim]; k/v [B,T,Hkv*dim]
+    float *dq, *dk, *dv;                 // assigned, never accumulated into
+    float *row_max, *row_den, *row_del;  // [B,T,H]
+    int B, T, H, Hkv, dim;
+    int HW, n_row_tiles, n_head_blocks;  // dq kernel decomposition (as the forward)
+    int HS, n_key_tiles;                 // dk/dv kernel: head split, ceil(T / (16 * 4/HS))
+    float scale, scale_log2e;
+};
+
+#define ZT_DEC_MAXB 64  // sequences per decode launch (n_keys travels in the arguments)
+
+struct DecArgs {
+    const float *q;   // [B, H*dim]
+    const float *kc;  // [B, n_ctx, Hkv*dim]
+    const float *vc;  // [B, n_ctx, Hkv*dim]
+    float *out;       // [B, H*dim]
+    float *part_acc;  // [B, H, n_chunks, dim]
+    float *part_ml;   // [B, H, n_chunks, 2]
+    int n_keys[ZT_DEC_MAXB];
+    int b_base, nb, n_ctx, H, Hkv, dim;
+    int chunk;     // keys per workgroup
+    int n_chunks;  // chunk slots per (sequence, head) in the workspace
+    int n_gsub;    // head sub-groups per kv group (group / G)
+    float scale_log2e;
+};
+
+struct NormArgs {
+    const float *x, *w;
+    float *y;
+    int rows, cols;
+    double eps;
+};
+
+struct RopeArgs {
+    const float *x;
+    float *y;
+    int rows, cols, pos, head_dim;
+    double theta;
+};
+
+struct FillArgs {
+    float *dst;
+    unsigned long long n, seed;
+    double p0, p1;  // normal: mean, sigma; uniform: lo, hi
+};

@@ -1,0 +1,317 @@
+// Fused causal grouped-query attention, backward, f32 on FP32 MFMA (gfx950).
+//
+// Two kernels on one stream, no atomics, so every run is bit-reproducible --
+// the determinism argument of src/cuda/attn_kernels.cu:538-543 kept, with a
+// different schedule:
+//
+// Kernel A (zt_bwd_dq_*), Q-outer.  Same workgroup shape as the forward: 4
+// waves = HW query heads of one kv group x (4 / HW) blocks of 16 rows, K/V
+// tiles staged in LDS once per kv group.  Per key tile it forms
+// S^T = K Q^T and dP^T = V dO^T on MFMA, keeps the online softmax, and
+// accumulates a0 = sum_s p~ k_s and a1 = sum_s p~ dp_s k_s, so that at the end
+//     delta = sum p~ dp / l,   dq = scale (a1 - delta a0) / l
+// -- the identity src/cuda/attn_kernels.cu:508-517 uses (dq = sum_s
+// p (dp - delta) k scale, autograd.zig:799-820).  It writes the per-row
+// row_max (natural units), row_den and row_del, the scratch contract of
+// attn_kernels.cu:520-532.
+//
+// Kernel B (zt_bwd_dkdv_*), KV-outer.  A workgroup owns 16*KW keys of one kv
+// group: wave (kb, hs) owns 16 keys and every HS-th query head of the group.
+// K and V stay in registers; Q and dO rows are staged in LDS 16 rows at a
+// time for the suffix t >= s.  With the row statistics from kernel A:
+//     p = exp(S - row_max) / row_den,  dS = p (dP - row_del)
+//     dV^T += dO^T P,   dK^T += Q^T dS      (MFMA, P and dS register-resident)
+// The HS head-split partials are summed in LDS in a fixed order at the end.
+// dv carries no scale, dk carries 1/sqrt(d) (autograd.zig:829-836).
+#include "common.h"
+#include "args.h"
+
+
+template <int DP, int BK>
+__device__ __forceinline__ void bwd_dq_body(const BwdArgs &a) {
+    constexpr int LW = DP + 4, DQ = DP / 4, NT = DP / 16, NJ = BK / 16;
+    __shared__ float Ks[BK * LW];
+    __shared__ float Vs[BK * LW];
+
+    const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, grp = lane >> 4, w = tid >> 6;
+    const int RB = 4 / a.HW;
+    const int per_tile = a.n_head_blocks * a.B;
+    const int tile = a.n_row_tiles - 1 - (int)blockIdx.x / per_tile;
+    const int rem = (int)blockIdx.x % per_tile;
+    const int hb = rem % a.n_head_blocks, b = rem / a.n_head_blocks;
+    const int group = a.H / a.Hkv;
+    const int h = hb * a.HW + (w % a.HW);
+    const int kvh = h / group;
+    const int wg_row0 = tile * 16 * RB;
+    const int row0 = wg_row0 + 16 * (w / a.HW);
+    const bool vec4 = (a.dim & 3) == 0;
+    const size_t qld = (size_t)a.H * a.dim, kld = (size_t)a.Hkv * a.dim;
+    const size_t qoff = (size_t)b * a.T * qld + (size_t)h * a.dim;
+    const float *kb = a.k + (size_t)b * a.T * kld + (size_t)kvh * a.dim;
+    const float *vb = a.v + (size_t)b * a.T * kld + (size_t)kvh * a.dim;
+
+    const int my_row = row0 + l16;
+    const bool row_ok = my_row < a.T;
+    float qr[DQ], dor[DQ];
+    load_row_seg<DQ>(qr, a.q + qoff + (size_t)my_row * qld, grp * DQ, a.dim, vec4, row_ok, a.scale_log2e);
+    load_row_seg<DQ>(dor, a.dout + qoff + (size_t)my_row * qld, grp * DQ, a.dim, vec4, row_ok, 1.f);
+
+    f4 a0[NT], a1[NT];
+#pragma unroll
+    for (int i = 0; i < NT; ++i) { a0[i] = zero4(); a1[i] = zero4(); }
+    float m = -INFINITY, lsum = 0.f, dlsum = 0.f;
+    const int kend_wg = min(a.T, wg_row0 + 16 * RB);
+    const int kend_w = row0 < a.T ? min(a.T, row0 + 16) : 0;
+
+    for (int k0 = 0; k0 < kend_wg; k0 += BK) {
+        __syncthreads();
+        const int nvalid = min(BK, a.T - k0);
+        stage_rows<DP, LW, 256>(Ks, kb + (size_t)k0 * kld, kld, BK, nvalid, a.dim, vec4, tid);
+        stage_rows<DP, LW, 256>(Vs, vb + (size_t)k0 * kld, kld, BK, nvalid, a.dim, vec4, tid);
+        __syncthreads();
+        if (k0 >= kend_w) continue;
+
+        f4 s[NJ], dp[NJ];
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            s[j] = zero4();
+            dp[j] = zero4();
+            if (k0 + 16 * j < kend_w) {
+                const float *krow = Ks + (16 * j + l16) * LW + grp * DQ;
+                const float *vrow = Vs + (16 * j + l16) * LW + grp * DQ;
+#pragma unroll
+                for (int kk = 0; kk < DQ; kk += 4) {
+                    const f4 kx = *reinterpret_cast<const f4 *>(krow + kk);
+                    const f4 vx = *reinterpret_cast<const f4 *>(vrow + kk);
+                    s[j] = mfma16(kx.x, qr[kk + 0], s[j]);
+                    dp[j] = mfma16(vx.x, dor[kk + 0], dp[j]);
+                    s[j] = mfma16(kx.y, qr[kk + 1], s[j]);
+                    dp[j] = mfma16(vx.y, dor[kk + 1], dp[j]);
+                    s[j] = mfma16(kx.z, qr[kk + 2], s[j]);
+                    dp[j] = mfma16(vx.z, dor[kk + 2], dp[j]);
+                    s[j] = mfma16(kx.w, qr[kk + 3], s[j]);
+                    dp[j] = mfma16(vx.w, dor[kk + 3], dp[j]);
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int key = k0 + 16 * j + 4 * grp + r;
+                if (key > my_row || key >= a.T) s[j][r] = -INFINITY;
+            }
+        }
+        float mt = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+            mt = fmaxf(mt, fmaxf(fmaxf(s[j][0], s[j][1]), fmaxf(s[j][2], s[j][3])));
+        mt = max4grp(mt);
+        const float mnew = fmaxf(m, mt);
+        const float corr = exp2f(m - mnew);
+        m = mnew;
+        float ps = 0.f, pds = 0.f;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float p = exp2f(s[j][r] - mnew);
+                s[j][r] = p;
+                dp[j][r] *= p;  // p~ dp
+                ps += p;
+                pds += dp[j][r];
+            }
+        lsum = lsum * corr + ps;
+        dlsum = dlsum * corr + pds;
+#pragma unroll
+        for (int i = 0; i < NT; ++i) { a0[i] *= corr; a1[i] *= corr; }
+
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            if (k0 + 16 * j >= kend_w) continue;
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+                const float pv = s[j][kk], pd = dp[j][kk];
+                const float *krow = Ks + (16 * j + 4 * grp + kk) * LW + l16;
+#pragma unroll
+                for (int i = 0; i < NT; ++i) {
+                    const float kx = krow[16 * i];
+                    a0[i] = mfma16(kx, pv, a0[i]);
+                    a1[i] = mfma16(kx, pd, a1[i]);
+                }
+            }
+        }
+    }
+
+    const float l = sum4grp(lsum);
+    const float delta = sum4grp(dlsum) / l;
+    const float f = a.scale / l;
+    if (row_ok) {
+        float *dqrow = a.dq + qoff + (size_t)my_row * qld;
+#pragma unroll
+        for (int i = 0; i < NT; ++i) store4(dqrow, 16 * i + 4 * grp, a.dim, vec4, (a1[i] - delta * a0[i]) * f);
+        if (grp == 0) {
+            const size_t o = ((size_t)b * a.T + my_row) * a.H + h;
+            a.row_max[o] = m * 0.69314718055994531f;  // back to natural units
+            a.row_den[o] = l;
+            a.row_del[o] = delta;
+        }
+    }
+}
+
+template <int DP, int HS>
+__device__ __forceinline__ void bwd_dkdv_body(const BwdArgs &a) {
+    constexpr int LW = DP + 4, DQ = DP / 4, NT = DP / 16, KW = 4 / HS;
+    constexpr int BQ = 16;
+    // Per head-split part: Q rows, dO rows, and (m2, 1/l, delta) per row.
+    // One buffer: the staging tiles, reused at the end for the head-split sum,
+    // which needs (HS-1)*KW*64*2*NT float4 <= 2*HS*BQ*LW floats for HS in {1,2,4}.
+    __shared__ float smem[2 * HS * BQ * LW + HS * BQ * 4];
+    float *Qs = smem, *Ds = smem + HS * BQ * LW, *St = smem + 2 * HS * BQ * LW;
+    static_assert((HS - 1) * KW * 64 * 2 * NT * 4 <= 2 * HS * BQ * LW, "reduction buffer");
+
+    const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, grp = lane >> 4, w = tid >> 6;
+    const int kbw = w % KW, hs = w / KW;
+    const int per_tile = a.Hkv * a.B;
+    const int ktile = (int)blockIdx.x / per_tile;  // ascending = heaviest first
+    const int rem = (int)blockIdx.x % per_tile;
+    const int kvh = rem % a.Hkv, b = rem / a.Hkv;
+    const int group = a.H / a.Hkv;
+    const int hpp = group / HS;  // heads per part
+    const int wg_s0 = ktile * 16 * KW;
+    const int s0 = wg_s0 + 16 * kbw;
+    const bool vec4 = (a.dim & 3) == 0;
+    const size_t qld = (size_t)a.H * a.dim, kld = (size_t)a.Hkv * a.dim;
+    const size_t kvoff = (size_t)b * a.T * kld + (size_t)kvh * a.dim;
+
+    const int my_key = s0 + l16;
+    const bool key_ok = my_key < a.T;
+    float kr[DQ], vr[DQ];
+    load_row_seg<DQ>(kr, a.k + kvoff + (size_t)my_key * kld, grp * DQ, a.dim, vec4, key_ok, a.scale_log2e);
+    load_row_seg<DQ>(vr, a.v + kvoff + (size_t)my_key * kld, grp * DQ, a.dim, vec4, key_ok, 1.f);
+
+    f4 dka[NT], dva[NT];
+#pragma unroll
+    for (int i = 0; i < NT; ++i) { dka[i] = zero4(); dva[i] = zero4(); }
+
+    float *qs = Qs + hs * BQ * LW;
+    float *ds = Ds + hs * BQ * LW;
+    float *st = St + hs * BQ * 4;
+    for (int hi = 0; hi < hpp; ++hi) {
+        for (int t0 = wg_s0; t0 < a.T; t0 += BQ) {
+            __syncthreads();
+            // Stage Q, dO rows [t0, t0+16) for every part's head.
+            {
+                const int nvalid = min(BQ, a.T - t0);
+                for (int part = 0; part < HS; ++part) {
+                    const int hh = kvh * group + part * hpp + hi;
+                    const size_t off = (size_t)b * a.T * qld + (size_t)t0 * qld + (size_t)hh * a.dim;
+                    stage_rows<DP, LW, 256>(Qs + part * BQ * LW, a.q + off, qld, BQ, nvalid, a.dim, vec4, tid);
+                    stage_rows<DP, LW, 256>(Ds + part * BQ * LW, a.dout + off, qld, BQ, nvalid, a.dim, vec4, tid);
+                }
+                if (tid < HS * BQ) {
+                    const int part = tid / BQ, r = tid % BQ, t = t0 + r;
+                    const int hh = kvh * group + part * hpp + hi;
+                    float m2 = 0.f, il = 0.f, de = 0.f;
+                    if (t < a.T) {
+                        const size_t o = ((size_t)b * a.T + t) * a.H + hh;
+                        m2 = a.row_max[o] * kLog2e;
+                        il = 1.f / a.row_den[o];
+                        de = a.row_del[o];
+                    }
+                    St[(part * BQ + r) * 4 + 0] = m2;
+                    St[(part * BQ + r) * 4 + 1] = il;
+                    St[(part * BQ + r) * 4 + 2] = de;
+                }
+            }
+            __syncthreads();
+            if (t0 + 15 < s0 || s0 >= a.T) continue;  // wave-uniform: no visible pair
+
+            f4 s = zero4(), dp = zero4();
+            {
+                const float *qrow = qs + l16 * LW + grp * DQ;
+                const float *drow = ds + l16 * LW + grp * DQ;
+#pragma unroll
+                for (int kk = 0; kk < DQ; kk += 4) {
+                    const f4 qx = *reinterpret_cast<const f4 *>(qrow + kk);
+                    const f4 dx = *reinterpret_cast<const f4 *>(drow + kk);
+                    s = mfma16(qx.x, kr[kk + 0], s);
+                    dp = mfma16(dx.x, vr[kk + 0], dp);
+                    s = mfma16(qx.y, kr[kk + 1], s);
+                    dp = mfma16(dx.y, vr[kk + 1], dp);
+                    s = mfma16(qx.z, kr[kk + 2], s);
+                    dp = mfma16(dx.z, vr[kk + 2], dp);
+                    s = mfma16(qx.w, kr[kk + 3], s);
+                    dp = mfma16(dx.w, vr[kk + 3], dp);
+                }
+            }
+            // s[r] = S[t = t0 + 4 grp + r][key = s0 + l16]
+            f4 p, dsv;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int tr = 4 * grp + r, t = t0 + tr;
+                const float m2 = st[tr * 4 + 0], il = st[tr * 4 + 1], de = st[tr * 4 + 2];
+                const bool vis = (t < a.T) && (t >= my_key);
+                const float pr = vis ? exp2f(s[r] - m2) * il : 0.f;
+                p[r] = pr;
+                dsv[r] = pr * (dp[r] - de);
+            }
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+                const float *drow = ds + (4 * grp + kk) * LW + l16;
+                const float *qrow = qs + (4 * grp + kk) * LW + l16;
+                const float pv = p[kk], dv = dsv[kk];
+#pragma unroll
+                for (int i = 0; i < NT; ++i) {
+                    dva[i] = mfma16(drow[16 * i], pv, dva[i]);
+                    dka[i] = mfma16(qrow[16 * i], dv, dka[i]);
+                }
+            }
+        }
+    }
+
+    // Sum the head-split partials in a fixed order (part 0 + 1 + ...).
+    if constexpr (HS > 1) {
+        float *red = Qs;  // reuse: (HS-1) parts x KW blocks x 64 lanes x 2*NT f4
+        __syncthreads();
+        if (hs > 0) {
+            f4 *dst = reinterpret_cast<f4 *>(red) + (((hs - 1) * KW + kbw) * 64 + lane) * 2 * NT;
+#pragma unroll
+            for (int i = 0; i < NT; ++i) { dst[i] = dka[i]; dst[NT + i] = dva[i]; }
+        }
+        __syncthreads();
+        if (hs == 0) {
+            for (int part = 1; part < HS; ++part) {
+                const f4 *src = reinterpret_cast<const f4 *>(red) + (((part - 1) * KW + kbw) * 64 + lane) * 2 * NT;
+#pragma unroll
+                for (int i = 0; i < NT; ++i) { dka[i] += src[i]; dva[i] += src[NT + i]; }
+            }
+        }
+    }
+    if (hs == 0 && key_ok) {
+        float *dkrow = a.dk + kvoff + (size_t)my_key * kld;
+        float *dvrow = a.dv + kvoff + (size_t)my_key * kld;
+#pragma unroll
+        for (int i = 0; i < NT; ++i) {
+            store4(dkrow, 16 * i + 4 * grp, a.dim, vec4, dka[i] * a.scale);
+            store4(dvrow, 16 * i + 4 * grp, a.dim, vec4, dva[i]);
+        }
+    }
+}
+
+#define ZT_BWD_DQ(DP, BK)                                                                          \
+    extern "C" __global__ void __launch_bounds__(256) zt_bwd_dq_d##DP##_k##BK(BwdArgs a) {      \
+        bwd_dq_body<DP, BK>(a);                                                                    \
+    }
+#define ZT_BWD_DKDV(DP, HS)                                                                        \
+    extern "C" __global__ void __launch_bounds__(256) zt_bwd_dkdv_d##DP##_hs##HS(BwdArgs a) {   \
+        bwd_dkdv_body<DP, HS>(a);                                                                  \
+    }
+#define ZT_BWD_ALL(DP)                                                                             \
+    ZT_BWD_DQ(DP, 32) ZT_BWD_DQ(DP, 64) ZT_BWD_DKDV(DP, 1) ZT_BWD_DKDV(DP, 2) ZT_BWD_DKDV(DP, 4)
+
+ZT_BWD_ALL(32)
+ZT_BWD_ALL(64)
+ZT_BWD_ALL(96)
+ZT_BWD_ALL(128)
+ZT_BWD_ALL(160)
+ZT_BWD_ALL(192)
+ZT_BWD_ALL(224)
+ZT_BWD_ALL(256)

@@ -1,0 +1,268 @@
+// KV-cache decode step: one new query row per sequence against its cached
+// keys, split over the key axis (gfx950).
+//
+// Computes what src/decode.zig:326-392 (attnStep) computes for each sequence
+// b: out[b, h] = softmax_s(q[b,h] . k[b,s] / sqrt(d)) v[b,s] over s < n_keys[b],
+// with the cache laid out as src/kv_cache.zig:58-63 keeps it ([n_ctx, Hkv*d]
+// per sequence).  The reference reaches this through zt_attn_forward with
+// T = 1 (src/decode.zig:462); that entry point still works here, this one is
+// the bandwidth kernel.
+//
+// Bound: HBM.  Every K/V byte is read once: a workgroup owns (sequence, kv
+// head, key chunk) and serves all G query heads of the group from one read.
+// Layout in a wave: LPR = DP/4 lanes cover one cache row with 128-bit loads,
+// so one load instruction reads RPI = 64/LPR whole rows (fully coalesced).
+// A step is NI = 8 such loads of K and of V.  Partial q.k dots are reduced
+// across the LPR lanes with a butterfly reduce-scatter (each exchange halves
+// what a lane holds), which leaves every lane with complete scores and costs
+// fewer cross-lane moves than one tree per (key, head).  p is broadcast back
+// through a small wave-private LDS table; P.V accumulates in registers.
+// Per-chunk (max, denominator, accumulator) partials go to a caller-provided
+// workspace and zt_dec_combine merges them.
+#include "common.h"
+#include "args.h"
+
+
+
+// Butterfly reduce-scatter over lane masks M, M/2, ..., 1.  On entry v[0..CNT)
+// are partial sums; on exit v[0..max(1, CNT/(2M))) are complete sums.
+template <int CNT, int M, int V0>
+struct Bfly {
+    static DEVI void run(float (&v)[V0], int lane) {
+        if constexpr (M >= 1) {
+            const bool up = (lane & M) != 0;
+            if constexpr (CNT > 1) {
+#pragma unroll
+                for (int j = 0; j < CNT / 2; ++j) {
+                    const float send = up ? v[j] : v[j + CNT / 2];
+                    const float keep = up ? v[j + CNT / 2] : v[j];
+                    v[j] = keep + __shfl_xor(send, M, 64);
+                }
+                Bfly<CNT / 2, M / 2, V0>::run(v, lane);
+            } else {
+                v[0] += __shfl_xor(v[0], M, 64);
+                Bfly<1, M / 2, V0>::run(v, lane);
+            }
+        }
+    }
+};
+
+DEVI float wave_max(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+    return v;
+}
+DEVI float wave_sum(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+    return v;
+}
+
+template <int DP, int G>
+__device__ __forceinline__ void decode_body(const DecArgs &a) {
+    constexpr int LPR = DP / 4;        // lanes per cache row
+    constexpr int RPI = 64 / LPR;      // rows per load instruction
+    constexpr int NI = 8;              // load instructions per step
+    constexpr int KS = NI * RPI;       // keys per step
+    constexpr int V0 = NI * G;         // partial dots per lane
+    constexpr int CNT = V0 >= LPR ? V0 / LPR : 1;  // complete scores per lane
+    __shared__ float Pl[4][KS * G];
+    __shared__ float Wm[4][G], Wl[4][G];
+    __shared__ f4 Wacc[4][G][LPR];
+
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int rg = lane / LPR, sub = lane % LPR;
+    const int per_seq = a.n_chunks * a.Hkv * a.n_gsub;
+    const int bl = (int)blockIdx.x / per_seq;
+    int rem = (int)blockIdx.x % per_seq;
+    const int c = rem % a.n_chunks;
+    rem /= a.n_chunks;
+    const int kvh = rem % a.Hkv, gs = rem / a.Hkv;
+    const int b = a.b_base + bl;
+    const int nk = a.n_keys[bl];
+    const int key0 = c * a.chunk;
+    if (key0 >= nk) return;  // workgroup-uniform: nothing of this sequence here
+    const int key1 = min(nk, key0 + a.chunk);
+    const int group = a.H / a.Hkv;
+    const int h0 = kvh * group + gs * G;
+    const bool vec4 = (a.dim & 3) == 0;
+    const int d0 = 4 * sub;
+    const bool dim_ok = d0 < a.dim;
+    const size_t kld = (size_t)a.Hkv * a.dim;
+    const float *kb = a.kc + (size_t)b * a.n_ctx * kld + (size_t)kvh * a.dim + d0;
+    const float *vb = a.vc + (size_t)b * a.n_ctx * kld + (size_t)kvh * a.dim + d0;
+
+    auto ld4 = [&](const float *p) -> f4 {
+        f4 x = zero4();
+        if (dim_ok) {
+            if (vec4) {
+                x = *reinterpret_cast<const f4 *>(p);
+            } else {
+                const f2 lo = *reinterpret_cast<const f2 *>(p);
+                x.x = lo.x; x.y = lo.y;
+                if (d0 + 2 < a.dim) {
+                    const f2 hi = *reinterpret_cast<const f2 *>(p + 2);
+                    x.z = hi.x; x.w = hi.y;
+                }
+            }
+        }
+        return x;
+    };
+
+    f4 qv[G];
+#pragma unroll
+    for (int gi = 0; gi < G; ++gi) {
+        qv[gi] = ld4(a.q + (size_t)b * a.H * a.dim + (size_t)(h0 + gi) * a.dim + d0);
+        qv[gi] *= a.scale_log2e;
+    }
+    f4 acc[G];
+    float m[G], ls[G];
+#pragma unroll
+    for (int gi = 0; gi < G; ++gi) { acc[gi] = zero4(); m[gi] = -INFINITY; ls[gi] = 0.f; }
+
+    const int nsteps = (key1 - key0 + KS - 1) / KS;
+    f4 kx[NI], vx[NI], kn[NI], vn[NI];
+    auto load_step = [&](int st, f4 (&kd)[NI], f4 (&vd)[NI]) {
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int key = min(key0 + st * KS + i * RPI + rg, nk - 1);  // clamp: stays in the cache
+            kd[i] = ld4(kb + (size_t)key * kld);
+            vd[i] = ld4(vb + (size_t)key * kld);
+        }
+    };
+    if (w < nsteps) load_step(w, kn, vn);
+
+    // Which (row i, head gi) each of this lane's complete scores belongs to.
+    int jidx[CNT];
+#pragma unroll
+    for (int cc = 0; cc < CNT; ++cc) jidx[cc] = (V0 >= LPR) ? sub * CNT + cc : sub / (LPR / V0);
+    const bool counted = (V0 >= LPR) || (sub % (LPR / (V0 < LPR ? V0 : LPR))) == 0;
+
+    for (int st = w; st < nsteps; st += 4) {
+#pragma unroll
+        for (int i = 0; i < NI; ++i) { kx[i] = kn[i]; vx[i] = vn[i]; }
+        if (st + 4 < nsteps) load_step(st + 4, kn, vn);
+        const int kbase = key0 + st * KS;
+
+        float part[V0];
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+#pragma unroll
+            for (int gi = 0; gi < G; ++gi) {
+                const f4 x = kx[i] * qv[gi];
+                part[i * G + gi] = (x.x + x.y) + (x.z + x.w);
+            }
+        Bfly<V0, LPR / 2, V0>::run(part, lane);
+
+        float sc[CNT];
+#pragma unroll
+        for (int cc = 0; cc < CNT; ++cc) {
+            const int j = jidx[cc];
+            const int key = kbase + (j / G) * RPI + rg;
+            sc[cc] = key < key1 ? part[cc] : -INFINITY;
+        }
+        float msafe[G], corr[G];
+#pragma unroll
+        for (int gi = 0; gi < G; ++gi) {
+            float lm = -INFINITY;
+#pragma unroll
+            for (int cc = 0; cc < CNT; ++cc)
+                if (jidx[cc] % G == gi) lm = fmaxf(lm, sc[cc]);
+            const float mnew = fmaxf(m[gi], wave_max(lm));
+            msafe[gi] = mnew == -INFINITY ? 0.f : mnew;
+            corr[gi] = exp2f(m[gi] - msafe[gi]);
+            m[gi] = mnew;
+            ls[gi] *= corr[gi];
+            acc[gi] *= corr[gi];
+        }
+        float *pl = Pl[w];
+#pragma unroll
+        for (int cc = 0; cc < CNT; ++cc) {
+            const int j = jidx[cc], gi = j % G;
+            float ms = msafe[0];
+#pragma unroll
+            for (int g2 = 1; g2 < G; ++g2) ms = (gi == g2) ? msafe[g2] : ms;
+            const float p = exp2f(sc[cc] - ms);
+            if (counted) {
+#pragma unroll
+                for (int g2 = 0; g2 < G; ++g2) ls[g2] += (gi == g2) ? p : 0.f;
+            }
+            pl[((j / G) * RPI + rg) * G + gi] = p;
+        }
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const float *pr = pl + (i * RPI + rg) * G;
+#pragma unroll
+            for (int gi = 0; gi < G; ++gi) acc[gi] += pr[gi] * vx[i];
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+
+    // Fold the row groups of this wave, then the four waves of the workgroup.
+#pragma unroll
+    for (int gi = 0; gi < G; ++gi) {
+#pragma unroll
+        for (int msk = LPR; msk < 64; msk <<= 1) {
+            acc[gi].x += __shfl_xor(acc[gi].x, msk, 64);
+            acc[gi].y += __shfl_xor(acc[gi].y, msk, 64);
+            acc[gi].z += __shfl_xor(acc[gi].z, msk, 64);
+            acc[gi].w += __shfl_xor(acc[gi].w, msk, 64);
+        }
+        const float lt = wave_sum(ls[gi]);
+        if (lane == 0) { Wm[w][gi] = m[gi]; Wl[w][gi] = lt; }
+        if (rg == 0) Wacc[w][gi][sub] = acc[gi];
+    }
+    __syncthreads();
+    for (int e = tid; e < G * LPR; e += 256) {
+        const int gi = e / LPR, sb = e % LPR;
+        float M = -INFINITY;
+        for (int ww = 0; ww < 4; ++ww) M = fmaxf(M, Wm[ww][gi]);
+        float L = 0.f;
+        f4 A = zero4();
+        for (int ww = 0; ww < 4; ++ww) {
+            const float f = Wm[ww][gi] == -INFINITY ? 0.f : exp2f(Wm[ww][gi] - M);
+            L += Wl[ww][gi] * f;
+            A += Wacc[ww][gi][sb] * f;
+        }
+        const size_t slot = ((size_t)b * a.H + (h0 + gi)) * a.n_chunks + c;
+        float *pa = a.part_acc + slot * a.dim;
+        if (4 * sb < a.dim) {
+            if (vec4) {
+                *reinterpret_cast<f4 *>(pa + 4 * sb) = A;
+            } else {
+                pa[4 * sb] = A.x; pa[4 * sb + 1] = A.y;
+                if (4 * sb + 2 < a.dim) { pa[4 * sb + 2] = A.z; pa[4 * sb + 3] = A.w; }
+            }
+        }
+        if (sb == 0) { a.part_ml[slot * 2] = M; a.part_ml[slot * 2 + 1] = L; }
+    }
+}
+
+// One workgroup per (sequence, query head): merge the chunk partials.
+extern "C" __global__ void __launch_bounds__(256) zt_dec_combine(DecArgs a) {
+    const int bl = (int)blockIdx.x / a.H, h = (int)blockIdx.x % a.H;
+    const int b = a.b_base + bl;
+    const int nch = (a.n_keys[bl] + a.chunk - 1) / a.chunk;
+    const size_t slot0 = ((size_t)b * a.H + h) * a.n_chunks;
+    float M = -INFINITY;
+    for (int c = 0; c < nch; ++c) M = fmaxf(M, a.part_ml[(slot0 + c) * 2]);
+    float L = 0.f;
+    for (int c = 0; c < nch; ++c) L += a.part_ml[(slot0 + c) * 2 + 1] * exp2f(a.part_ml[(slot0 + c) * 2] - M);
+    const float inv = 1.f / L;
+    for (int n = threadIdx.x; n < a.dim; n += blockDim.x) {
+        float o = 0.f;
+        for (int c = 0; c < nch; ++c) o += a.part_acc[(slot0 + c) * a.dim + n] * exp2f(a.part_ml[(slot0 + c) * 2] - M);
+        a.out[(size_t)b * a.H * a.dim + (size_t)h * a.dim + n] = o * inv;
+    }
+}
+
+#define ZT_DEC(DP, G)                                                                              \
+    extern "C" __global__ void __launch_bounds__(256) zt_dec_d##DP##_g##G(DecArgs a) {           \
+        decode_body<DP, G>(a);                                                                     \
+    }
+#define ZT_DEC_ALL(DP) ZT_DEC(DP, 1) ZT_DEC(DP, 2) ZT_DEC(DP, 4) ZT_DEC(DP, 8)
+ZT_DEC_ALL(32)
+ZT_DEC_ALL(64)
+ZT_DEC_ALL(128)
+ZT_DEC_ALL(256)

@@ -1,0 +1,144 @@
+// Fused causal grouped-query attention, forward, f32 on FP32 MFMA (gfx950).
+//
+// Computes what src/cuda/attn_kernels.cu:197-369 (fusedAttnForward) computes
+// -- O = softmax(Q K^T / sqrt(d), causal) V with query row t at absolute
+// position q_offset + t seeing keys s <= q_offset + t, s < n_keys -- but with
+// a different schedule:
+//   * a workgroup is 4 waves; each wave owns 16 query rows of one query head.
+//     The 4 waves are HW query heads of ONE kv group x (4 / HW) row blocks,
+//     so each K/V tile staged in LDS is read from HBM/L2 once per kv group
+//     instead of once per query (the reference re-reads the prefix per query);
+//   * Q stays in registers for the whole key loop, pre-scaled by
+//     log2(e)/sqrt(d) so the softmax runs on exp2;
+//   * S^T = K Q^T and O^T += V^T P^T on v_mfma_f32_16x16x4_f32, with P passed
+//     register to register (layout notes in common.h);
+//   * online softmax with a per-lane partial denominator that is reduced once
+//     at the end; only the running max is exchanged across lanes per tile.
+// The grid is 1-D, heaviest (latest) row tiles first, with the kv group as the
+// fastest-varying index so that consecutive workgroups -- which the dispatcher
+// spreads across the XCDs -- keep one kv group's K/V per XCD L2.
+#include "common.h"
+#include "args.h"
+
+
+template <int DP, int BK>
+__device__ __forceinline__ void attn_fwd_body(const FwdArgs &a) {
+    constexpr int LW = DP + 4;  // LDS row stride: +16 B spreads row starts over banks
+    constexpr int DQ = DP / 4;  // d values per lane group
+    constexpr int NT = DP / 16; // 16-wide column tiles of the output
+    constexpr int NJ = BK / 16; // 16-key sub-blocks per LDS tile
+    __shared__ float Ks[BK * LW];
+    __shared__ float Vs[BK * LW];
+
+    const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, grp = lane >> 4, w = tid >> 6;
+    const int RB = 4 / a.HW;
+    const int per_tile = a.n_head_blocks * a.B;
+    const int tile = a.n_row_tiles - 1 - (int)blockIdx.x / per_tile;
+    const int rem = (int)blockIdx.x % per_tile;
+    const int hb = rem % a.n_head_blocks, b = rem / a.n_head_blocks;
+    const int group = a.H / a.Hkv;
+    const int h = hb * a.HW + (w % a.HW);
+    const int kvh = h / group;
+    const int wg_row0 = tile * 16 * RB;
+    const int row0 = wg_row0 + 16 * (w / a.HW);
+    const bool vec4 = (a.dim & 3) == 0;
+    const size_t qld = (size_t)a.H * a.dim, kld = (size_t)a.Hkv * a.dim;
+    const float *qb = a.q + (size_t)b * a.T * qld + (size_t)h * a.dim;
+    const float *kb = a.k + (size_t)b * a.kv_rows * kld + (size_t)kvh * a.dim;
+    const float *vb = a.v + (size_t)b * a.kv_rows * kld + (size_t)kvh * a.dim;
+
+    const int my_row = row0 + l16;
+    float qr[DQ];
+    load_row_seg<DQ>(qr, qb + (size_t)my_row * qld, grp * DQ, a.dim, vec4, my_row < a.T, a.scale_log2e);
+
+    f4 o[NT];
+#pragma unroll
+    for (int i = 0; i < NT; ++i) o[i] = zero4();
+    float m = -INFINITY, lsum = 0.f;
+    const int qpos = a.q_offset + my_row;
+    const int kend_wg = min(a.n_keys, a.q_offset + min(a.T, wg_row0 + 16 * RB));
+    const int kend_w = row0 < a.T ? min(a.n_keys, a.q_offset + min(a.T, row0 + 16)) : 0;
+
+    for (int k0 = 0; k0 < kend_wg; k0 += BK) {
+        __syncthreads();
+        const int nvalid = min(BK, a.n_keys - k0);
+        stage_rows<DP, LW, 256>(Ks, kb + (size_t)k0 * kld, kld, BK, nvalid, a.dim, vec4, tid);
+        stage_rows<DP, LW, 256>(Vs, vb + (size_t)k0 * kld, kld, BK, nvalid, a.dim, vec4, tid);
+        __syncthreads();
+        if (k0 >= kend_w) continue;  // wave-uniform: nothing here is visible to this wave
+
+        f4 s[NJ];
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            s[j] = zero4();
+            if (k0 + 16 * j < kend_w) {
+                const float *krow = Ks + (16 * j + l16) * LW + grp * DQ;
+#pragma unroll
+                for (int kk = 0; kk < DQ; kk += 4) {
+                    const f4 kx = *reinterpret_cast<const f4 *>(krow + kk);
+                    s[j] = mfma16(kx.x, qr[kk + 0], s[j]);
+                    s[j] = mfma16(kx.y, qr[kk + 1], s[j]);
+                    s[j] = mfma16(kx.z, qr[kk + 2], s[j]);
+                    s[j] = mfma16(kx.w, qr[kk + 3], s[j]);
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int key = k0 + 16 * j + 4 * grp + r;
+                if (key > qpos || key >= a.n_keys) s[j][r] = -INFINITY;
+            }
+        }
+        float mt = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+            mt = fmaxf(mt, fmaxf(fmaxf(s[j][0], s[j][1]), fmaxf(s[j][2], s[j][3])));
+        mt = max4grp(mt);
+        const float mnew = fmaxf(m, mt);  // finite: key 0 is visible to every row
+        const float corr = exp2f(m - mnew);
+        m = mnew;
+        float ps = 0.f;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                s[j][r] = exp2f(s[j][r] - mnew);
+                ps += s[j][r];
+            }
+        lsum = lsum * corr + ps;
+#pragma unroll
+        for (int i = 0; i < NT; ++i) o[i] *= corr;
+
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            if (k0 + 16 * j >= kend_w) continue;
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+                const float pv = s[j][kk];
+                const float *vrow = Vs + (16 * j + 4 * grp + kk) * LW + l16;
+#pragma unroll
+                for (int i = 0; i < NT; ++i) o[i] = mfma16(vrow[16 * i], pv, o[i]);
+            }
+        }
+    }
+
+    const float inv = 1.f / sum4grp(lsum);
+    if (my_row < a.T) {
+        float *orow = a.out + (size_t)b * a.T * qld + (size_t)my_row * qld + (size_t)h * a.dim;
+#pragma unroll
+        for (int i = 0; i < NT; ++i) store4(orow, 16 * i + 4 * grp, a.dim, vec4, o[i] * inv);
+    }
+}
+
+#define ZT_FWD(DP, BK)                                                                             \
+    extern "C" __global__ void __launch_bounds__(256) zt_fwd_d##DP##_k##BK(FwdArgs a) {          \
+        attn_fwd_body<DP, BK>(a);                                                                  \
+    }
+
+ZT_FWD(32, 32) ZT_FWD(32, 64)
+ZT_FWD(64, 32) ZT_FWD(64, 64)
+ZT_FWD(96, 32) ZT_FWD(96, 64)
+ZT_FWD(128, 32) ZT_FWD(128, 64)
+ZT_FWD(160, 32) ZT_FWD(160, 64)
+ZT_FWD(192, 32) ZT_FWD(192, 64)
+ZT_FWD(224, 32) ZT_FWD(224, 64)
+ZT_FWD(256, 32) ZT_FWD(256, 64)

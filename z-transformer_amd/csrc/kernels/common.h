@@ -1,0 +1,106 @@
+// Device-side helpers shared by the gfx950 kernels.
+//
+// Conventions used by every attention kernel in this directory:
+//   * One wavefront is 64 lanes.  lane = threadIdx.x & 63, l16 = lane & 15,
+//     grp = lane >> 4 (0..3).
+//   * FP32 matrix-core op: v_mfma_f32_16x16x4_f32, D[16x16] += A[16x4] B[4x16].
+//       A operand: lane holds A[i = l16][k = grp]
+//       B operand: lane holds B[k = grp][j = l16]
+//       C/D:       lane holds D[i = 4*grp + r][j = l16], r = 0..3 (one float4)
+//   * A contraction over the head dimension d is split so that lane group grp
+//     owns d in [grp*DP/4, (grp+1)*DP/4); k-step kk uses d = grp*DP/4 + kk.  A
+//     sum is order-free across k-steps, so each lane then reads DP/4
+//     contiguous floats of a row (128-bit loads) instead of a strided column.
+//   * Scores are kept transposed (keys on the M axis, queries on the N axis):
+//     the C layout of S^T (lane = query column, 4 key rows per register group)
+//     is then exactly the B-operand layout the P.V product needs, with key
+//     4*grp + kk on k-step kk.  P never leaves registers.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f2 __attribute__((ext_vector_type(2)));
+
+#define DEVI __device__ __forceinline__
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+DEVI f4 mfma16(float a, float b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+DEVI int lane_id() { return threadIdx.x & 63; }
+
+DEVI float wave_xor(float v, int mask) { return __shfl_xor(v, mask, 64); }
+
+DEVI float max4grp(float v) {  // max over the four lane groups sharing l16
+    v = fmaxf(v, wave_xor(v, 16));
+    v = fmaxf(v, wave_xor(v, 32));
+    return v;
+}
+DEVI float sum4grp(float v) {
+    v += wave_xor(v, 16);
+    v += wave_xor(v, 32);
+    return v;
+}
+
+DEVI f4 zero4() { return f4{0.f, 0.f, 0.f, 0.f}; }
+
+// Loads `n` floats (n a multiple of 4) of a row starting at column c0 into
+// dst, zero for columns >= dim.  `vec4` says rows are 16-byte aligned and dim
+// is a multiple of 4; otherwise rows are only 8-byte aligned (dim even) and
+// float2 loads are used.  Wave-uniform branch.
+template <int N>
+DEVI void load_row_seg(float *dst, const float *row, int c0, int dim, bool vec4, bool valid, float mul) {
+    if (vec4) {
+#pragma unroll
+        for (int i = 0; i < N; i += 4) {
+            f4 x = zero4();
+            if (valid && c0 + i < dim) x = *reinterpret_cast<const f4 *>(row + c0 + i);
+            dst[i] = x.x * mul; dst[i + 1] = x.y * mul; dst[i + 2] = x.z * mul; dst[i + 3] = x.w * mul;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < N; i += 2) {
+            f2 x = f2{0.f, 0.f};
+            if (valid && c0 + i < dim) x = *reinterpret_cast<const f2 *>(row + c0 + i);
+            dst[i] = x.x * mul; dst[i + 1] = x.y * mul;
+        }
+    }
+}
+
+// Stores float4 `x` at row[c0..c0+3], columns >= dim dropped.
+DEVI void store4(float *row, int c0, int dim, bool vec4, f4 x) {
+    if (vec4) {
+        if (c0 < dim) *reinterpret_cast<f4 *>(row + c0) = x;
+    } else {
+        if (c0 < dim) *reinterpret_cast<f2 *>(row + c0) = f2{x.x, x.y};
+        if (c0 + 2 < dim) *reinterpret_cast<f2 *>(row + c0 + 2) = f2{x.z, x.w};
+    }
+}
+
+// Cooperative copy of `rows` rows x DP columns (global row stride `ld`
+// floats) into LDS rows of stride LDSW floats.  Rows >= nvalid and columns
+// >= dim are written as zero.  NT threads take part.
+template <int DP, int LDSW, int NT>
+DEVI void stage_rows(float *lds, const float *g, size_t ld, int rows, int nvalid, int dim, bool vec4,
+                     int tid) {
+    if (vec4) {
+        constexpr int CPR = DP / 4;  // float4 chunks per row
+        for (int e = tid; e < rows * CPR; e += NT) {
+            const int r = e / CPR, c = (e % CPR) * 4;
+            f4 x = zero4();
+            if (r < nvalid && c < dim) x = *reinterpret_cast<const f4 *>(g + (size_t)r * ld + c);
+            *reinterpret_cast<f4 *>(lds + r * LDSW + c) = x;
+        }
+    } else {
+        constexpr int CPR = DP / 2;
+        for (int e = tid; e < rows * CPR; e += NT) {
+            const int r = e / CPR, c = (e % CPR) * 2;
+            f2 x = f2{0.f, 0.f};
+            if (r < nvalid && c < dim) x = *reinterpret_cast<const f2 *>(g + (size_t)r * ld + c);
+            *reinterpret_cast<f2 *>(lds + r * LDSW + c) = x;
+        }
+    }
+}

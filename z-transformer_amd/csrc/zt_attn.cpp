@@ -1,0 +1,560 @@
+// Host side of libzt_attn.so: validation, tile choice and kernel launch.
+//
+// The gfx950 code objects (kernels/*.hip built with --genco) are embedded in
+// this library and loaded per device with hipModuleLoadData on first use;
+// kernels are launched with hipModuleLaunchKernel, each taking one argument
+// block (kernels/args.h).  There is one code path per operation and no CPU
+// fallback: without a usable device every launcher refuses.
+//
+// Validation follows the reference launchers' order and return convention
+// (src/cuda/attn_kernels.cu:833-1036): 0 = launch accepted, 1 = refused with
+// the reason on stderr.
+#include <hip/hip_runtime_api.h>
+
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <functional>
+#include <initializer_list>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+
+#include "../../include/zt_attn.h"
+#include "kernels/args.h"
+
+extern "C" {
+extern const unsigned char zt_co_fwd[], zt_co_fwd_end[];
+extern const unsigned char zt_co_bwd[], zt_co_bwd_end[];
+extern const unsigned char zt_co_dec[], zt_co_dec_end[];
+extern const unsigned char zt_co_misc[], zt_co_misc_end[];
+}
+
+namespace {
+
+constexpr int kMinDim = 32, kMaxDim = 256;
+constexpr int kMaxDevices = 64;
+constexpr int kThreads = 256;
+
+struct DeviceState {
+    std::once_flag once;
+    bool ok = false;
+    size_t lds_limit = 0;
+    hipModule_t mods[4] = {};
+    std::mutex mu;
+    std::unordered_map<std::string, hipFunction_t> fns;
+};
+DeviceState g_dev[kMaxDevices];
+
+void load_device(DeviceState &st, int dev) {
+    int lds = 0;
+    if (hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || lds <= 0)
+        return;
+    const unsigned char *images[4] = {zt_co_fwd, zt_co_bwd, zt_co_dec, zt_co_misc};
+    for (int i = 0; i < 4; ++i) {
+        if (hipModuleLoadData(&st.mods[i], images[i]) != hipSuccess) {
+            fprintf(stderr, "zt_attn: the gfx950 code object %d would not load on device %d.\n", i, dev);
+            return;
+        }
+    }
+    st.lds_limit = (size_t)lds;
+    st.ok = true;
+}
+
+// The current device's state, code objects loaded; nullptr when there is no
+// usable device (which every launcher reads as a refusal).
+DeviceState *device_state() {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    DeviceState &st = g_dev[dev];
+    std::call_once(st.once, load_device, std::ref(st), dev);
+    return st.ok ? &st : nullptr;
+}
+
+hipFunction_t get_fn(DeviceState *st, const char *name) {
+    std::lock_guard<std::mutex> lk(st->mu);
+    auto it = st->fns.find(name);
+    if (it != st->fns.end()) return it->second;
+    for (hipModule_t m : st->mods) {
+        hipFunction_t f = nullptr;
+        if (hipModuleGetFunction(&f, m, name) == hipSuccess && f) {
+            st->fns.emplace(name, f);
+            return f;
+        }
+    }
+    (void)hipGetLastError();
+    return nullptr;
+}
+
+template <class Args>
+int launch(DeviceState *st, const char *name, unsigned blocks, const Args &args, hipStream_t stream) {
+    hipFunction_t f = get_fn(st, name);
+    if (!f) {
+        fprintf(stderr, "zt_attn: FAIL kernel %s is missing from the code object.\n", name);
+        return 1;
+    }
+    Args copy = args;
+    void *params[] = {&copy};
+    const hipError_t e = hipModuleLaunchKernel(f, blocks, 1, 1, kThreads, 1, 1, 0, stream, params, nullptr);
+    if (e != hipSuccess) {
+        fprintf(stderr, "zt_attn: FAIL launch of %s: %s\n", name, hipGetErrorString(e));
+        return 1;
+    }
+    return 0;
+}
+
+// Tuning knobs for sweeps (validated; anything else falls back to the default).
+int env_choice(const char *name, int dflt, std::initializer_list<int> allowed) {
+    const char *s = getenv(name);
+    if (!s || !*s) return dflt;
+    char *end = nullptr;
+    const long v = strtol(s, &end, 10);
+    if (*end) return dflt;
+    for (int a : allowed)
+        if (v == a) return a;
+    return dflt;
+}
+
+int pad32(int dim) { return (dim + 31) / 32 * 32; }
+
+int heads_per_wg(int group) { return group % 4 == 0 ? 4 : (group % 2 == 0 ? 2 : 1); }
+
+// Forward / dq key tile for a width and a caller cap: 64 or 32 keys.
+int key_tile(int dp, int max_tile) {
+    const int preferred = env_choice("ZT_ATTN_BK", dp <= 64 ? 64 : 32, {32, 64});
+    return max_tile >= 64 ? preferred : 32;
+}
+size_t kv_tile_bytes(int dp, int bk) { return (size_t)2 * bk * (dp + 4) * sizeof(float); }
+size_t dkdv_bytes(int dp, int hs) { return ((size_t)2 * hs * 16 * (dp + 4) + (size_t)hs * 16 * 4) * sizeof(float); }
+
+int refuse_T(int T) {
+    fprintf(stderr,
+            "zt_attn: T %d is not launchable. A zero or negative query count\n"
+            "       gives a grid with no workgroups.\n",
+            T);
+    return 1;
+}
+
+int refuse_dim(int dim) {
+    fprintf(stderr, "zt_attn: head_dim %d is refused. It must be even and in [%d, %d].\n", dim, kMinDim, kMaxDim);
+    return 1;
+}
+
+int check_group(int n_heads, int n_kv_heads) {
+    if (n_heads <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads != 0) {
+        fprintf(stderr, "zt_attn: %d heads over %d kv heads is not a group.\n", n_heads, n_kv_heads);
+        return 1;
+    }
+    if (n_heads > 65535) {
+        fprintf(stderr, "zt_attn: %d heads exceeds the 65535 head limit.\n", n_heads);
+        return 1;
+    }
+    return 0;
+}
+
+int refuse_max_tile(int max_tile) {
+    fprintf(stderr, "zt_attn: max_tile %d is not launchable. A tile of zero never advances the key loop.\n",
+            max_tile);
+    return 1;
+}
+
+DeviceState *require_device() {
+    DeviceState *st = device_state();
+    if (!st) {
+        fprintf(stderr, "zt_attn: this device's LDS ceiling could not be read (no usable gfx950 device or code\n"
+                        "       object), so no tile can be sized against it. Refusing rather than guessing.\n");
+    }
+    return st;
+}
+
+bool grid_ok(unsigned long long blocks) {
+    if (blocks == 0 || blocks * kThreads > 0xFFFFFFFFull) {
+        fprintf(stderr, "zt_attn: the launch would need %llu workgroups, beyond the 2^32 work-item grid.\n", blocks);
+        return false;
+    }
+    return true;
+}
+
+int forward_impl(const float *q, const float *k, const float *v, float *out, int B, int T, int n_heads,
+                 int n_kv_heads, int dim, int group_q, int max_tile, int q_offset, int n_keys, int kv_rows,
+                 hipStream_t stream) {
+    if (T < 1) return refuse_T(T);
+    if (!zt_attn_dim_ok(dim)) return refuse_dim(dim);
+    if (check_group(n_heads, n_kv_heads)) return 1;
+    if (group_q < 1 || group_q > 64 || (size_t)dim * (size_t)group_q > 1024) {
+        fprintf(stderr, "zt_attn: group_q %d at head_dim %d is not launchable.\n", group_q, dim);
+        return 1;
+    }
+    if (q_offset < 0 || n_keys < 1 || q_offset > n_keys - T) {
+        fprintf(stderr, "zt_attn: q_offset %d, n_keys %d is not launchable.\n", q_offset, n_keys);
+        return 1;
+    }
+    if (max_tile < 1) return refuse_max_tile(max_tile);
+    if (B < 1 || kv_rows < n_keys) {
+        fprintf(stderr, "zt_attn: batch %d with %d kv rows per sequence (n_keys %d) is not launchable.\n", B,
+                kv_rows, n_keys);
+        return 1;
+    }
+    DeviceState *st = require_device();
+    if (!st) return 1;
+    const int dp = pad32(dim);
+    int bk = key_tile(dp, max_tile);
+    if (kv_tile_bytes(dp, bk) > st->lds_limit) bk = 32;
+    if (kv_tile_bytes(dp, bk) > st->lds_limit) {
+        fprintf(stderr, "zt_attn: head_dim %d needs %zu bytes of LDS per workgroup even at a 32-key tile, and\n"
+                        "       this device grants %zu. Refusing.\n",
+                dim, kv_tile_bytes(dp, bk), st->lds_limit);
+        return 1;
+    }
+    if (!q || !k || !v || !out) {
+        fprintf(stderr, "zt_attn: a null tensor pointer is not launchable.\n");
+        return 1;
+    }
+    FwdArgs a{};
+    a.q = q; a.k = k; a.v = v; a.out = out;
+    a.B = B; a.T = T; a.H = n_heads; a.Hkv = n_kv_heads; a.dim = dim;
+    a.q_offset = q_offset; a.n_keys = n_keys; a.kv_rows = kv_rows;
+    a.HW = heads_per_wg(n_heads / n_kv_heads);
+    const int rows_per_wg = 16 * (4 / a.HW);
+    a.n_row_tiles = (T + rows_per_wg - 1) / rows_per_wg;
+    a.n_head_blocks = n_heads / a.HW;
+    a.scale_log2e = (float)(1.4426950408889634 / std::sqrt((double)dim));
+    const unsigned long long blocks = (unsigned long long)a.n_row_tiles * a.n_head_blocks * B;
+    if (!grid_ok(blocks)) return 1;
+    char name[64];
+    snprintf(name, sizeof name, "zt_fwd_d%d_k%d", dp, bk);
+    return launch(st, name, (unsigned)blocks, a, stream);
+}
+
+// Validates a backward call and fills the argument block and kernel names.
+// Returns 0 when launchable; prints the refusal and returns 1 otherwise.
+int backward_prepare(const float *q, const float *k, const float *v, const float *dout, float *dq, float *dk,
+                     float *dv, float *row_max, float *row_den, float *row_del, int B, int T, int n_heads,
+                     int n_kv_heads, int dim, int max_tile, BwdArgs *a, DeviceState **st_out, char *name_dq,
+                     char *name_dkdv, unsigned *blocks_dq, unsigned *blocks_dkdv) {
+    if (T < 1) return refuse_T(T);
+    if (!zt_attn_dim_ok(dim)) return refuse_dim(dim);
+    if (check_group(n_heads, n_kv_heads)) return 1;
+    if (max_tile < 1) return refuse_max_tile(max_tile);
+    if (B < 1) {
+        fprintf(stderr, "zt_attn: batch %d is not launchable.\n", B);
+        return 1;
+    }
+    DeviceState *st = require_device();
+    if (!st) return 1;
+    const int dp = pad32(dim);
+    int bk = key_tile(dp, max_tile);
+    if (kv_tile_bytes(dp, bk) > st->lds_limit) bk = 32;
+    const int group = n_heads / n_kv_heads;
+    int hs = env_choice("ZT_ATTN_HS", heads_per_wg(group), {1, 2, 4});
+    if (group % hs != 0) hs = heads_per_wg(group);
+    while (hs > 1 && dkdv_bytes(dp, hs) > st->lds_limit) hs /= 2;
+    if (kv_tile_bytes(dp, bk) > st->lds_limit || dkdv_bytes(dp, hs) > st->lds_limit) {
+        fprintf(stderr, "zt_attn: head_dim %d needs more LDS per workgroup than this device grants (%zu).\n", dim,
+                st->lds_limit);
+        return 1;
+    }
+    if (!q || !k || !v || !dout || !row_max || !row_den || !row_del || (!dq && !dk && !dv)) {
+        fprintf(stderr, "zt_attn: a null tensor pointer is not launchable.\n");
+        return 1;
+    }
+    *a = BwdArgs{};
+    a->q = q; a->k = k; a->v = v; a->dout = dout;
+    a->dq = dq; a->dk = dk; a->dv = dv;
+    a->row_max = row_max; a->row_den = row_den; a->row_del = row_del;
+    a->B = B; a->T = T; a->H = n_heads; a->Hkv = n_kv_heads; a->dim = dim;
+    a->HW = heads_per_wg(group);
+    const int rows_per_wg = 16 * (4 / a->HW);
+    a->n_row_tiles = (T + rows_per_wg - 1) / rows_per_wg;
+    a->n_head_blocks = n_heads / a->HW;
+    a->HS = hs;
+    const int keys_per_wg = 16 * (4 / hs);
+    a->n_key_tiles = (T + keys_per_wg - 1) / keys_per_wg;
+    a->scale = (float)(1.0 / std::sqrt((double)dim));
+    a->scale_log2e = (float)(1.4426950408889634 / std::sqrt((double)dim));
+    const unsigned long long blocks_a = (unsigned long long)a->n_row_tiles * a->n_head_blocks * B;
+    const unsigned long long blocks_b = (unsigned long long)a->n_key_tiles * n_kv_heads * B;
+    if (!grid_ok(blocks_a) || !grid_ok(blocks_b)) return 1;
+    snprintf(name_dq, 64, "zt_bwd_dq_d%d_k%d", dp, bk);
+    snprintf(name_dkdv, 64, "zt_bwd_dkdv_d%d_hs%d", dp, hs);
+    *blocks_dq = (unsigned)blocks_a;
+    *blocks_dkdv = (unsigned)blocks_b;
+    *st_out = st;
+    return 0;
+}
+
+// stage: 1 = dq + row statistics, 2 = dk/dv (reads the statistics), 3 = both.
+int backward_impl(const float *q, const float *k, const float *v, const float *dout, float *dq, float *dk,
+                  float *dv, float *row_max, float *row_den, float *row_del, int B, int T, int n_heads,
+                  int n_kv_heads, int dim, int max_tile, int stage, hipStream_t stream) {
+    BwdArgs a;
+    DeviceState *st = nullptr;
+    char name_a[64], name_b[64];
+    unsigned blocks_a = 0, blocks_b = 0;
+    if (backward_prepare(q, k, v, dout, dq, dk, dv, row_max, row_den, row_del, B, T, n_heads, n_kv_heads, dim,
+                         max_tile, &a, &st, name_a, name_b, &blocks_a, &blocks_b))
+        return 1;
+    if ((stage & 1) && !dq) {
+        fprintf(stderr, "zt_attn: a null dq is not launchable.\n");
+        return 1;
+    }
+    if ((stage & 2) && (!dk || !dv)) {
+        fprintf(stderr, "zt_attn: a null dk or dv is not launchable.\n");
+        return 1;
+    }
+    if ((stage & 1) && launch(st, name_a, blocks_a, a, stream)) return 1;
+    // Same stream: the dk/dv kernel reads the row statistics the first wrote.
+    if ((stage & 2) && launch(st, name_b, blocks_b, a, stream)) return 1;
+    return 0;
+}
+
+// Decode geometry: head sub-group G, padded width, keys per step and chunk.
+struct DecGeom {
+    int G, n_gsub, dp, ks, chunk, n_chunks;
+};
+
+DecGeom decode_geom(int B, int n_ctx, int n_heads, int n_kv_heads, int dim) {
+    DecGeom g{};
+    const int group = n_heads / n_kv_heads;
+    g.G = group % 8 == 0 ? 8 : group % 4 == 0 ? 4 : group % 2 == 0 ? 2 : 1;
+    g.n_gsub = group / g.G;
+    g.dp = dim <= 32 ? 32 : dim <= 64 ? 64 : dim <= 128 ? 128 : 256;
+    g.ks = 8 * (64 / (g.dp / 4));
+    const long long pairs = (long long)B * n_kv_heads * g.n_gsub;
+    const long long target = env_choice("ZT_DEC_WGS", 4096, {1024, 2048, 4096, 8192, 16384, 32768});
+    long long per_seq = (target + pairs - 1) / pairs;
+    if (per_seq < 1) per_seq = 1;
+    long long chunk = (n_ctx + per_seq - 1) / per_seq;
+    const long long gran = 4LL * g.ks;  // every wave gets at least one step
+    chunk = (chunk + gran - 1) / gran * gran;
+    if (chunk < gran) chunk = gran;
+    g.chunk = (int)chunk;
+    g.n_chunks = (int)((n_ctx + chunk - 1) / chunk);
+    return g;
+}
+
+}  // namespace
+
+extern "C" {
+
+int zt_attn_dim_ok(int dim) { return !(dim < kMinDim || dim > kMaxDim || (dim & 1) != 0); }
+
+size_t zt_attn_forward_shmem(int dim, int tile, int group_q) {
+    (void)group_q;
+    if (!zt_attn_dim_ok(dim)) return 0;
+    const int dp = pad32(dim);
+    return kv_tile_bytes(dp, key_tile(dp, tile));
+}
+
+size_t zt_attn_bwd_dq_shmem(int dim, int tile) {
+    if (!zt_attn_dim_ok(dim)) return 0;
+    const int dp = pad32(dim);
+    return kv_tile_bytes(dp, key_tile(dp, tile));
+}
+
+size_t zt_attn_bwd_dkdv_shmem(int dim) {
+    if (!zt_attn_dim_ok(dim)) return 0;
+    return dkdv_bytes(pad32(dim), 4);
+}
+
+int zt_attn_forward(const float *q, const float *k, const float *v, float *out, int T, int n_heads,
+                    int n_kv_heads, int dim, int group_q, int max_tile, int q_offset, int n_keys,
+                    hipStream_t stream) {
+    return forward_impl(q, k, v, out, 1, T, n_heads, n_kv_heads, dim, group_q, max_tile, q_offset, n_keys,
+                        n_keys, stream);
+}
+
+int zt_attn_forward_batched(const float *q, const float *k, const float *v, float *out, int B, int T,
+                            int n_heads, int n_kv_heads, int dim, int group_q, int max_tile, int q_offset,
+                            int n_keys, int kv_rows, hipStream_t stream) {
+    return forward_impl(q, k, v, out, B, T, n_heads, n_kv_heads, dim, group_q, max_tile, q_offset, n_keys,
+                        kv_rows, stream);
+}
+
+int zt_attn_backward(const float *q, const float *k, const float *v, const float *dout, float *dq, float *dk,
+                     float *dv, float *row_max, float *row_den, float *row_del, int T, int n_heads,
+                     int n_kv_heads, int dim, int max_tile, hipStream_t stream) {
+    return backward_impl(q, k, v, dout, dq, dk, dv, row_max, row_den, row_del, 1, T, n_heads, n_kv_heads, dim,
+                         max_tile, 3, stream);
+}
+
+int zt_attn_backward_batched(const float *q, const float *k, const float *v, const float *dout, float *dq,
+                             float *dk, float *dv, float *row_max, float *row_den, float *row_del, int B, int T,
+                             int n_heads, int n_kv_heads, int dim, int max_tile, hipStream_t stream) {
+    return backward_impl(q, k, v, dout, dq, dk, dv, row_max, row_den, row_del, B, T, n_heads, n_kv_heads, dim,
+                         max_tile, 3, stream);
+}
+
+int zt_attn_bwd_dq(const float *q, const float *k, const float *v, const float *dout, float *dq, float *row_max,
+                   float *row_den, float *row_del, int B, int T, int n_heads, int n_kv_heads, int dim, int max_tile,
+                   hipStream_t stream) {
+    return backward_impl(q, k, v, dout, dq, nullptr, nullptr, row_max, row_den, row_del, B, T, n_heads, n_kv_heads,
+                         dim, max_tile, 1, stream);
+}
+
+int zt_attn_bwd_dkdv(const float *q, const float *k, const float *v, const float *dout, float *dk, float *dv,
+                     const float *row_max, const float *row_den, const float *row_del, int B, int T, int n_heads,
+                     int n_kv_heads, int dim, hipStream_t stream) {
+    return backward_impl(q, k, v, dout, nullptr, dk, dv, const_cast<float *>(row_max), const_cast<float *>(row_den),
+                         const_cast<float *>(row_del), B, T, n_heads, n_kv_heads, dim, 64, 2, stream);
+}
+
+size_t zt_attn_decode_workspace(int B, int n_ctx, int n_heads, int n_kv_heads, int dim) {
+    if (B < 1 || n_ctx < 1 || !zt_attn_dim_ok(dim) || n_heads <= 0 || n_kv_heads <= 0 ||
+        n_heads % n_kv_heads != 0)
+        return 0;
+    const DecGeom g = decode_geom(B, n_ctx, n_heads, n_kv_heads, dim);
+    return (size_t)B * n_heads * g.n_chunks * ((size_t)dim + 2) * sizeof(float);
+}
+
+int zt_attn_decode(const float *q, const float *k_cache, const float *v_cache, float *out, const int *n_keys,
+                   int B, int n_ctx, int n_heads, int n_kv_heads, int dim, void *workspace,
+                   size_t workspace_bytes, hipStream_t stream) {
+    if (B < 1 || n_ctx < 1) {
+        fprintf(stderr, "zt_attn: decode over %d sequences of %d cached rows is not launchable.\n", B, n_ctx);
+        return 1;
+    }
+    if (!zt_attn_dim_ok(dim)) return refuse_dim(dim);
+    if (check_group(n_heads, n_kv_heads)) return 1;
+    if (!n_keys) {
+        fprintf(stderr, "zt_attn: decode needs the host n_keys array.\n");
+        return 1;
+    }
+    for (int b = 0; b < B; ++b) {
+        if (n_keys[b] < 1 || n_keys[b] > n_ctx) {
+            fprintf(stderr, "zt_attn: sequence %d has n_keys %d, outside [1, %d].\n", b, n_keys[b], n_ctx);
+            return 1;
+        }
+    }
+    const size_t need = zt_attn_decode_workspace(B, n_ctx, n_heads, n_kv_heads, dim);
+    if (!workspace || workspace_bytes < need) {
+        fprintf(stderr, "zt_attn: decode workspace of %zu bytes is short of the %zu needed.\n", workspace_bytes,
+                need);
+        return 1;
+    }
+    if (!q || !k_cache || !v_cache || !out) {
+        fprintf(stderr, "zt_attn: a null tensor pointer is not launchable.\n");
+        return 1;
+    }
+    DeviceState *st = require_device();
+    if (!st) return 1;
+    const DecGeom g = decode_geom(B, n_ctx, n_heads, n_kv_heads, dim);
+    DecArgs a{};
+    a.q = q; a.kc = k_cache; a.vc = v_cache; a.out = out;
+    a.part_acc = static_cast<float *>(workspace);
+    a.part_ml = a.part_acc + (size_t)B * n_heads * g.n_chunks * dim;
+    a.n_ctx = n_ctx; a.H = n_heads; a.Hkv = n_kv_heads; a.dim = dim;
+    a.chunk = g.chunk; a.n_chunks = g.n_chunks; a.n_gsub = g.n_gsub;
+    a.scale_log2e = (float)(1.4426950408889634 / std::sqrt((double)dim));
+    char name[64];
+    snprintf(name, sizeof name, "zt_dec_d%d_g%d", g.dp, g.G);
+    for (int b0 = 0; b0 < B; b0 += ZT_DEC_MAXB) {
+        a.b_base = b0;
+        a.nb = B - b0 < ZT_DEC_MAXB ? B - b0 : ZT_DEC_MAXB;
+        for (int i = 0; i < a.nb; ++i) a.n_keys[i] = n_keys[b0 + i];
+        const unsigned long long blocks = (unsigned long long)a.nb * g.n_chunks * n_kv_heads * g.n_gsub;
+        if (!grid_ok(blocks)) return 1;
+        if (launch(st, name, (unsigned)blocks, a, stream)) return 1;
+        if (launch(st, "zt_dec_combine", (unsigned)(a.nb * n_heads), a, stream)) return 1;
+    }
+    return 0;
+}
+
+int zt_rmsnorm_forward(const float *x, const float *w, float *y, int rows, int cols, double eps,
+                       hipStream_t stream) {
+    if (rows < 0 || cols < 1 || !(eps >= 0.0)) {
+        fprintf(stderr, "zt_rmsnorm: %d rows of %d columns with eps %g is not launchable.\n", rows, cols, eps);
+        return 1;
+    }
+    if (rows == 0) return 0;
+    if (!x || !w || !y) {
+        fprintf(stderr, "zt_rmsnorm: a null tensor pointer is not launchable.\n");
+        return 1;
+    }
+    DeviceState *st = device_state();
+    if (!st) {
+        fprintf(stderr, "zt_rmsnorm: no usable gfx950 device or code object.\n");
+        return 1;
+    }
+    if (!grid_ok((unsigned long long)rows)) return 1;
+    NormArgs a{x, w, y, rows, cols, eps};
+    const bool aligned = ((uintptr_t)x % 16 == 0) && ((uintptr_t)w % 16 == 0) && ((uintptr_t)y % 16 == 0);
+    const int n4 = cols / 4;
+    const char *name = "zt_rmsnorm_any";
+    if (cols % 4 == 0 && aligned) {
+        if (n4 <= 256) name = "zt_rmsnorm_v1";
+        else if (n4 <= 512) name = "zt_rmsnorm_v2";
+        else if (n4 <= 1024) name = "zt_rmsnorm_v4";
+        else if (n4 <= 2048) name = "zt_rmsnorm_v8";
+        else if (n4 <= 4096) name = "zt_rmsnorm_v16";
+    }
+    return launch(st, name, (unsigned)rows, a, stream);
+}
+
+int zt_rope_forward(const float *x, float *y, int rows, int cols, int pos, double theta, int head_dim,
+                    hipStream_t stream) {
+    if (head_dim <= 0 || head_dim % 2 != 0) {
+        fprintf(stderr, "zt_rope: head_dim %d is odd or not positive.\n", head_dim);
+        return 1;
+    }
+    if (rows < 0 || cols < 0 || cols % head_dim != 0 || pos < 0) {
+        fprintf(stderr, "zt_rope: %d rows of %d columns is not a whole number of %d-wide heads.\n", rows, cols,
+                head_dim);
+        return 1;
+    }
+    const long long work = (long long)rows * (cols / 2);
+    if (work == 0) return 0;
+    if (!x || !y) {
+        fprintf(stderr, "zt_rope: a null tensor pointer is not launchable.\n");
+        return 1;
+    }
+    DeviceState *st = device_state();
+    if (!st) {
+        fprintf(stderr, "zt_rope: no usable gfx950 device or code object.\n");
+        return 1;
+    }
+    RopeArgs a{x, y, rows, cols, pos, head_dim, theta};
+    long long blocks = (work + kThreads - 1) / kThreads;
+    if (blocks > 65536) blocks = 65536;
+    return launch(st, "zt_rope", (unsigned)blocks, a, stream);
+}
+
+static int fill_impl(const char *name, float *dst, size_t n, uint64_t seed, double p0, double p1,
+                     hipStream_t stream) {
+    if (n == 0) return 0;
+    if (!dst) {
+        fprintf(stderr, "zt_fill: a null pointer is not fillable.\n");
+        return 1;
+    }
+    DeviceState *st = device_state();
+    if (!st) {
+        fprintf(stderr, "zt_fill: no usable gfx950 device or code object.\n");
+        return 1;
+    }
+    FillArgs a{dst, (unsigned long long)n, (unsigned long long)seed, p0, p1};
+    unsigned long long blocks = (n + kThreads - 1) / kThreads;
+    if (blocks > 65536) blocks = 65536;
+    return launch(st, name, (unsigned)blocks, a, stream);
+}
+
+int zt_fill_normal(float *dst, size_t n, uint64_t seed, double mean, double sigma, hipStream_t stream) {
+    return fill_impl("zt_fill_normal", dst, n, seed, mean, sigma, stream);
+}
+
+int zt_fill_uniform(float *dst, size_t n, uint64_t seed, double lo, double hi, hipStream_t stream) {
+    return fill_impl("zt_fill_uniform", dst, n, seed, lo, hi, stream);
+}
+
+const char *zt_attn_version(void) { return "zt_attn gfx950 0.1"; }
+
+size_t zt_attn_lds_limit(void) {
+    DeviceState *st = device_state();
+    return st ? st->lds_limit : 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,197 @@
+// The reference's device.Attn holder (src/cuda/device.zig:119-501) restated in
+// C++ over the zt_attn C ABI.  Same checks in the same order, same five errors.
+// One deliberate difference: a failed hipMemcpy is DeviceTransferFailed, the
+// error device.zig:134-140 documents for it (its upload/download at :418,:430
+// return DeviceAllocFailed instead).
+#include <hip/hip_runtime_api.h>
+
+#include <climits>
+#include <cstdint>
+#include <new>
+
+#include "../../include/zt_attn.h"
+#include "../../include/zt_holder.h"
+
+namespace zt {
+
+static bool mul_ok(size_t a, size_t b, size_t *out) {
+    if (a != 0 && b > SIZE_MAX / a) return false;
+    *out = a * b;
+    return true;
+}
+
+int bytes_for(int kind, size_t t, size_t n_heads, size_t n_kv_heads, size_t dim, size_t *out) {
+    if (t == 0 || dim == 0 || n_heads == 0 || n_kv_heads == 0) return ZT_DEGENERATE_SHAPE;
+    size_t cols = 0;
+    switch (kind) {
+    case ZT_QUERY_HEADED:
+        if (!mul_ok(n_heads, dim, &cols)) return ZT_SHAPE_TOO_LARGE;
+        break;
+    case ZT_KV_HEADED:
+        if (!mul_ok(n_kv_heads, dim, &cols)) return ZT_SHAPE_TOO_LARGE;
+        break;
+    case ZT_PER_ROW:
+        cols = n_heads;
+        break;
+    default:
+        return ZT_CONFIG_REFUSED;
+    }
+    size_t elems = 0;
+    if (!mul_ok(t, cols, &elems)) return ZT_SHAPE_TOO_LARGE;
+    if (!mul_ok(elems, sizeof(float), out)) return ZT_SHAPE_TOO_LARGE;
+    return ZT_OK;
+}
+
+int to_cint(size_t x, int *out) {
+    if (x > (size_t)INT_MAX) return ZT_SHAPE_TOO_LARGE;
+    *out = (int)x;
+    return ZT_OK;
+}
+
+int forward_bounds(int c_t, int q_offset, int n_keys, int t) {
+    if (n_keys < 1 || n_keys > c_t) return ZT_SHAPE_TOO_LARGE;
+    if (t < 1 || t > c_t) return ZT_SHAPE_TOO_LARGE;
+    if (q_offset < 0 || q_offset > c_t || t > c_t - q_offset) return ZT_SHAPE_TOO_LARGE;
+    if (q_offset + t > n_keys) return ZT_SHAPE_TOO_LARGE;
+    return ZT_OK;
+}
+
+struct Attn {
+    float *buf[ZT_N_BUFFERS] = {};
+    size_t t = 0, n_heads = 0, n_kv_heads = 0, dim = 0;
+    int c_t = 0, c_heads = 0, c_kv_heads = 0, c_dim = 0;
+
+    size_t buffer_bytes(int which) const {
+        size_t n = 0;
+        const int kind = (which == ZT_BUF_Q || which == ZT_BUF_OUT || which == ZT_BUF_DOUT || which == ZT_BUF_DQ)
+                             ? ZT_QUERY_HEADED
+                             : (which >= ZT_BUF_ROW_MAX ? ZT_PER_ROW : ZT_KV_HEADED);
+        if (bytes_for(kind, t, n_heads, n_kv_heads, dim, &n) != ZT_OK) return 0;
+        return n;
+    }
+    void free_taken(int taken) {
+        for (int i = 0; i < taken; ++i) {
+            if (buf[i]) (void)hipFree(buf[i]);
+            buf[i] = nullptr;
+        }
+    }
+};
+
+}  // namespace zt
+
+struct zt_holder {
+    zt::Attn a;
+};
+
+extern "C" {
+
+int zt_bytes_for(int kind, size_t t, size_t n_heads, size_t n_kv_heads, size_t dim, size_t *out) {
+    return zt::bytes_for(kind, t, n_heads, n_kv_heads, dim, out);
+}
+
+int zt_to_cint(size_t x, int *out) { return zt::to_cint(x, out); }
+
+int zt_forward_bounds(int c_t, int q_offset, int n_keys, int t) {
+    return zt::forward_bounds(c_t, q_offset, n_keys, t);
+}
+
+int zt_holder_init(size_t t, size_t n_heads, size_t n_kv_heads, size_t dim, zt_holder **out) {
+    if (!out) return ZT_CONFIG_REFUSED;
+    *out = nullptr;
+    int c_t, c_heads, c_kv, c_dim, e;
+    if ((e = zt::to_cint(t, &c_t)) || (e = zt::to_cint(n_heads, &c_heads)) || (e = zt::to_cint(n_kv_heads, &c_kv)) ||
+        (e = zt::to_cint(dim, &c_dim)))
+        return e;
+    if (zt_attn_dim_ok(c_dim) == 0) return ZT_CONFIG_REFUSED;
+    if (c_heads <= 0 || c_kv <= 0 || c_heads % c_kv != 0) return ZT_CONFIG_REFUSED;
+    if (n_heads > 65535) return ZT_CONFIG_REFUSED;
+    size_t qh, kvh, pr;
+    if ((e = zt::bytes_for(ZT_QUERY_HEADED, t, n_heads, n_kv_heads, dim, &qh)) ||
+        (e = zt::bytes_for(ZT_KV_HEADED, t, n_heads, n_kv_heads, dim, &kvh)) ||
+        (e = zt::bytes_for(ZT_PER_ROW, t, n_heads, n_kv_heads, dim, &pr)))
+        return e;
+    zt_holder *h = new (std::nothrow) zt_holder;
+    if (!h) return ZT_DEVICE_ALLOC_FAILED;
+    const size_t sizes[ZT_N_BUFFERS] = {qh, kvh, kvh, qh, qh, qh, kvh, kvh, pr, pr, pr};
+    for (int i = 0; i < ZT_N_BUFFERS; ++i) {
+        void *p = nullptr;
+        if (hipMalloc(&p, sizes[i]) != hipSuccess || !p) {
+            (void)hipGetLastError();
+            h->a.free_taken(i);
+            delete h;
+            return ZT_DEVICE_ALLOC_FAILED;
+        }
+        h->a.buf[i] = static_cast<float *>(p);
+    }
+    h->a.t = t; h->a.n_heads = n_heads; h->a.n_kv_heads = n_kv_heads; h->a.dim = dim;
+    h->a.c_t = c_t; h->a.c_heads = c_heads; h->a.c_kv_heads = c_kv; h->a.c_dim = c_dim;
+    *out = h;
+    return ZT_OK;
+}
+
+void zt_holder_deinit(zt_holder *h) {
+    if (!h) return;
+    h->a.free_taken(ZT_N_BUFFERS);
+    delete h;
+}
+
+size_t zt_holder_total_bytes(const zt_holder *h) {
+    size_t qh = 0, kvh = 0, pr = 0;
+    if (zt::bytes_for(ZT_QUERY_HEADED, h->a.t, h->a.n_heads, h->a.n_kv_heads, h->a.dim, &qh) ||
+        zt::bytes_for(ZT_KV_HEADED, h->a.t, h->a.n_heads, h->a.n_kv_heads, h->a.dim, &kvh) ||
+        zt::bytes_for(ZT_PER_ROW, h->a.t, h->a.n_heads, h->a.n_kv_heads, h->a.dim, &pr))
+        return 0;
+    return 4 * qh + 4 * kvh + 3 * pr;
+}
+
+float *zt_holder_buffer(const zt_holder *h, int which) {
+    if (!h || which < 0 || which >= ZT_N_BUFFERS) return nullptr;
+    return h->a.buf[which];
+}
+
+int zt_holder_forward_at(const zt_holder *h, int group_q, int max_tile, int q_offset, int n_keys, int t) {
+    const zt::Attn &a = h->a;
+    if (int e = zt::forward_bounds(a.c_t, q_offset, n_keys, t)) return e;
+    const int rc = zt_attn_forward(a.buf[ZT_BUF_Q], a.buf[ZT_BUF_K], a.buf[ZT_BUF_V], a.buf[ZT_BUF_OUT], t, a.c_heads,
+                                   a.c_kv_heads, a.c_dim, group_q, max_tile, q_offset, n_keys, nullptr);
+    return rc != 0 ? ZT_CONFIG_REFUSED : ZT_OK;
+}
+
+int zt_holder_forward(const zt_holder *h, int group_q, int max_tile) {
+    return zt_holder_forward_at(h, group_q, max_tile, 0, h->a.c_t, h->a.c_t);
+}
+
+int zt_holder_backward(const zt_holder *h, int max_tile) {
+    const zt::Attn &a = h->a;
+    const int rc = zt_attn_backward(a.buf[ZT_BUF_Q], a.buf[ZT_BUF_K], a.buf[ZT_BUF_V], a.buf[ZT_BUF_DOUT],
+                                    a.buf[ZT_BUF_DQ], a.buf[ZT_BUF_DK], a.buf[ZT_BUF_DV], a.buf[ZT_BUF_ROW_MAX],
+                                    a.buf[ZT_BUF_ROW_DEN], a.buf[ZT_BUF_ROW_DEL], a.c_t, a.c_heads, a.c_kv_heads,
+                                    a.c_dim, max_tile, nullptr);
+    return rc != 0 ? ZT_CONFIG_REFUSED : ZT_OK;
+}
+
+int zt_holder_upload(const zt_holder *h, int which, const float *src, size_t n_floats) {
+    if (!h || which < 0 || which >= ZT_N_BUFFERS) return ZT_CONFIG_REFUSED;
+    size_t n = 0;
+    if (!zt::mul_ok(n_floats, sizeof(float), &n)) return ZT_SHAPE_TOO_LARGE;
+    if (n > h->a.buffer_bytes(which)) return ZT_SHAPE_TOO_LARGE;
+    if (hipMemcpy(h->a.buf[which], src, n, hipMemcpyHostToDevice) != hipSuccess) {
+        (void)hipGetLastError();
+        return ZT_DEVICE_TRANSFER_FAILED;
+    }
+    return ZT_OK;
+}
+
+int zt_holder_download(const zt_holder *h, float *dst, int which, size_t n_floats) {
+    if (!h || which < 0 || which >= ZT_N_BUFFERS) return ZT_CONFIG_REFUSED;
+    size_t n = 0;
+    if (!zt::mul_ok(n_floats, sizeof(float), &n)) return ZT_SHAPE_TOO_LARGE;
+    if (n > h->a.buffer_bytes(which)) return ZT_SHAPE_TOO_LARGE;
+    if (hipMemcpy(dst, h->a.buf[which], n, hipMemcpyDeviceToHost) != hipSuccess) {
+        (void)hipGetLastError();
+        return ZT_DEVICE_TRANSFER_FAILED;
+    }
+    return ZT_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,187 @@
+"""ctypes binding of libzt_attn.so (include/zt_attn.h, include/zt_holder.h).
+
+Plumbing for tests and the benchmark: device memory and streams come from
+torch tensors, every computation runs in the HIP library.  There is no
+fallback: `lib()` raises when the library has not been built, and every
+wrapper raises `ZtRefused` when the C side returns non-zero.
+"""
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "_build", "libzt_attn.so")
+
+_lib = None
+
+# The reference C ABI's six symbols, then the extensions (include/zt_attn.h),
+# then the holder's C face (include/zt_holder.h).
+ABI_SYMBOLS = [
+    "zt_attn_dim_ok", "zt_attn_forward_shmem", "zt_attn_bwd_dq_shmem", "zt_attn_bwd_dkdv_shmem",
+    "zt_attn_forward", "zt_attn_backward",
+    "zt_attn_forward_batched", "zt_attn_backward_batched", "zt_attn_bwd_dq", "zt_attn_bwd_dkdv",
+    "zt_attn_decode_workspace", "zt_attn_decode",
+    "zt_rmsnorm_forward", "zt_rope_forward", "zt_fill_normal", "zt_fill_uniform", "zt_attn_version",
+    "zt_attn_lds_limit",
+]
+HOLDER_SYMBOLS = [
+    "zt_bytes_for", "zt_to_cint", "zt_forward_bounds", "zt_holder_init", "zt_holder_deinit",
+    "zt_holder_total_bytes", "zt_holder_buffer", "zt_holder_forward", "zt_holder_forward_at",
+    "zt_holder_backward", "zt_holder_upload", "zt_holder_download",
+]
+
+# include/zt_holder.h enum zt_error
+ZT_OK, ZT_DEGENERATE_SHAPE, ZT_SHAPE_TOO_LARGE, ZT_CONFIG_REFUSED, ZT_DEVICE_ALLOC_FAILED, \
+    ZT_DEVICE_TRANSFER_FAILED = range(6)
+ZT_QUERY_HEADED, ZT_KV_HEADED, ZT_PER_ROW = range(3)
+(ZT_BUF_Q, ZT_BUF_K, ZT_BUF_V, ZT_BUF_OUT, ZT_BUF_DOUT, ZT_BUF_DQ, ZT_BUF_DK, ZT_BUF_DV, ZT_BUF_ROW_MAX,
+ ZT_BUF_ROW_DEN, ZT_BUF_ROW_DEL) = range(11)
+
+
+class ZtRefused(RuntimeError):
+    """The C side refused a call (it printed the reason on stderr)."""
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise FileNotFoundError(
+                f"{LIB_PATH} is not built; run `python z-transformer_amd/build.py` (or __graft_entry__.build())")
+        L = ctypes.CDLL(LIB_PATH)
+        P, I, Z, D, U64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t, ctypes.c_double, ctypes.c_uint64
+        sig = {
+            "zt_attn_dim_ok": (I, [I]),
+            "zt_attn_forward_shmem": (Z, [I, I, I]),
+            "zt_attn_bwd_dq_shmem": (Z, [I, I]),
+            "zt_attn_bwd_dkdv_shmem": (Z, [I]),
+            "zt_attn_forward": (I, [P, P, P, P, I, I, I, I, I, I, I, I, P]),
+            "zt_attn_backward": (I, [P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, P]),
+            "zt_attn_forward_batched": (I, [P, P, P, P, I, I, I, I, I, I, I, I, I, I, P]),
+            "zt_attn_backward_batched": (I, [P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, P]),
+            "zt_attn_bwd_dq": (I, [P] * 8 + [I] * 6 + [P]),
+            "zt_attn_bwd_dkdv": (I, [P] * 9 + [I] * 5 + [P]),
+            "zt_attn_decode_workspace": (Z, [I, I, I, I, I]),
+            "zt_attn_decode": (I, [P, P, P, P, P, I, I, I, I, I, P, Z, P]),
+            "zt_rmsnorm_forward": (I, [P, P, P, I, I, D, P]),
+            "zt_rope_forward": (I, [P, P, I, I, I, D, I, P]),
+            "zt_fill_normal": (I, [P, Z, U64, D, D, P]),
+            "zt_fill_uniform": (I, [P, Z, U64, D, D, P]),
+            "zt_attn_version": (ctypes.c_char_p, []),
+            "zt_attn_lds_limit": (Z, []),
+            "zt_bytes_for": (I, [I, Z, Z, Z, Z, ctypes.POINTER(Z)]),
+            "zt_to_cint": (I, [Z, ctypes.POINTER(I)]),
+            "zt_forward_bounds": (I, [I, I, I, I]),
+            "zt_holder_init": (I, [Z, Z, Z, Z, ctypes.POINTER(P)]),
+            "zt_holder_deinit": (None, [P]),
+            "zt_holder_total_bytes": (Z, [P]),
+            "zt_holder_buffer": (P, [P, I]),
+            "zt_holder_forward": (I, [P, I, I]),
+            "zt_holder_forward_at": (I, [P, I, I, I, I, I]),
+            "zt_holder_backward": (I, [P, I]),
+            "zt_holder_upload": (I, [P, I, P, Z]),
+            "zt_holder_download": (I, [P, P, I, Z]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(stream):
+    if stream is None:
+        import torch
+        stream = torch.cuda.current_stream()
+    return ctypes.c_void_p(stream.cuda_stream)
+
+
+def _check(rc, what):
+    if rc != 0:
+        raise ZtRefused(f"{what} refused (rc={rc})")
+
+
+def _f32_cuda(*ts):
+    import torch
+    for t in ts:
+        if t.dtype != torch.float32 or not t.is_cuda or not t.is_contiguous():
+            raise ValueError("tensors must be contiguous float32 on the GPU")
+
+
+def forward(q, k, v, out, T, n_heads, n_kv_heads, dim, group_q=1, max_tile=64, q_offset=0, n_keys=None,
+            B=1, kv_rows=None, stream=None):
+    """zt_attn_forward (B == 1, kv_rows == n_keys) or zt_attn_forward_batched."""
+    _f32_cuda(q, k, v, out)
+    n_keys = T if n_keys is None else n_keys
+    if B == 1 and (kv_rows is None or kv_rows == n_keys):
+        rc = lib().zt_attn_forward(_ptr(q), _ptr(k), _ptr(v), _ptr(out), T, n_heads, n_kv_heads, dim, group_q,
+                                   max_tile, q_offset, n_keys, _stream(stream))
+    else:
+        kv_rows = n_keys if kv_rows is None else kv_rows
+        rc = lib().zt_attn_forward_batched(_ptr(q), _ptr(k), _ptr(v), _ptr(out), B, T, n_heads, n_kv_heads, dim,
+                                           group_q, max_tile, q_offset, n_keys, kv_rows, _stream(stream))
+    _check(rc, "zt_attn_forward")
+
+
+def backward(q, k, v, dout, dq, dk, dv, row_max, row_den, row_del, T, n_heads, n_kv_heads, dim, max_tile=64, B=1,
+             stream=None):
+    _f32_cuda(q, k, v, dout, dq, dk, dv, row_max, row_den, row_del)
+    if B == 1:
+        rc = lib().zt_attn_backward(*map(_ptr, (q, k, v, dout, dq, dk, dv, row_max, row_den, row_del)), T, n_heads,
+                                    n_kv_heads, dim, max_tile, _stream(stream))
+    else:
+        rc = lib().zt_attn_backward_batched(*map(_ptr, (q, k, v, dout, dq, dk, dv, row_max, row_den, row_del)), B,
+                                            T, n_heads, n_kv_heads, dim, max_tile, _stream(stream))
+    _check(rc, "zt_attn_backward")
+
+
+def bwd_dq(q, k, v, dout, dq, row_max, row_den, row_del, T, n_heads, n_kv_heads, dim, max_tile=64, B=1,
+           stream=None):
+    _f32_cuda(q, k, v, dout, dq, row_max, row_den, row_del)
+    _check(lib().zt_attn_bwd_dq(*map(_ptr, (q, k, v, dout, dq, row_max, row_den, row_del)), B, T, n_heads,
+                                n_kv_heads, dim, max_tile, _stream(stream)), "zt_attn_bwd_dq")
+
+
+def bwd_dkdv(q, k, v, dout, dk, dv, row_max, row_den, row_del, T, n_heads, n_kv_heads, dim, B=1, stream=None):
+    _f32_cuda(q, k, v, dout, dk, dv, row_max, row_den, row_del)
+    _check(lib().zt_attn_bwd_dkdv(*map(_ptr, (q, k, v, dout, dk, dv, row_max, row_den, row_del)), B, T, n_heads,
+                                  n_kv_heads, dim, _stream(stream)), "zt_attn_bwd_dkdv")
+
+
+def decode_workspace_bytes(B, n_ctx, n_heads, n_kv_heads, dim):
+    return lib().zt_attn_decode_workspace(B, n_ctx, n_heads, n_kv_heads, dim)
+
+
+def decode(q, k_cache, v_cache, out, n_keys, B, n_ctx, n_heads, n_kv_heads, dim, workspace, stream=None):
+    """n_keys: a sequence of B ints (host)."""
+    _f32_cuda(q, k_cache, v_cache, out)
+    arr = (ctypes.c_int * B)(*[int(x) for x in n_keys])
+    nbytes = workspace.numel() * workspace.element_size()
+    rc = lib().zt_attn_decode(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out), arr, B, n_ctx, n_heads, n_kv_heads,
+                              dim, _ptr(workspace), nbytes, _stream(stream))
+    _check(rc, "zt_attn_decode")
+
+
+def rmsnorm(x, w, y, rows, cols, eps=1e-5, stream=None):
+    _f32_cuda(x, w, y)
+    _check(lib().zt_rmsnorm_forward(_ptr(x), _ptr(w), _ptr(y), rows, cols, eps, _stream(stream)), "zt_rmsnorm_forward")
+
+
+def rope(x, y, rows, cols, pos, theta, head_dim, stream=None):
+    _f32_cuda(x, y)
+    _check(lib().zt_rope_forward(_ptr(x), _ptr(y), rows, cols, pos, theta, head_dim, _stream(stream)),
+           "zt_rope_forward")
+
+
+def fill_normal(t, seed, mean=0.0, sigma=1.0, stream=None):
+    _f32_cuda(t)
+    _check(lib().zt_fill_normal(_ptr(t), t.numel(), seed, mean, sigma, _stream(stream)), "zt_fill_normal")
+
+
+def fill_uniform(t, seed, lo=0.0, hi=1.0, stream=None):
+    _f32_cuda(t)
+    _check(lib().zt_fill_uniform(_ptr(t), t.numel(), seed, lo, hi, _stream(stream)), "zt_fill_uniform")
