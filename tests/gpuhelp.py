@@ -8,6 +8,7 @@ THETA = 500000.0
 
 FWD_TOL = 1e-4    # max |out - twin|, forward and decode (north_star)
 BWD_REL = 1e-3    # max |g - twin| / max |twin| per gradient (north_star)
+BWD_FLOOR = 1e-6  # absolute floor, for gradients the twin makes exactly zero (dq, dk at T = 1)
 
 
 def dev_normal(torch, zt, n, seed, sigma=1.0):
@@ -33,5 +34,8 @@ def max_abs(a, b):
 
 
 def rel_err(a, b):
-    scale = float(np.max(np.abs(np.asarray(b, np.float64)))) if np.size(b) else 1.0
-    return max_abs(a, b) / max(scale, 1e-30)
+    """max|a - b| / max|b|, the reference's relative convention
+    (src/train.zig:682-693), with BWD_FLOOR * BWD_REL^-1 as the smallest scale so
+    a twin gradient that is exactly zero is met by rounding noise below 1e-6."""
+    scale = float(np.max(np.abs(np.asarray(b, np.float64)))) if np.size(b) else 0.0
+    return max_abs(a, b) / max(scale, BWD_FLOOR / BWD_REL)

@@ -76,19 +76,27 @@ DeviceState *device_state() {
     return st.ok ? &st : nullptr;
 }
 
+// Kernels live in the code object named by their prefix; a lookup never
+// touches another module, so no failed hipModuleGetFunction is left behind in
+// the thread's last-error slot for the caller's next HIP call to report.
+int module_of(const char *name) {
+    if (strncmp(name, "zt_fwd_", 7) == 0) return 0;
+    if (strncmp(name, "zt_bwd_", 7) == 0) return 1;
+    if (strncmp(name, "zt_dec_", 7) == 0) return 2;
+    return 3;
+}
+
 hipFunction_t get_fn(DeviceState *st, const char *name) {
     std::lock_guard<std::mutex> lk(st->mu);
     auto it = st->fns.find(name);
     if (it != st->fns.end()) return it->second;
-    for (hipModule_t m : st->mods) {
-        hipFunction_t f = nullptr;
-        if (hipModuleGetFunction(&f, m, name) == hipSuccess && f) {
-            st->fns.emplace(name, f);
-            return f;
-        }
+    hipFunction_t f = nullptr;
+    if (hipModuleGetFunction(&f, st->mods[module_of(name)], name) != hipSuccess || !f) {
+        (void)hipGetLastError();
+        return nullptr;
     }
-    (void)hipGetLastError();
-    return nullptr;
+    st->fns.emplace(name, f);
+    return f;
 }
 
 template <class Args>
