@@ -132,10 +132,11 @@ def main():
     # Algorithmic FLOPs per launch: the forward's two matmuls; of the backward's
     # five (S recompute, dP, dV, dK, dQ) the dk/dv kernel owns four and the dq
     # kernel one -- the dq kernel's own recompute earns no credit.
+    n_fwd, n_dq, n_dkdv = zt.plan(B, T, H, Hkv, D)
     kernels = [
-        {"kernel": f"zt_fwd_d128", "ms": t_fwd, "flop": fwd_flop},
-        {"kernel": f"zt_bwd_dq_d128", "ms": t_dq, "flop": unit},
-        {"kernel": f"zt_bwd_dkdv_d128_hs4", "ms": t_dkdv, "flop": 4 * unit},
+        {"kernel": n_fwd, "ms": t_fwd, "flop": fwd_flop},
+        {"kernel": n_dq, "ms": t_dq, "flop": unit},
+        {"kernel": n_dkdv, "ms": t_dkdv, "flop": 4 * unit},
     ]
     for kk in kernels:
         kk["tflops"] = kk["flop"] / (kk["ms"] * 1e-3) / 1e12

@@ -136,6 +136,13 @@ int zt_rope_forward(const float *x, float *y, int rows, int cols, int pos, doubl
 int zt_fill_normal(float *dst, size_t n, uint64_t seed, double mean, double sigma, hipStream_t stream);
 int zt_fill_uniform(float *dst, size_t n, uint64_t seed, double lo, double hi, hipStream_t stream);
 
+/* The kernel names this library launches for a forward and a backward at
+ * this shape on the current device (for profilers and benchmarks), each
+ * written NUL-terminated into a buffer of `len` bytes.  1 if the shape is
+ * refused or no device is usable. */
+int zt_attn_plan(int B, int T, int n_heads, int n_kv_heads, int dim, int max_tile, char *fwd, char *dq,
+                 char *dkdv, size_t len);
+
 /* Library version string, and the LDS ceiling per workgroup the library read
  * for the current device (0 = no usable device / code object). */
 const char *zt_attn_version(void);

@@ -52,7 +52,7 @@ def test_shmem_counts(zt):
     for d in range(32, 257, 2):
         f64, f32 = L.zt_attn_forward_shmem(d, 64, 1), L.zt_attn_forward_shmem(d, 32, 1)
         assert 0 < f32 <= f64 <= 160 * 1024
-        assert L.zt_attn_bwd_dq_shmem(d, 64) == f64
+        assert 0 < L.zt_attn_bwd_dq_shmem(d, 32) <= L.zt_attn_bwd_dq_shmem(d, 64) <= 160 * 1024
         assert 0 < L.zt_attn_bwd_dkdv_shmem(d) <= 160 * 1024
     assert L.zt_attn_forward_shmem(33, 64, 1) == 0 and L.zt_attn_bwd_dkdv_shmem(300) == 0
 

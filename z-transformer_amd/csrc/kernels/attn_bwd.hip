@@ -296,8 +296,12 @@ __device__ __forceinline__ void bwd_dkdv_body(const BwdArgs &a) {
     }
 }
 
+// Up to d = 192 the dq kernel fits two waves per SIMD without spilling when
+// asked to (four accumulator/operand sets of DP/4 registers each); above that
+// it keeps one.
 #define ZT_BWD_DQ(DP, BK)                                                                          \
-    extern "C" __global__ void __launch_bounds__(256) zt_bwd_dq_d##DP##_k##BK(BwdArgs a) {      \
+    extern "C" __global__ void __launch_bounds__(256, (DP) <= 192 ? 2 : 1)                        \
+        zt_bwd_dq_d##DP##_k##BK(BwdArgs a) {                                                       \
         bwd_dq_body<DP, BK>(a);                                                                    \
     }
 #define ZT_BWD_DKDV(DP, HS)                                                                        \

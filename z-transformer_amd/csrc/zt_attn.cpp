@@ -132,9 +132,14 @@ int pad32(int dim) { return (dim + 31) / 32 * 32; }
 
 int heads_per_wg(int group) { return group % 4 == 0 ? 4 : (group % 2 == 0 ? 2 : 1); }
 
-// Forward / dq key tile for a width and a caller cap: 64 or 32 keys.
-int key_tile(int dp, int max_tile) {
-    const int preferred = env_choice("ZT_ATTN_BK", dp <= 64 ? 64 : 32, {32, 64});
+// Key tile (keys staged in LDS per step) for a width and a caller cap: 64 or
+// 32.  Measured on MI355X (C2/C3/C5 shapes): the 64-key tile wins wherever it
+// does not cost a resident workgroup per CU; for the forward at d in [96, 192]
+// the 32-key tile keeps three workgroups resident instead of two and wins.
+enum class Tiled { Forward, Dq };
+int key_tile(Tiled which, int dp, int max_tile) {
+    const int dflt = (which == Tiled::Forward && dp >= 96 && dp <= 192) ? 32 : 64;
+    const int preferred = env_choice("ZT_ATTN_BK", dflt, {32, 64});
     return max_tile >= 64 ? preferred : 32;
 }
 size_t kv_tile_bytes(int dp, int bk) { return (size_t)2 * bk * (dp + 4) * sizeof(float); }
@@ -211,7 +216,7 @@ int forward_impl(const float *q, const float *k, const float *v, float *out, int
     DeviceState *st = require_device();
     if (!st) return 1;
     const int dp = pad32(dim);
-    int bk = key_tile(dp, max_tile);
+    int bk = key_tile(Tiled::Forward, dp, max_tile);
     if (kv_tile_bytes(dp, bk) > st->lds_limit) bk = 32;
     if (kv_tile_bytes(dp, bk) > st->lds_limit) {
         fprintf(stderr, "zt_attn: head_dim %d needs %zu bytes of LDS per workgroup even at a 32-key tile, and\n"
@@ -256,11 +261,15 @@ int backward_prepare(const float *q, const float *k, const float *v, const float
     DeviceState *st = require_device();
     if (!st) return 1;
     const int dp = pad32(dim);
-    int bk = key_tile(dp, max_tile);
+    int bk = key_tile(Tiled::Dq, dp, max_tile);
     if (kv_tile_bytes(dp, bk) > st->lds_limit) bk = 32;
     const int group = n_heads / n_kv_heads;
-    int hs = env_choice("ZT_ATTN_HS", heads_per_wg(group), {1, 2, 4});
-    if (group % hs != 0) hs = heads_per_wg(group);
+    // dk/dv head split: two parts where the group allows (measured best at
+    // g = 4, d = 128 and 256: half the Q/dO staging of a 4-way split, twice
+    // the workgroups of none).
+    const int hs_dflt = group % 2 == 0 ? 2 : 1;
+    int hs = env_choice("ZT_ATTN_HS", hs_dflt, {1, 2, 4});
+    if (group % hs != 0) hs = hs_dflt;
     while (hs > 1 && dkdv_bytes(dp, hs) > st->lds_limit) hs /= 2;
     if (kv_tile_bytes(dp, bk) > st->lds_limit || dkdv_bytes(dp, hs) > st->lds_limit) {
         fprintf(stderr, "zt_attn: head_dim %d needs more LDS per workgroup than this device grants (%zu).\n", dim,
@@ -334,7 +343,7 @@ DecGeom decode_geom(int B, int n_ctx, int n_heads, int n_kv_heads, int dim) {
     g.dp = dim <= 32 ? 32 : dim <= 64 ? 64 : dim <= 128 ? 128 : 256;
     g.ks = 8 * (64 / (g.dp / 4));
     const long long pairs = (long long)B * n_kv_heads * g.n_gsub;
-    const long long target = env_choice("ZT_DEC_WGS", 4096, {1024, 2048, 4096, 8192, 16384, 32768});
+    const long long target = env_choice("ZT_DEC_WGS", 2048, {1024, 2048, 4096, 8192, 16384, 32768});
     long long per_seq = (target + pairs - 1) / pairs;
     if (per_seq < 1) per_seq = 1;
     long long chunk = (n_ctx + per_seq - 1) / per_seq;
@@ -356,13 +365,13 @@ size_t zt_attn_forward_shmem(int dim, int tile, int group_q) {
     (void)group_q;
     if (!zt_attn_dim_ok(dim)) return 0;
     const int dp = pad32(dim);
-    return kv_tile_bytes(dp, key_tile(dp, tile));
+    return kv_tile_bytes(dp, key_tile(Tiled::Forward, dp, tile));
 }
 
 size_t zt_attn_bwd_dq_shmem(int dim, int tile) {
     if (!zt_attn_dim_ok(dim)) return 0;
     const int dp = pad32(dim);
-    return kv_tile_bytes(dp, key_tile(dp, tile));
+    return kv_tile_bytes(dp, key_tile(Tiled::Dq, dp, tile));
 }
 
 size_t zt_attn_bwd_dkdv_shmem(int dim) {
@@ -556,6 +565,31 @@ int zt_fill_normal(float *dst, size_t n, uint64_t seed, double mean, double sigm
 
 int zt_fill_uniform(float *dst, size_t n, uint64_t seed, double lo, double hi, hipStream_t stream) {
     return fill_impl("zt_fill_uniform", dst, n, seed, lo, hi, stream);
+}
+
+int zt_attn_plan(int B, int T, int n_heads, int n_kv_heads, int dim, int max_tile, char *fwd, char *dq,
+                 char *dkdv, size_t len) {
+    if (!fwd || !dq || !dkdv || len < 32 || B < 1 || T < 1 || !zt_attn_dim_ok(dim) || n_heads <= 0 ||
+        n_kv_heads <= 0 || n_heads % n_kv_heads != 0 || max_tile < 1)
+        return 1;
+    DeviceState *st = device_state();
+    if (!st) return 1;
+    const int dp = pad32(dim);
+    int bk = key_tile(Tiled::Forward, dp, max_tile);
+    if (kv_tile_bytes(dp, bk) > st->lds_limit) bk = 32;
+    snprintf(fwd, len, "zt_fwd_d%d_k%d", dp, bk);
+    BwdArgs a;
+    DeviceState *st2 = nullptr;
+    unsigned ba = 0, bb = 0;
+    char na[64], nb[64];
+    // Shape-only planning: the pointers are placeholders that are never used.
+    float dummy = 0.f;
+    if (backward_prepare(&dummy, &dummy, &dummy, &dummy, &dummy, &dummy, &dummy, &dummy, &dummy, &dummy, B, T,
+                         n_heads, n_kv_heads, dim, max_tile, &a, &st2, na, nb, &ba, &bb))
+        return 1;
+    snprintf(dq, len, "%s", na);
+    snprintf(dkdv, len, "%s", nb);
+    return 0;
 }
 
 const char *zt_attn_version(void) { return "zt_attn gfx950 0.1"; }

@@ -21,7 +21,7 @@ ABI_SYMBOLS = [
     "zt_attn_forward_batched", "zt_attn_backward_batched", "zt_attn_bwd_dq", "zt_attn_bwd_dkdv",
     "zt_attn_decode_workspace", "zt_attn_decode",
     "zt_rmsnorm_forward", "zt_rope_forward", "zt_fill_normal", "zt_fill_uniform", "zt_attn_version",
-    "zt_attn_lds_limit",
+    "zt_attn_lds_limit", "zt_attn_plan",
 ]
 HOLDER_SYMBOLS = [
     "zt_bytes_for", "zt_to_cint", "zt_forward_bounds", "zt_holder_init", "zt_holder_deinit",
@@ -68,6 +68,7 @@ def lib():
             "zt_fill_uniform": (I, [P, Z, U64, D, D, P]),
             "zt_attn_version": (ctypes.c_char_p, []),
             "zt_attn_lds_limit": (Z, []),
+            "zt_attn_plan": (I, [I, I, I, I, I, I, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, Z]),
             "zt_bytes_for": (I, [I, Z, Z, Z, Z, ctypes.POINTER(Z)]),
             "zt_to_cint": (I, [Z, ctypes.POINTER(I)]),
             "zt_forward_bounds": (I, [I, I, I, I]),
@@ -175,6 +176,13 @@ def rope(x, y, rows, cols, pos, theta, head_dim, stream=None):
     _f32_cuda(x, y)
     _check(lib().zt_rope_forward(_ptr(x), _ptr(y), rows, cols, pos, theta, head_dim, _stream(stream)),
            "zt_rope_forward")
+
+
+def plan(B, T, n_heads, n_kv_heads, dim, max_tile=64):
+    """(forward, dq, dk/dv) kernel names the library launches at this shape."""
+    bufs = [ctypes.create_string_buffer(64) for _ in range(3)]
+    _check(lib().zt_attn_plan(B, T, n_heads, n_kv_heads, dim, max_tile, *bufs, 64), "zt_attn_plan")
+    return tuple(b.value.decode() for b in bufs)
 
 
 def fill_normal(t, seed, mean=0.0, sigma=1.0, stream=None):
