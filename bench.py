@@ -201,6 +201,17 @@ def main():
         log(f"RMSNorm {rows}x{cols}: {t_n * 1e3:.2f} us, {gbs:.0f} GB/s")
         del xs, ys
 
+    # ---------------- Reference point: a plain 1 GiB device copy ----------------
+    # The achievable streaming rate on this box, and the known-size kernel that
+    # calibrates the FETCH_SIZE / WRITE_SIZE counters in profiles/.
+    src = torch.empty(1 << 28, device=dev)
+    dst = torch.empty_like(src)
+    src.fill_(1.0)
+    t_cp = event_time(torch, lambda: dst.copy_(src), 10)
+    copy_gbs = 2 * src.numel() * 4 / (t_cp * 1e-3) / 1e9
+    log(f"device copy 1 GiB: {t_cp * 1e3:.0f} us, {copy_gbs:.0f} GB/s")
+    del src, dst
+
     # ---------------- CPU baseline: the restatement on a bounded sample ----------------
     cpu = None
     if not args.no_cpu:
@@ -241,6 +252,7 @@ def main():
         "decode": {"workload": "C4 B=64 n_keys=8192 Hq=32 Hkv=8 d=128 f32", "us": round(t_dec * 1e3, 2),
                    "GB/s": round(dec_gbs, 1), "bytes": dec_bytes, "frac_hbm": round(dec_gbs / PEAK_HBM, 4)},
         "rmsnorm": norm,
+        "hbm_copy": {"bytes": 2 * (1 << 30), "GB/s": round(copy_gbs, 1), "frac_hbm": round(copy_gbs / PEAK_HBM, 4)},
     }
     print(json.dumps(line), flush=True)
 
