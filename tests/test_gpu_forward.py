@@ -48,6 +48,16 @@ def test_forward_matches_twin(gpu, zt, oracle, threads, B, T, H, Hkv, D):
     assert max_abs(out, ref) <= FWD_TOL
 
 
+@pytest.mark.parametrize("bk", ["32", "64"])
+@pytest.mark.parametrize("B,T,H,Hkv,D", [(1, 150, 8, 2, 128), (2, 70, 4, 4, 256), (1, 99, 6, 3, 66)])
+def test_forward_both_key_tiles(gpu, zt, oracle, monkeypatch, bk, B, T, H, Hkv, D):
+    monkeypatch.setenv("ZT_ATTN_BK", bk)
+    q, k, v = _inputs(gpu, zt, B, T, H, Hkv, D)
+    out = _run(gpu, zt, q, k, v, B, T, H, Hkv, D)
+    ref = oracle.attention_forward(host(q), host(k), host(v), B, T, H, Hkv, D)
+    assert max_abs(out, ref) <= FWD_TOL
+
+
 @pytest.mark.parametrize("max_tile", [1, 32, 64, 1024])
 def test_forward_any_tile_cap(gpu, zt, oracle, max_tile):
     B, T, H, Hkv, D = 1, 77, 4, 2, 64

@@ -71,28 +71,41 @@ __device__ __forceinline__ void bwd_dq_body(const BwdArgs &a) {
         __syncthreads();
         if (k0 >= kend_w) continue;
 
+        // S^T and dP^T for every 16-key sub-block.  Up to d = 192 the 2 * NJ
+        // independent accumulation chains are interleaved so consecutive MFMAs
+        // do not wait on each other; wider heads keep one sub-block at a time
+        // (interleaving them would spill).  Wholly invisible sub-blocks are
+        // computed and then masked.
         f4 s[NJ], dp[NJ];
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-            s[j] = zero4();
-            dp[j] = zero4();
-            if (k0 + 16 * j < kend_w) {
-                const float *krow = Ks + (16 * j + l16) * LW + grp * DQ;
-                const float *vrow = Vs + (16 * j + l16) * LW + grp * DQ;
+        for (int j = 0; j < NJ; ++j) { s[j] = zero4(); dp[j] = zero4(); }
+        const float *krow = Ks + l16 * LW + grp * DQ;
+        const float *vrow = Vs + l16 * LW + grp * DQ;
+        auto score_step = [&](int j, int kk) {
+            const f4 kx = *reinterpret_cast<const f4 *>(krow + 16 * j * LW + kk);
+            const f4 vx = *reinterpret_cast<const f4 *>(vrow + 16 * j * LW + kk);
+            s[j] = mfma16(kx.x, qr[kk + 0], s[j]);
+            dp[j] = mfma16(vx.x, dor[kk + 0], dp[j]);
+            s[j] = mfma16(kx.y, qr[kk + 1], s[j]);
+            dp[j] = mfma16(vx.y, dor[kk + 1], dp[j]);
+            s[j] = mfma16(kx.z, qr[kk + 2], s[j]);
+            dp[j] = mfma16(vx.z, dor[kk + 2], dp[j]);
+            s[j] = mfma16(kx.w, qr[kk + 3], s[j]);
+            dp[j] = mfma16(vx.w, dor[kk + 3], dp[j]);
+        };
+        if constexpr (DP <= 192) {
 #pragma unroll
-                for (int kk = 0; kk < DQ; kk += 4) {
-                    const f4 kx = *reinterpret_cast<const f4 *>(krow + kk);
-                    const f4 vx = *reinterpret_cast<const f4 *>(vrow + kk);
-                    s[j] = mfma16(kx.x, qr[kk + 0], s[j]);
-                    dp[j] = mfma16(vx.x, dor[kk + 0], dp[j]);
-                    s[j] = mfma16(kx.y, qr[kk + 1], s[j]);
-                    dp[j] = mfma16(vx.y, dor[kk + 1], dp[j]);
-                    s[j] = mfma16(kx.z, qr[kk + 2], s[j]);
-                    dp[j] = mfma16(vx.z, dor[kk + 2], dp[j]);
-                    s[j] = mfma16(kx.w, qr[kk + 3], s[j]);
-                    dp[j] = mfma16(vx.w, dor[kk + 3], dp[j]);
-                }
-            }
+            for (int kk = 0; kk < DQ; kk += 4)
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) score_step(j, kk);
+        } else {
+#pragma unroll
+            for (int j = 0; j < NJ; ++j)
+#pragma unroll
+                for (int kk = 0; kk < DQ; kk += 4) score_step(j, kk);
+        }
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int key = k0 + 16 * j + 4 * grp + r;
@@ -156,16 +169,17 @@ __device__ __forceinline__ void bwd_dq_body(const BwdArgs &a) {
     }
 }
 
-template <int DP, int HS>
+template <int DP, int HS, int KW>
 __device__ __forceinline__ void bwd_dkdv_body(const BwdArgs &a) {
-    constexpr int LW = DP + 4, DQ = DP / 4, NT = DP / 16, KW = 4 / HS;
+    constexpr int LW = DP + 4, DQ = DP / 4, NT = DP / 16, NTH = 64 * KW * HS;
     constexpr int BQ = 16;
     // Per head-split part: Q rows, dO rows, and (m2, 1/l, delta) per row.
-    // One buffer: the staging tiles, reused at the end for the head-split sum,
-    // which needs (HS-1)*KW*64*2*NT float4 <= 2*HS*BQ*LW floats for HS in {1,2,4}.
-    __shared__ float smem[2 * HS * BQ * LW + HS * BQ * 4];
+    // One buffer: the staging tiles, reused at the end for the head-split sum
+    // ((HS-1) parts x KW blocks x 64 lanes x 2*NT float4).
+    constexpr int STAGE_F = 2 * HS * BQ * LW + HS * BQ * 4;
+    constexpr int RED_F = (HS - 1) * KW * 64 * 2 * NT * 4;
+    __shared__ float smem[STAGE_F > RED_F ? STAGE_F : RED_F];
     float *Qs = smem, *Ds = smem + HS * BQ * LW, *St = smem + 2 * HS * BQ * LW;
-    static_assert((HS - 1) * KW * 64 * 2 * NT * 4 <= 2 * HS * BQ * LW, "reduction buffer");
 
     const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, grp = lane >> 4, w = tid >> 6;
     const int kbw = w % KW, hs = w / KW;
@@ -203,8 +217,8 @@ __device__ __forceinline__ void bwd_dkdv_body(const BwdArgs &a) {
                 for (int part = 0; part < HS; ++part) {
                     const int hh = kvh * group + part * hpp + hi;
                     const size_t off = (size_t)b * a.T * qld + (size_t)t0 * qld + (size_t)hh * a.dim;
-                    stage_rows<DP, LW, 256>(Qs + part * BQ * LW, a.q + off, qld, BQ, nvalid, a.dim, vec4, tid);
-                    stage_rows<DP, LW, 256>(Ds + part * BQ * LW, a.dout + off, qld, BQ, nvalid, a.dim, vec4, tid);
+                    stage_rows<DP, LW, NTH>(Qs + part * BQ * LW, a.q + off, qld, BQ, nvalid, a.dim, vec4, tid);
+                    stage_rows<DP, LW, NTH>(Ds + part * BQ * LW, a.dout + off, qld, BQ, nvalid, a.dim, vec4, tid);
                 }
                 if (tid < HS * BQ) {
                     const int part = tid / BQ, r = tid % BQ, t = t0 + r;
@@ -269,7 +283,7 @@ __device__ __forceinline__ void bwd_dkdv_body(const BwdArgs &a) {
 
     // Sum the head-split partials in a fixed order (part 0 + 1 + ...).
     if constexpr (HS > 1) {
-        float *red = Qs;  // reuse: (HS-1) parts x KW blocks x 64 lanes x 2*NT f4
+        float *red = smem;  // (HS-1) parts x KW blocks x 64 lanes x 2*NT f4
         __syncthreads();
         if (hs > 0) {
             f4 *dst = reinterpret_cast<f4 *>(red) + (((hs - 1) * KW + kbw) * 64 + lane) * 2 * NT;
@@ -296,6 +310,163 @@ __device__ __forceinline__ void bwd_dkdv_body(const BwdArgs &a) {
     }
 }
 
+// dk/dv with asynchronous staging: the Q/dO rows of stage s+1 stream into the
+// other half of a double-buffered LDS tile (dma16, no registers) while stage s
+// computes, with one barrier per stage.  Requires dim == DP (every chunk of a
+// row is inside the head) and 16-byte aligned q/dout; the host falls back to
+// bwd_dkdv_body otherwise.  Same arithmetic as bwd_dkdv_body.
+template <int DP, int HS>
+__device__ __forceinline__ void bwd_dkdv_dma_body(const BwdArgs &a) {
+    constexpr int DQ = DP / 4, NT = DP / 16, KW = 4 / HS, BQ = 16;
+    constexpr int CPR = DP / 4;          // 16-byte chunks per row
+    constexpr int TILE = BQ * DP;        // floats per (part, array) tile
+    constexpr int NI = BQ * CPR / 64;    // dma16 wave-instructions per tile
+    constexpr int STAGE = HS * 2 * TILE; // floats per buffer
+    __shared__ __attribute__((aligned(16))) float smem[2 * STAGE + 2 * HS * BQ * 4];
+    float *const stats = smem + 2 * STAGE;
+    static_assert((HS - 1) * KW * 64 * 2 * NT * 4 <= 2 * STAGE, "reduction buffer");
+
+    const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, grp = lane >> 4, w = tid >> 6;
+    const int kbw = w % KW, hs = w / KW;
+    const int per_tile = a.Hkv * a.B;
+    const int ktile = (int)blockIdx.x / per_tile;
+    const int rem = (int)blockIdx.x % per_tile;
+    const int kvh = rem % a.Hkv, b = rem / a.Hkv;
+    const int group = a.H / a.Hkv;
+    const int hpp = group / HS;
+    const int wg_s0 = ktile * 16 * KW;
+    const int s0 = wg_s0 + 16 * kbw;
+    const size_t qld = (size_t)a.H * DP, kld = (size_t)a.Hkv * DP;
+    const size_t kvoff = (size_t)b * a.T * kld + (size_t)kvh * DP;
+    const size_t qbat = (size_t)b * a.T * qld;
+
+    const int my_key = s0 + l16;
+    const bool key_ok = my_key < a.T;
+    float kr[DQ], vr[DQ];
+    load_row_seg<DQ>(kr, a.k + kvoff + (size_t)my_key * kld, grp * DQ, DP, true, key_ok, a.scale_log2e);
+    load_row_seg<DQ>(vr, a.v + kvoff + (size_t)my_key * kld, grp * DQ, DP, true, key_ok, 1.f);
+
+    f4 dka[NT], dva[NT];
+#pragma unroll
+    for (int i = 0; i < NT; ++i) { dka[i] = zero4(); dva[i] = zero4(); }
+
+    const int n_t = (a.T - wg_s0 + BQ - 1) / BQ;  // 16-row tiles of the suffix
+    const int n_stage = hpp * n_t;                // times the heads of a part
+
+    // Issues the copies of stage `st` into buffer `buf`; the statistics go to
+    // registers and are written to LDS by put_stats after the current compute.
+    float sm2 = 0.f, sil = 0.f, sde = 0.f;
+    auto issue = [&](int st, int buf) {
+        const int hi = st / n_t, t0 = wg_s0 + (st % n_t) * BQ;
+        if (tid < HS * BQ) {
+            const int part = tid / BQ, t = t0 + tid % BQ;
+            const int hh = kvh * group + part * hpp + hi;
+            sm2 = 0.f; sil = 0.f; sde = 0.f;
+            if (t < a.T) {
+                const size_t o = ((size_t)b * a.T + t) * a.H + hh;
+                sm2 = a.row_max[o] * kLog2e;
+                sil = 1.f / a.row_den[o];
+                sde = a.row_del[o];
+            }
+        }
+        for (int i = w; i < HS * 2 * NI; i += 4) {
+            const int part = i / (2 * NI), arr = (i / NI) & 1, ii = i % NI;
+            const int hh = kvh * group + part * hpp + hi;
+            const float *src = (arr ? a.dout : a.q) + qbat + (size_t)hh * DP;
+            const int e = ii * 64 + lane;
+            const int r = e / CPR, c = swz<CPR>(e % CPR, r);
+            const int t = min(t0 + r, a.T - 1);  // rows past T: a real row, masked below
+            dma16(src + (size_t)t * qld + 4 * c, smem + buf * STAGE + (part * 2 + arr) * TILE + ii * 256);
+        }
+    };
+    auto put_stats = [&](int buf) {
+        if (tid < HS * BQ) {
+            float *sp = stats + (buf * HS * BQ + tid) * 4;
+            sp[0] = sm2; sp[1] = sil; sp[2] = sde;
+        }
+    };
+
+    issue(0, 0);
+    put_stats(0);
+    wait_dma();
+    __syncthreads();
+    for (int st = 0; st < n_stage; ++st) {
+        const int buf = st & 1;
+        if (st + 1 < n_stage) issue(st + 1, buf ^ 1);
+        const int t0 = wg_s0 + (st % n_t) * BQ;
+        if (!(t0 + 15 < s0 || s0 >= a.T)) {
+            const float *qs = smem + buf * STAGE + (hs * 2 + 0) * TILE;
+            const float *ds = smem + buf * STAGE + (hs * 2 + 1) * TILE;
+            const float *sp = stats + buf * HS * BQ * 4 + hs * BQ * 4;
+            f4 s = zero4(), dp = zero4();
+#pragma unroll
+            for (int kk = 0; kk < DQ; kk += 4) {
+                const int off = l16 * DP + 4 * swz<CPR>((grp * DQ + kk) >> 2, l16);
+                const f4 qx = *reinterpret_cast<const f4 *>(qs + off);
+                const f4 dx = *reinterpret_cast<const f4 *>(ds + off);
+                s = mfma16(qx.x, kr[kk + 0], s);
+                dp = mfma16(dx.x, vr[kk + 0], dp);
+                s = mfma16(qx.y, kr[kk + 1], s);
+                dp = mfma16(dx.y, vr[kk + 1], dp);
+                s = mfma16(qx.z, kr[kk + 2], s);
+                dp = mfma16(dx.z, vr[kk + 2], dp);
+                s = mfma16(qx.w, kr[kk + 3], s);
+                dp = mfma16(dx.w, vr[kk + 3], dp);
+            }
+            f4 p, dsv;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int tr = 4 * grp + r, t = t0 + tr;
+                const float m2 = sp[tr * 4 + 0], il = sp[tr * 4 + 1], de = sp[tr * 4 + 2];
+                const bool vis = (t < a.T) && (t >= my_key);
+                const float pr = vis ? exp2f(s[r] - m2) * il : 0.f;
+                p[r] = pr;
+                dsv[r] = pr * (dp[r] - de);
+            }
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+                const int tr = 4 * grp + kk;
+                const float pv = p[kk], dv = dsv[kk];
+#pragma unroll
+                for (int i = 0; i < NT; ++i) {
+                    const int off = tr * DP + 4 * swz<CPR>(4 * i + (l16 >> 2), tr) + (l16 & 3);
+                    dva[i] = mfma16(ds[off], pv, dva[i]);
+                    dka[i] = mfma16(qs[off], dv, dka[i]);
+                }
+            }
+        }
+        if (st + 1 < n_stage) put_stats(buf ^ 1);
+        wait_dma();
+        __syncthreads();
+    }
+
+    if constexpr (HS > 1) {
+        float *red = smem;
+        if (hs > 0) {
+            f4 *dst = reinterpret_cast<f4 *>(red) + (((hs - 1) * KW + kbw) * 64 + lane) * 2 * NT;
+#pragma unroll
+            for (int i = 0; i < NT; ++i) { dst[i] = dka[i]; dst[NT + i] = dva[i]; }
+        }
+        __syncthreads();
+        if (hs == 0) {
+            for (int part = 1; part < HS; ++part) {
+                const f4 *src = reinterpret_cast<const f4 *>(red) + (((part - 1) * KW + kbw) * 64 + lane) * 2 * NT;
+#pragma unroll
+                for (int i = 0; i < NT; ++i) { dka[i] += src[i]; dva[i] += src[NT + i]; }
+            }
+        }
+    }
+    if (hs == 0 && key_ok) {
+        float *dkrow = a.dk + kvoff + (size_t)my_key * kld;
+        float *dvrow = a.dv + kvoff + (size_t)my_key * kld;
+#pragma unroll
+        for (int i = 0; i < NT; ++i) {
+            *reinterpret_cast<f4 *>(dkrow + 16 * i + 4 * grp) = dka[i] * a.scale;
+            *reinterpret_cast<f4 *>(dvrow + 16 * i + 4 * grp) = dva[i];
+        }
+    }
+}
+
 // Up to d = 192 the dq kernel fits two waves per SIMD without spilling when
 // asked to (four accumulator/operand sets of DP/4 registers each); above that
 // it keeps one.
@@ -306,15 +477,35 @@ __device__ __forceinline__ void bwd_dkdv_body(const BwdArgs &a) {
     }
 #define ZT_BWD_DKDV(DP, HS)                                                                        \
     extern "C" __global__ void __launch_bounds__(256) zt_bwd_dkdv_d##DP##_hs##HS(BwdArgs a) {   \
-        bwd_dkdv_body<DP, HS>(a);                                                                  \
+        bwd_dkdv_body<DP, HS, 4 / HS>(a);                                                          \
+    }
+// Eight waves: 4 key blocks x 2 head halves share each staged Q/dO tile.
+#define ZT_BWD_DKDV8(DP)                                                                           \
+    extern "C" __global__ void __launch_bounds__(512) zt_bwd_dkdv8_d##DP##_hs2(BwdArgs a) {     \
+        bwd_dkdv_body<DP, 2, 4>(a);                                                                \
+    }
+#define ZT_BWD_DKDV_DMA(DP, HS)                                                                    \
+    extern "C" __global__ void __launch_bounds__(256) zt_bwd_dkdv_dma_d##DP##_hs##HS(BwdArgs a) { \
+        bwd_dkdv_dma_body<DP, HS>(a);                                                              \
     }
 #define ZT_BWD_ALL(DP)                                                                             \
-    ZT_BWD_DQ(DP, 32) ZT_BWD_DQ(DP, 64) ZT_BWD_DKDV(DP, 1) ZT_BWD_DKDV(DP, 2) ZT_BWD_DKDV(DP, 4)
+    ZT_BWD_DQ(DP, 32) ZT_BWD_DQ(DP, 64) ZT_BWD_DKDV(DP, 1) ZT_BWD_DKDV(DP, 2) ZT_BWD_DKDV8(DP)    \
+    ZT_BWD_DKDV_DMA(DP, 1) ZT_BWD_DKDV_DMA(DP, 2)
 
 ZT_BWD_ALL(32)
 ZT_BWD_ALL(64)
 ZT_BWD_ALL(96)
 ZT_BWD_ALL(128)
+// The 4-way splits: the 160 KB LDS holds 4 parts' tiles (double-buffered for
+// the asynchronous variant) up to d = 128.
+ZT_BWD_DKDV(32, 4)
+ZT_BWD_DKDV(64, 4)
+ZT_BWD_DKDV(96, 4)
+ZT_BWD_DKDV(128, 4)
+ZT_BWD_DKDV_DMA(32, 4)
+ZT_BWD_DKDV_DMA(64, 4)
+ZT_BWD_DKDV_DMA(96, 4)
+ZT_BWD_DKDV_DMA(128, 4)
 ZT_BWD_ALL(160)
 ZT_BWD_ALL(192)
 ZT_BWD_ALL(224)

@@ -27,8 +27,9 @@ __device__ __forceinline__ void attn_fwd_body(const FwdArgs &a) {
     constexpr int DQ = DP / 4;  // d values per lane group
     constexpr int NT = DP / 16; // 16-wide column tiles of the output
     constexpr int NJ = BK / 16; // 16-key sub-blocks per LDS tile
+    constexpr int LT = BK + 4;  // row stride of the transposed V tile
     __shared__ float Ks[BK * LW];
-    __shared__ float Vs[BK * LW];
+    __shared__ float Vt[DP * LT];  // V^T: column n of the tile is row n here
 
     const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, grp = lane >> 4, w = tid >> 6;
     const int RB = 4 / a.HW;
@@ -63,25 +64,30 @@ __device__ __forceinline__ void attn_fwd_body(const FwdArgs &a) {
         __syncthreads();
         const int nvalid = min(BK, a.n_keys - k0);
         stage_rows<DP, LW, 256>(Ks, kb + (size_t)k0 * kld, kld, BK, nvalid, a.dim, vec4, tid);
-        stage_rows<DP, LW, 256>(Vs, vb + (size_t)k0 * kld, kld, BK, nvalid, a.dim, vec4, tid);
+        stage_rows_t<DP, LT, 256>(Vt, vb + (size_t)k0 * kld, kld, BK, nvalid, a.dim, vec4, tid);
         __syncthreads();
         if (k0 >= kend_w) continue;  // wave-uniform: nothing here is visible to this wave
 
+        // Scores for every 16-key sub-block, the NJ accumulation chains
+        // interleaved so consecutive MFMAs are independent.  A sub-block that is
+        // wholly invisible to this wave is computed and then masked.
         f4 s[NJ];
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-            s[j] = zero4();
-            if (k0 + 16 * j < kend_w) {
-                const float *krow = Ks + (16 * j + l16) * LW + grp * DQ;
+        for (int j = 0; j < NJ; ++j) s[j] = zero4();
+        const float *krow = Ks + l16 * LW + grp * DQ;
 #pragma unroll
-                for (int kk = 0; kk < DQ; kk += 4) {
-                    const f4 kx = *reinterpret_cast<const f4 *>(krow + kk);
-                    s[j] = mfma16(kx.x, qr[kk + 0], s[j]);
-                    s[j] = mfma16(kx.y, qr[kk + 1], s[j]);
-                    s[j] = mfma16(kx.z, qr[kk + 2], s[j]);
-                    s[j] = mfma16(kx.w, qr[kk + 3], s[j]);
-                }
+        for (int kk = 0; kk < DQ; kk += 4) {
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+                const f4 kx = *reinterpret_cast<const f4 *>(krow + 16 * j * LW + kk);
+                s[j] = mfma16(kx.x, qr[kk + 0], s[j]);
+                s[j] = mfma16(kx.y, qr[kk + 1], s[j]);
+                s[j] = mfma16(kx.z, qr[kk + 2], s[j]);
+                s[j] = mfma16(kx.w, qr[kk + 3], s[j]);
             }
+        }
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int key = k0 + 16 * j + 4 * grp + r;
@@ -111,12 +117,15 @@ __device__ __forceinline__ void attn_fwd_body(const FwdArgs &a) {
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
             if (k0 + 16 * j >= kend_w) continue;
+            // A operand V^T[n = 16 i + l16][key = 16 j + 4 grp + kk], kk = 0..3: one 128-bit read.
+            const float *vcol = Vt + l16 * LT + 16 * j + 4 * grp;
 #pragma unroll
-            for (int kk = 0; kk < 4; ++kk) {
-                const float pv = s[j][kk];
-                const float *vrow = Vs + (16 * j + 4 * grp + kk) * LW + l16;
-#pragma unroll
-                for (int i = 0; i < NT; ++i) o[i] = mfma16(vrow[16 * i], pv, o[i]);
+            for (int i = 0; i < NT; ++i) {
+                const f4 vx = *reinterpret_cast<const f4 *>(vcol + 16 * i * LT);
+                o[i] = mfma16(vx.x, s[j][0], o[i]);
+                o[i] = mfma16(vx.y, s[j][1], o[i]);
+                o[i] = mfma16(vx.z, s[j][2], o[i]);
+                o[i] = mfma16(vx.w, s[j][3], o[i]);
             }
         }
     }

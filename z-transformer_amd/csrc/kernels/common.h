@@ -104,3 +104,82 @@ DEVI void stage_rows(float *lds, const float *g, size_t ld, int rows, int nvalid
         }
     }
 }
+
+// Asynchronous 16-byte global -> LDS copy (gfx950 global_load_lds_dwordx4): the
+// 64 lanes' 16 bytes land contiguously at lds_base + 16 * lane.  lds_base must
+// be the same for the whole wave.  Completion is awaited with wait_dma().
+DEVI void dma16(const float *g, float *lds_base) {
+    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void *)lds_base, 16, 0, 0);
+}
+DEVI void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// LDS tiles filled by dma16 have no row padding; instead the 16-byte chunk c of
+// row r is stored at chunk position c ^ (r & M), M = 15 when a row has a
+// multiple of 16 chunks (DP a multiple of 64), else 7.  With 16 rows read at one
+// column (MFMA A operand) the XOR puts them on 16 distinct 4-bank groups, and
+// with the 4 rows 4 apart a transposed read visits, their 4-chunk runs on 4
+// distinct groups: both conflict-free on 64 banks, as a +4-float pad is.  The
+// XOR stays inside an aligned group of M+1 chunks, so a row maps onto itself.
+template <int CPR>
+DEVI int swz(int chunk, int row) { return chunk ^ (row & (CPR % 16 == 0 ? 15 : 7)); }
+
+// Cooperative copy of `rows` rows x DP columns into LDS TRANSPOSED: element
+// (r, c) lands at lds[c * LT + r] (LT = rows + 4).  Consecutive lanes take
+// consecutive rows of one column chunk, so each scattered store of a wave hits
+// consecutive banks; a later 128-bit read of lds[n * LT + 4g .. 4g+3] then
+// yields four consecutive rows of column n, the A operand of four successive
+// k-steps.  Rows >= nvalid and columns >= dim are written as zero.
+template <int DP, int LT, int NT>
+DEVI void stage_rows_t(float *lds, const float *g, size_t ld, int rows, int nvalid, int dim, bool vec4,
+                       int tid) {
+    if (vec4) {
+        for (int e = tid; e < rows * (DP / 4); e += NT) {
+            const int r = e % rows, c = (e / rows) * 4;
+            f4 x = zero4();
+            if (r < nvalid && c < dim) x = *reinterpret_cast<const f4 *>(g + (size_t)r * ld + c);
+            lds[(c + 0) * LT + r] = x.x;
+            lds[(c + 1) * LT + r] = x.y;
+            lds[(c + 2) * LT + r] = x.z;
+            lds[(c + 3) * LT + r] = x.w;
+        }
+    } else {
+        for (int e = tid; e < rows * (DP / 2); e += NT) {
+            const int r = e % rows, c = (e / rows) * 2;
+            f2 x = f2{0.f, 0.f};
+            if (r < nvalid && c < dim) x = *reinterpret_cast<const f2 *>(g + (size_t)r * ld + c);
+            lds[(c + 0) * LT + r] = x.x;
+            lds[(c + 1) * LT + r] = x.y;
+        }
+    }
+}
+
+// One global read, two LDS layouts: element (r, c) of a rows x DP block goes to
+// rm[r * LW + c] (row-major, LW = DP + 4) and to tr[c * LT + r] (transposed,
+// LT = rows + 4).  Consecutive lanes take consecutive rows of one column chunk:
+// the row-major 128-bit stores then walk 4-bank steps (LW = DP + 4) and the
+// transposed scalar stores consecutive banks.  Zero beyond nvalid rows / dim.
+template <int DP, int LW, int LT, int NT>
+DEVI void stage_rows_both(float *rm, float *tr, const float *g, size_t ld, int rows, int nvalid, int dim,
+                          bool vec4, int tid) {
+    if (vec4) {
+        for (int e = tid; e < rows * (DP / 4); e += NT) {
+            const int r = e % rows, c = (e / rows) * 4;
+            f4 x = zero4();
+            if (r < nvalid && c < dim) x = *reinterpret_cast<const f4 *>(g + (size_t)r * ld + c);
+            *reinterpret_cast<f4 *>(rm + r * LW + c) = x;
+            tr[(c + 0) * LT + r] = x.x;
+            tr[(c + 1) * LT + r] = x.y;
+            tr[(c + 2) * LT + r] = x.z;
+            tr[(c + 3) * LT + r] = x.w;
+        }
+    } else {
+        for (int e = tid; e < rows * (DP / 2); e += NT) {
+            const int r = e % rows, c = (e / rows) * 2;
+            f2 x = f2{0.f, 0.f};
+            if (r < nvalid && c < dim) x = *reinterpret_cast<const f2 *>(g + (size_t)r * ld + c);
+            *reinterpret_cast<f2 *>(rm + r * LW + c) = x;
+            tr[(c + 0) * LT + r] = x.x;
+            tr[(c + 1) * LT + r] = x.y;
+        }
+    }
+}

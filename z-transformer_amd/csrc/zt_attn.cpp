@@ -42,6 +42,7 @@ struct DeviceState {
     std::once_flag once;
     bool ok = false;
     size_t lds_limit = 0;
+    int cus = 0;
     hipModule_t mods[4] = {};
     std::mutex mu;
     std::unordered_map<std::string, hipFunction_t> fns;
@@ -59,6 +60,9 @@ void load_device(DeviceState &st, int dev) {
             return;
         }
     }
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 1;
+    st.cus = cus;
     st.lds_limit = (size_t)lds;
     st.ok = true;
 }
@@ -100,7 +104,8 @@ hipFunction_t get_fn(DeviceState *st, const char *name) {
 }
 
 template <class Args>
-int launch(DeviceState *st, const char *name, unsigned blocks, const Args &args, hipStream_t stream) {
+int launch(DeviceState *st, const char *name, unsigned blocks, const Args &args, hipStream_t stream,
+           unsigned threads = kThreads) {
     hipFunction_t f = get_fn(st, name);
     if (!f) {
         fprintf(stderr, "zt_attn: FAIL kernel %s is missing from the code object.\n", name);
@@ -108,7 +113,7 @@ int launch(DeviceState *st, const char *name, unsigned blocks, const Args &args,
     }
     Args copy = args;
     void *params[] = {&copy};
-    const hipError_t e = hipModuleLaunchKernel(f, blocks, 1, 1, kThreads, 1, 1, 0, stream, params, nullptr);
+    const hipError_t e = hipModuleLaunchKernel(f, blocks, 1, 1, threads, 1, 1, 0, stream, params, nullptr);
     if (e != hipSuccess) {
         fprintf(stderr, "zt_attn: FAIL launch of %s: %s\n", name, hipGetErrorString(e));
         return 1;
@@ -133,17 +138,26 @@ int pad32(int dim) { return (dim + 31) / 32 * 32; }
 int heads_per_wg(int group) { return group % 4 == 0 ? 4 : (group % 2 == 0 ? 2 : 1); }
 
 // Key tile (keys staged in LDS per step) for a width and a caller cap: 64 or
-// 32.  Measured on MI355X (C2/C3/C5 shapes): the 64-key tile wins wherever it
-// does not cost a resident workgroup per CU; for the forward at d in [96, 192]
-// the 32-key tile keeps three workgroups resident instead of two and wins.
+// 32.  Measured on MI355X (C2/C3/C5 shapes): the dq kernel prefers 64 keys;
+// the forward prefers 64 only at d <= 64 -- above that the 32-key tile keeps
+// one more workgroup resident per CU (C5, d = 256: 0.84 ms vs 1.11 ms).
 enum class Tiled { Forward, Dq };
 int key_tile(Tiled which, int dp, int max_tile) {
-    const int dflt = (which == Tiled::Forward && dp >= 96 && dp <= 192) ? 32 : 64;
+    const int dflt = (which == Tiled::Forward && dp > 64) ? 32 : 64;
     const int preferred = env_choice("ZT_ATTN_BK", dflt, {32, 64});
     return max_tile >= 64 ? preferred : 32;
 }
+// LDS per workgroup: forward = K tile + transposed V tile; dq = K and V tiles.
+size_t fwd_tile_bytes(int dp, int bk) { return ((size_t)bk * (dp + 4) + (size_t)dp * (bk + 4)) * sizeof(float); }
 size_t kv_tile_bytes(int dp, int bk) { return (size_t)2 * bk * (dp + 4) * sizeof(float); }
-size_t dkdv_bytes(int dp, int hs) { return ((size_t)2 * hs * 16 * (dp + 4) + (size_t)hs * 16 * 4) * sizeof(float); }
+size_t dkdv_bytes(int dp, int hs, int kw = 0) {
+    if (kw == 0) kw = 4 / hs;
+    const size_t stage = (size_t)2 * hs * 16 * (dp + 4) + (size_t)hs * 16 * 4;
+    const size_t red = (size_t)(hs - 1) * kw * 64 * 2 * (dp / 16) * 4;
+    return (stage > red ? stage : red) * sizeof(float);
+}
+// The asynchronously staged dk/dv kernel: two buffers of unpadded tiles.
+size_t dkdv_dma_bytes(int dp, int hs) { return ((size_t)2 * hs * 2 * 16 * dp + (size_t)2 * hs * 16 * 4) * sizeof(float); }
 
 int refuse_T(int T) {
     fprintf(stderr,
@@ -217,11 +231,11 @@ int forward_impl(const float *q, const float *k, const float *v, float *out, int
     if (!st) return 1;
     const int dp = pad32(dim);
     int bk = key_tile(Tiled::Forward, dp, max_tile);
-    if (kv_tile_bytes(dp, bk) > st->lds_limit) bk = 32;
-    if (kv_tile_bytes(dp, bk) > st->lds_limit) {
+    if (fwd_tile_bytes(dp, bk) > st->lds_limit) bk = 32;
+    if (fwd_tile_bytes(dp, bk) > st->lds_limit) {
         fprintf(stderr, "zt_attn: head_dim %d needs %zu bytes of LDS per workgroup even at a 32-key tile, and\n"
                         "       this device grants %zu. Refusing.\n",
-                dim, kv_tile_bytes(dp, bk), st->lds_limit);
+                dim, fwd_tile_bytes(dp, bk), st->lds_limit);
         return 1;
     }
     if (!q || !k || !v || !out) {
@@ -249,7 +263,7 @@ int forward_impl(const float *q, const float *k, const float *v, float *out, int
 int backward_prepare(const float *q, const float *k, const float *v, const float *dout, float *dq, float *dk,
                      float *dv, float *row_max, float *row_den, float *row_del, int B, int T, int n_heads,
                      int n_kv_heads, int dim, int max_tile, BwdArgs *a, DeviceState **st_out, char *name_dq,
-                     char *name_dkdv, unsigned *blocks_dq, unsigned *blocks_dkdv) {
+                     char *name_dkdv, unsigned *blocks_dq, unsigned *blocks_dkdv, unsigned *threads_dkdv) {
     if (T < 1) return refuse_T(T);
     if (!zt_attn_dim_ok(dim)) return refuse_dim(dim);
     if (check_group(n_heads, n_kv_heads)) return 1;
@@ -269,7 +283,7 @@ int backward_prepare(const float *q, const float *k, const float *v, const float
     // the workgroups of none).
     const int hs_dflt = group % 2 == 0 ? 2 : 1;
     int hs = env_choice("ZT_ATTN_HS", hs_dflt, {1, 2, 4});
-    if (group % hs != 0) hs = hs_dflt;
+    if (group % hs != 0 || (hs == 4 && dp > 128)) hs = hs_dflt;  // 4-way split instantiated up to d = 128
     while (hs > 1 && dkdv_bytes(dp, hs) > st->lds_limit) hs /= 2;
     if (kv_tile_bytes(dp, bk) > st->lds_limit || dkdv_bytes(dp, hs) > st->lds_limit) {
         fprintf(stderr, "zt_attn: head_dim %d needs more LDS per workgroup than this device grants (%zu).\n", dim,
@@ -290,15 +304,33 @@ int backward_prepare(const float *q, const float *k, const float *v, const float
     a->n_row_tiles = (T + rows_per_wg - 1) / rows_per_wg;
     a->n_head_blocks = n_heads / a->HW;
     a->HS = hs;
-    const int keys_per_wg = 16 * (4 / hs);
+    // dk/dv variant, measured on MI355X (C2/C3/C5 shapes):
+    //  - eight-wave workgroups (4 key blocks x 2 head halves share each staged
+    //    Q/dO tile) for a 2-way split up to d = 128 (C3: 2.91 ms vs 3.22 ms);
+    //  - asynchronous double-buffered staging for wider heads (C5: 1.97 ms vs
+    //    2.27 ms) and for grids too small to hide the staging latency with
+    //    other workgroups; it needs whole-head rows on 16-byte aligned q/dout;
+    //  - otherwise the four-wave register-staged kernel.
+    const bool wide = env_choice("ZT_ATTN_W8", 1, {0, 1}) == 1 && hs == 2 && dp <= 128 &&
+                      dkdv_bytes(dp, 2, 4) <= st->lds_limit;
+    const int keys_per_wg = wide ? 64 : 16 * (4 / hs);
     a->n_key_tiles = (T + keys_per_wg - 1) / keys_per_wg;
+    const unsigned long long blocks_b = (unsigned long long)a->n_key_tiles * n_kv_heads * B;
+    const bool aligned = ((uintptr_t)q % 16 == 0) && ((uintptr_t)dout % 16 == 0);
+    const bool dma_ok = dim == dp && aligned && !(hs == 4 && dp > 128) && !(hs == 1 && dp >= 224) &&
+                        dkdv_dma_bytes(dp, hs) <= st->lds_limit;
+    const bool dma_pays = dp >= 160 || blocks_b < 2ull * (unsigned long long)st->cus;
+    const bool dma = !wide && dma_ok && env_choice("ZT_ATTN_DMA", dma_pays ? 1 : 0, {0, 1}) == 1;
     a->scale = (float)(1.0 / std::sqrt((double)dim));
     a->scale_log2e = (float)(1.4426950408889634 / std::sqrt((double)dim));
     const unsigned long long blocks_a = (unsigned long long)a->n_row_tiles * a->n_head_blocks * B;
-    const unsigned long long blocks_b = (unsigned long long)a->n_key_tiles * n_kv_heads * B;
     if (!grid_ok(blocks_a) || !grid_ok(blocks_b)) return 1;
     snprintf(name_dq, 64, "zt_bwd_dq_d%d_k%d", dp, bk);
-    snprintf(name_dkdv, 64, "zt_bwd_dkdv_d%d_hs%d", dp, hs);
+    if (wide)
+        snprintf(name_dkdv, 64, "zt_bwd_dkdv8_d%d_hs2", dp);
+    else
+        snprintf(name_dkdv, 64, dma ? "zt_bwd_dkdv_dma_d%d_hs%d" : "zt_bwd_dkdv_d%d_hs%d", dp, hs);
+    *threads_dkdv = wide ? 512 : kThreads;
     *blocks_dq = (unsigned)blocks_a;
     *blocks_dkdv = (unsigned)blocks_b;
     *st_out = st;
@@ -312,9 +344,9 @@ int backward_impl(const float *q, const float *k, const float *v, const float *d
     BwdArgs a;
     DeviceState *st = nullptr;
     char name_a[64], name_b[64];
-    unsigned blocks_a = 0, blocks_b = 0;
+    unsigned blocks_a = 0, blocks_b = 0, threads_b = kThreads;
     if (backward_prepare(q, k, v, dout, dq, dk, dv, row_max, row_den, row_del, B, T, n_heads, n_kv_heads, dim,
-                         max_tile, &a, &st, name_a, name_b, &blocks_a, &blocks_b))
+                         max_tile, &a, &st, name_a, name_b, &blocks_a, &blocks_b, &threads_b))
         return 1;
     if ((stage & 1) && !dq) {
         fprintf(stderr, "zt_attn: a null dq is not launchable.\n");
@@ -326,7 +358,7 @@ int backward_impl(const float *q, const float *k, const float *v, const float *d
     }
     if ((stage & 1) && launch(st, name_a, blocks_a, a, stream)) return 1;
     // Same stream: the dk/dv kernel reads the row statistics the first wrote.
-    if ((stage & 2) && launch(st, name_b, blocks_b, a, stream)) return 1;
+    if ((stage & 2) && launch(st, name_b, blocks_b, a, stream, threads_b)) return 1;
     return 0;
 }
 
@@ -365,7 +397,7 @@ size_t zt_attn_forward_shmem(int dim, int tile, int group_q) {
     (void)group_q;
     if (!zt_attn_dim_ok(dim)) return 0;
     const int dp = pad32(dim);
-    return kv_tile_bytes(dp, key_tile(Tiled::Forward, dp, tile));
+    return fwd_tile_bytes(dp, key_tile(Tiled::Forward, dp, tile));
 }
 
 size_t zt_attn_bwd_dq_shmem(int dim, int tile) {
@@ -376,7 +408,11 @@ size_t zt_attn_bwd_dq_shmem(int dim, int tile) {
 
 size_t zt_attn_bwd_dkdv_shmem(int dim) {
     if (!zt_attn_dim_ok(dim)) return 0;
-    return dkdv_bytes(pad32(dim), 4);
+    const int dp = pad32(dim);
+    size_t most = dkdv_bytes(dp, dp <= 128 ? 4 : 2);
+    for (int hs : {1, 2, 4})
+        if (!(hs == 4 && dp > 128) && dkdv_dma_bytes(dp, hs) > most) most = dkdv_dma_bytes(dp, hs);
+    return most;
 }
 
 int zt_attn_forward(const float *q, const float *k, const float *v, float *out, int T, int n_heads,
@@ -576,16 +612,16 @@ int zt_attn_plan(int B, int T, int n_heads, int n_kv_heads, int dim, int max_til
     if (!st) return 1;
     const int dp = pad32(dim);
     int bk = key_tile(Tiled::Forward, dp, max_tile);
-    if (kv_tile_bytes(dp, bk) > st->lds_limit) bk = 32;
+    if (fwd_tile_bytes(dp, bk) > st->lds_limit) bk = 32;
     snprintf(fwd, len, "zt_fwd_d%d_k%d", dp, bk);
     BwdArgs a;
     DeviceState *st2 = nullptr;
-    unsigned ba = 0, bb = 0;
+    unsigned ba = 0, bb = 0, tb = 0;
     char na[64], nb[64];
     // Shape-only planning: the pointers are placeholders that are never used.
     float dummy = 0.f;
     if (backward_prepare(&dummy, &dummy, &dummy, &dummy, &dummy, &dummy, &dummy, &dummy, &dummy, &dummy, B, T,
-                         n_heads, n_kv_heads, dim, max_tile, &a, &st2, na, nb, &ba, &bb))
+                         n_heads, n_kv_heads, dim, max_tile, &a, &st2, na, nb, &ba, &bb, &tb))
         return 1;
     snprintf(dq, len, "%s", na);
     snprintf(dkdv, len, "%s", nb);
