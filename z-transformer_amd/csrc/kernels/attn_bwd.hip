@@ -27,14 +27,14 @@
 #include "args.h"
 
 
-template <int DP, int BK>
+template <int DP, int BK, int NW>
 __device__ __forceinline__ void bwd_dq_body(const BwdArgs &a) {
     constexpr int LW = DP + 4, DQ = DP / 4, NT = DP / 16, NJ = BK / 16;
     __shared__ float Ks[BK * LW];
     __shared__ float Vs[BK * LW];
 
     const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, grp = lane >> 4, w = tid >> 6;
-    const int RB = 4 / a.HW;
+    const int RB = NW / a.HW;  // 16-row blocks per head in this workgroup
     const int per_tile = a.n_head_blocks * a.B;
     const int tile = a.n_row_tiles - 1 - (int)blockIdx.x / per_tile;
     const int rem = (int)blockIdx.x % per_tile;
@@ -66,8 +66,8 @@ __device__ __forceinline__ void bwd_dq_body(const BwdArgs &a) {
     for (int k0 = 0; k0 < kend_wg; k0 += BK) {
         __syncthreads();
         const int nvalid = min(BK, a.T - k0);
-        stage_rows<DP, LW, 256>(Ks, kb + (size_t)k0 * kld, kld, BK, nvalid, a.dim, vec4, tid);
-        stage_rows<DP, LW, 256>(Vs, vb + (size_t)k0 * kld, kld, BK, nvalid, a.dim, vec4, tid);
+        stage_rows<DP, LW, 64 * NW>(Ks, kb + (size_t)k0 * kld, kld, BK, nvalid, a.dim, vec4, tid);
+        stage_rows<DP, LW, 64 * NW>(Vs, vb + (size_t)k0 * kld, kld, BK, nvalid, a.dim, vec4, tid);
         __syncthreads();
         if (k0 >= kend_w) continue;
 
@@ -473,7 +473,10 @@ __device__ __forceinline__ void bwd_dkdv_dma_body(const BwdArgs &a) {
 #define ZT_BWD_DQ(DP, BK)                                                                          \
     extern "C" __global__ void __launch_bounds__(256, (DP) <= 192 ? 2 : 1)                        \
         zt_bwd_dq_d##DP##_k##BK(BwdArgs a) {                                                       \
-        bwd_dq_body<DP, BK>(a);                                                                    \
+        bwd_dq_body<DP, BK, 4>(a);                                                                 \
+    }                                                                                              \
+    extern "C" __global__ void __launch_bounds__(512) zt_bwd_dq8_d##DP##_k##BK(BwdArgs a) {      \
+        bwd_dq_body<DP, BK, 8>(a);                                                                 \
     }
 #define ZT_BWD_DKDV(DP, HS)                                                                        \
     extern "C" __global__ void __launch_bounds__(256) zt_bwd_dkdv_d##DP##_hs##HS(BwdArgs a) {   \

@@ -4,8 +4,8 @@
 // -- O = softmax(Q K^T / sqrt(d), causal) V with query row t at absolute
 // position q_offset + t seeing keys s <= q_offset + t, s < n_keys -- but with
 // a different schedule:
-//   * a workgroup is 4 waves; each wave owns 16 query rows of one query head.
-//     The 4 waves are HW query heads of ONE kv group x (4 / HW) row blocks,
+//   * a workgroup is NW = 4 or 8 waves; each wave owns 16 query rows of one
+//     query head.  The waves are HW query heads of ONE kv group x (NW / HW) row blocks,
 //     so each K/V tile staged in LDS is read from HBM/L2 once per kv group
 //     instead of once per query (the reference re-reads the prefix per query);
 //   * Q stays in registers for the whole key loop, pre-scaled by
@@ -21,7 +21,7 @@
 #include "args.h"
 
 
-template <int DP, int BK>
+template <int DP, int BK, int NW>
 __device__ __forceinline__ void attn_fwd_body(const FwdArgs &a) {
     constexpr int LW = DP + 4;  // LDS row stride: +16 B spreads row starts over banks
     constexpr int DQ = DP / 4;  // d values per lane group
@@ -32,7 +32,7 @@ __device__ __forceinline__ void attn_fwd_body(const FwdArgs &a) {
     __shared__ float Vt[DP * LT];  // V^T: column n of the tile is row n here
 
     const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, grp = lane >> 4, w = tid >> 6;
-    const int RB = 4 / a.HW;
+    const int RB = NW / a.HW;  // 16-row blocks per head in this workgroup
     const int per_tile = a.n_head_blocks * a.B;
     const int tile = a.n_row_tiles - 1 - (int)blockIdx.x / per_tile;
     const int rem = (int)blockIdx.x % per_tile;
@@ -63,8 +63,8 @@ __device__ __forceinline__ void attn_fwd_body(const FwdArgs &a) {
     for (int k0 = 0; k0 < kend_wg; k0 += BK) {
         __syncthreads();
         const int nvalid = min(BK, a.n_keys - k0);
-        stage_rows<DP, LW, 256>(Ks, kb + (size_t)k0 * kld, kld, BK, nvalid, a.dim, vec4, tid);
-        stage_rows_t<DP, LT, 256>(Vt, vb + (size_t)k0 * kld, kld, BK, nvalid, a.dim, vec4, tid);
+        stage_rows<DP, LW, 64 * NW>(Ks, kb + (size_t)k0 * kld, kld, BK, nvalid, a.dim, vec4, tid);
+        stage_rows_t<DP, LT, 64 * NW>(Vt, vb + (size_t)k0 * kld, kld, BK, nvalid, a.dim, vec4, tid);
         __syncthreads();
         if (k0 >= kend_w) continue;  // wave-uniform: nothing here is visible to this wave
 
@@ -140,7 +140,10 @@ __device__ __forceinline__ void attn_fwd_body(const FwdArgs &a) {
 
 #define ZT_FWD(DP, BK)                                                                             \
     extern "C" __global__ void __launch_bounds__(256) zt_fwd_d##DP##_k##BK(FwdArgs a) {          \
-        attn_fwd_body<DP, BK>(a);                                                                  \
+        attn_fwd_body<DP, BK, 4>(a);                                                               \
+    }                                                                                              \
+    extern "C" __global__ void __launch_bounds__(512) zt_fwd8_d##DP##_k##BK(FwdArgs a) {         \
+        attn_fwd_body<DP, BK, 8>(a);                                                               \
     }
 
 ZT_FWD(32, 32) ZT_FWD(32, 64)

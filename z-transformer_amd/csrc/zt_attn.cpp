@@ -84,9 +84,9 @@ DeviceState *device_state() {
 // touches another module, so no failed hipModuleGetFunction is left behind in
 // the thread's last-error slot for the caller's next HIP call to report.
 int module_of(const char *name) {
-    if (strncmp(name, "zt_fwd_", 7) == 0) return 0;
-    if (strncmp(name, "zt_bwd_", 7) == 0) return 1;
-    if (strncmp(name, "zt_dec_", 7) == 0) return 2;
+    if (strncmp(name, "zt_fwd", 6) == 0) return 0;
+    if (strncmp(name, "zt_bwd", 6) == 0) return 1;
+    if (strncmp(name, "zt_dec", 6) == 0) return 2;
     return 3;
 }
 
@@ -150,6 +150,16 @@ int key_tile(Tiled which, int dp, int max_tile) {
 // LDS per workgroup: forward = K tile + transposed V tile; dq = K and V tiles.
 size_t fwd_tile_bytes(int dp, int bk) { return ((size_t)bk * (dp + 4) + (size_t)dp * (bk + 4)) * sizeof(float); }
 size_t kv_tile_bytes(int dp, int bk) { return (size_t)2 * bk * (dp + 4) * sizeof(float); }
+
+// Waves per forward / dq workgroup (4 or 8): eight waves share each staged K/V
+// tile between twice as many query rows.  Measured on MI355X: the forward
+// gains when four query heads share a kv group (C3 1.39 -> 1.33 ms, C5 0.84 ->
+// 0.76 ms) and loses for MHA (C2); the dq kernel loses at every shape tried.
+int fwd_waves(int hw) { return env_choice("ZT_ATTN_FWD_W", hw == 4 ? 8 : 4, {4, 8}); }
+int dq_waves(int dp) {
+    const int w = env_choice("ZT_ATTN_DQ_W", 4, {4, 8});
+    return dp > 192 ? 4 : w;  // eight-wave dq spills above d = 192
+}
 size_t dkdv_bytes(int dp, int hs, int kw = 0) {
     if (kw == 0) kw = 4 / hs;
     const size_t stage = (size_t)2 * hs * 16 * (dp + 4) + (size_t)hs * 16 * 4;
@@ -247,15 +257,16 @@ int forward_impl(const float *q, const float *k, const float *v, float *out, int
     a.B = B; a.T = T; a.H = n_heads; a.Hkv = n_kv_heads; a.dim = dim;
     a.q_offset = q_offset; a.n_keys = n_keys; a.kv_rows = kv_rows;
     a.HW = heads_per_wg(n_heads / n_kv_heads);
-    const int rows_per_wg = 16 * (4 / a.HW);
+    const int nw = fwd_waves(a.HW);
+    const int rows_per_wg = 16 * (nw / a.HW);
     a.n_row_tiles = (T + rows_per_wg - 1) / rows_per_wg;
     a.n_head_blocks = n_heads / a.HW;
     a.scale_log2e = (float)(1.4426950408889634 / std::sqrt((double)dim));
     const unsigned long long blocks = (unsigned long long)a.n_row_tiles * a.n_head_blocks * B;
     if (!grid_ok(blocks)) return 1;
     char name[64];
-    snprintf(name, sizeof name, "zt_fwd_d%d_k%d", dp, bk);
-    return launch(st, name, (unsigned)blocks, a, stream);
+    snprintf(name, sizeof name, nw == 8 ? "zt_fwd8_d%d_k%d" : "zt_fwd_d%d_k%d", dp, bk);
+    return launch(st, name, (unsigned)blocks, a, stream, 64u * nw);
 }
 
 // Validates a backward call and fills the argument block and kernel names.
@@ -263,7 +274,8 @@ int forward_impl(const float *q, const float *k, const float *v, float *out, int
 int backward_prepare(const float *q, const float *k, const float *v, const float *dout, float *dq, float *dk,
                      float *dv, float *row_max, float *row_den, float *row_del, int B, int T, int n_heads,
                      int n_kv_heads, int dim, int max_tile, BwdArgs *a, DeviceState **st_out, char *name_dq,
-                     char *name_dkdv, unsigned *blocks_dq, unsigned *blocks_dkdv, unsigned *threads_dkdv) {
+                     char *name_dkdv, unsigned *blocks_dq, unsigned *blocks_dkdv, unsigned *threads_dq,
+                     unsigned *threads_dkdv) {
     if (T < 1) return refuse_T(T);
     if (!zt_attn_dim_ok(dim)) return refuse_dim(dim);
     if (check_group(n_heads, n_kv_heads)) return 1;
@@ -300,7 +312,8 @@ int backward_prepare(const float *q, const float *k, const float *v, const float
     a->row_max = row_max; a->row_den = row_den; a->row_del = row_del;
     a->B = B; a->T = T; a->H = n_heads; a->Hkv = n_kv_heads; a->dim = dim;
     a->HW = heads_per_wg(group);
-    const int rows_per_wg = 16 * (4 / a->HW);
+    const int nw_dq = dq_waves(dp);
+    const int rows_per_wg = 16 * (nw_dq / a->HW);
     a->n_row_tiles = (T + rows_per_wg - 1) / rows_per_wg;
     a->n_head_blocks = n_heads / a->HW;
     a->HS = hs;
@@ -325,7 +338,8 @@ int backward_prepare(const float *q, const float *k, const float *v, const float
     a->scale_log2e = (float)(1.4426950408889634 / std::sqrt((double)dim));
     const unsigned long long blocks_a = (unsigned long long)a->n_row_tiles * a->n_head_blocks * B;
     if (!grid_ok(blocks_a) || !grid_ok(blocks_b)) return 1;
-    snprintf(name_dq, 64, "zt_bwd_dq_d%d_k%d", dp, bk);
+    snprintf(name_dq, 64, nw_dq == 8 ? "zt_bwd_dq8_d%d_k%d" : "zt_bwd_dq_d%d_k%d", dp, bk);
+    *threads_dq = 64u * nw_dq;
     if (wide)
         snprintf(name_dkdv, 64, "zt_bwd_dkdv8_d%d_hs2", dp);
     else
@@ -344,9 +358,9 @@ int backward_impl(const float *q, const float *k, const float *v, const float *d
     BwdArgs a;
     DeviceState *st = nullptr;
     char name_a[64], name_b[64];
-    unsigned blocks_a = 0, blocks_b = 0, threads_b = kThreads;
+    unsigned blocks_a = 0, blocks_b = 0, threads_a = kThreads, threads_b = kThreads;
     if (backward_prepare(q, k, v, dout, dq, dk, dv, row_max, row_den, row_del, B, T, n_heads, n_kv_heads, dim,
-                         max_tile, &a, &st, name_a, name_b, &blocks_a, &blocks_b, &threads_b))
+                         max_tile, &a, &st, name_a, name_b, &blocks_a, &blocks_b, &threads_a, &threads_b))
         return 1;
     if ((stage & 1) && !dq) {
         fprintf(stderr, "zt_attn: a null dq is not launchable.\n");
@@ -356,7 +370,7 @@ int backward_impl(const float *q, const float *k, const float *v, const float *d
         fprintf(stderr, "zt_attn: a null dk or dv is not launchable.\n");
         return 1;
     }
-    if ((stage & 1) && launch(st, name_a, blocks_a, a, stream)) return 1;
+    if ((stage & 1) && launch(st, name_a, blocks_a, a, stream, threads_a)) return 1;
     // Same stream: the dk/dv kernel reads the row statistics the first wrote.
     if ((stage & 2) && launch(st, name_b, blocks_b, a, stream, threads_b)) return 1;
     return 0;
@@ -613,15 +627,16 @@ int zt_attn_plan(int B, int T, int n_heads, int n_kv_heads, int dim, int max_til
     const int dp = pad32(dim);
     int bk = key_tile(Tiled::Forward, dp, max_tile);
     if (fwd_tile_bytes(dp, bk) > st->lds_limit) bk = 32;
-    snprintf(fwd, len, "zt_fwd_d%d_k%d", dp, bk);
+    snprintf(fwd, len, fwd_waves(heads_per_wg(n_heads / n_kv_heads)) == 8 ? "zt_fwd8_d%d_k%d" : "zt_fwd_d%d_k%d", dp,
+             bk);
     BwdArgs a;
     DeviceState *st2 = nullptr;
-    unsigned ba = 0, bb = 0, tb = 0;
+    unsigned ba = 0, bb = 0, ta = 0, tb = 0;
     char na[64], nb[64];
     // Shape-only planning: the pointers are placeholders that are never used.
     float dummy = 0.f;
     if (backward_prepare(&dummy, &dummy, &dummy, &dummy, &dummy, &dummy, &dummy, &dummy, &dummy, &dummy, B, T,
-                         n_heads, n_kv_heads, dim, max_tile, &a, &st2, na, nb, &ba, &bb, &tb))
+                         n_heads, n_kv_heads, dim, max_tile, &a, &st2, na, nb, &ba, &bb, &ta, &tb))
         return 1;
     snprintf(dq, len, "%s", na);
     snprintf(dkdv, len, "%s", nb);
