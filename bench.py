@@ -25,6 +25,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 METRIC = "causal GQA attn fwd+bwd TFLOP/s f32 (T=4096,d=128); decode attn HBM GB/s"
 PEAK_MFMA_F32 = 157.3   # TFLOP/s, MI355X dense FP32 matrix
 PEAK_HBM = 8000.0       # GB/s, MI355X HBM3E
+THETA = 500000.0
 SEEDS = {"q": 0x5EED0001, "k": 0x5EED0002, "v": 0x5EED0003, "do": 0x5EED0004, "kc": 0x5EED0005,
          "vc": 0x5EED0006, "x": 0x5EED0007, "w": 0x5EED0008}
 
@@ -81,8 +82,8 @@ def main():
     B, T, H, Hkv, D = 1, 4096, 32, 8, 128
     q0, k0 = normal(B * T * H * D, SEEDS["q"]), normal(B * T * Hkv * D, SEEDS["k"])
     q, k = torch.empty_like(q0), torch.empty_like(k0)
-    zt.rope(q0, q, B * T, H * D, 0, 500000.0, D)
-    zt.rope(k0, k, B * T, Hkv * D, 0, 500000.0, D)
+    zt.rope(q0, q, B * T, H * D, 0, THETA, D)
+    zt.rope(k0, k, B * T, Hkv * D, 0, THETA, D)
     del q0, k0
     v, do = normal(B * T * Hkv * D, SEEDS["v"]), normal(B * T * H * D, SEEDS["do"])
     out, dq = torch.empty_like(q), torch.empty_like(q)
@@ -175,7 +176,22 @@ def main():
     dec_bytes = 2 * Bd * n_ctx * Hkv * D * 4 + 2 * Bd * H * D * 4
     dec_gbs = dec_bytes / (t_dec * 1e-3) / 1e9
     log(f"C4 decode: {t_dec * 1e3:.1f} us, {dec_gbs:.0f} GB/s ({100 * dec_gbs / PEAK_HBM:.1f}% of HBM peak)")
-    del kc, vc, qd, od, ws
+
+    # The device-resident step: RoPE on q and the new k, append at row 8191, attend.
+    kn = normal(Bd * Hkv * D, SEEDS["k"])
+    vn = normal(Bd * Hkv * D, SEEDS["v"])
+    ws2 = torch.empty(zt.decode_step_workspace_bytes(Bd, n_ctx, H, Hkv, D) // 4 + 1, device=dev)
+    pos = [n_ctx - 1] * Bd
+
+    def dec_step():
+        zt.decode_step(qd, kn, vn, kc, vc, od, pos, Bd, n_ctx, H, Hkv, D, ws2, THETA)
+
+    for _ in range(3):
+        dec_step()
+    t_step = event_time(torch, dec_step, max(10, args.steps))
+    step_gbs = dec_bytes / (t_step * 1e-3) / 1e9
+    log(f"C4 decode_step (rope + append + attention): {t_step * 1e3:.1f} us, {step_gbs:.0f} GB/s")
+    del kc, vc, qd, od, ws, kn, vn, ws2
 
     # ---------------- RMSNorm over rotating buffers ----------------
     norm = {}
@@ -220,8 +236,8 @@ def main():
         W = max(1, min(args.cpu_rows, T))
         qh = oracle.fill_normal(B * T * H * D, SEEDS["q"])
         kh = oracle.fill_normal(B * T * Hkv * D, SEEDS["k"])
-        qh = oracle.rope(qh, B * T, H * D, 0, 500000.0, D)
-        kh = oracle.rope(kh, B * T, Hkv * D, 0, 500000.0, D)
+        qh = oracle.rope(qh, B * T, H * D, 0, THETA, D)
+        kh = oracle.rope(kh, B * T, Hkv * D, 0, THETA, D)
         vh = oracle.fill_normal(B * T * Hkv * D, SEEDS["v"])
         dh = oracle.fill_normal(B * T * H * D, SEEDS["do"])
         t0 = time.perf_counter()
@@ -250,7 +266,8 @@ def main():
         "fwd_tflops": round(fwd_tflops, 3), "bwd_tflops": round(bwd_tflops, 3),
         "kernels": [{k2: (round(v2, 4) if isinstance(v2, float) else v2) for k2, v2 in kk.items()} for kk in kernels],
         "decode": {"workload": "C4 B=64 n_keys=8192 Hq=32 Hkv=8 d=128 f32", "us": round(t_dec * 1e3, 2),
-                   "GB/s": round(dec_gbs, 1), "bytes": dec_bytes, "frac_hbm": round(dec_gbs / PEAK_HBM, 4)},
+                   "GB/s": round(dec_gbs, 1), "bytes": dec_bytes, "frac_hbm": round(dec_gbs / PEAK_HBM, 4),
+                   "step_us": round(t_step * 1e3, 2), "step_GB/s": round(step_gbs, 1)},
         "rmsnorm": norm,
         "hbm_copy": {"bytes": 2 * (1 << 30), "GB/s": round(copy_gbs, 1), "frac_hbm": round(copy_gbs / PEAK_HBM, 4)},
     }

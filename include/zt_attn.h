@@ -116,6 +116,21 @@ int zt_attn_decode(const float *q, const float *k_cache, const float *v_cache, f
                    const int *n_keys, int B, int n_ctx, int n_heads, int n_kv_heads, int dim,
                    void *workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* One decode step with the KV cache resident on the device (no counterpart:
+ * the reference re-uploads the whole prefix every step, src/decode.zig:435-437).
+ * For each sequence b: RoPE (src/rope.zig:21-55, theta e.g. 500000) rotates
+ * q[b] and k_new[b] at position pos[b]; the rotated key and v_new[b] are
+ * written into cache row pos[b] (the src/kv_cache.zig:88-131 append: the cache
+ * stores post-RoPE keys); then out[b] attends the first pos[b] + 1 rows, as
+ * src/decode.zig:206-298 does per layer.  q/out [B, n_heads*dim], k_new/v_new
+ * [B, n_kv_heads*dim], caches [B, n_ctx, n_kv_heads*dim]; pos is a HOST array
+ * of B ints in [0, n_ctx) (a full cache is refused, kv_cache.zig:91).
+ * `workspace` holds zt_attn_decode_step_workspace(...) bytes. */
+size_t zt_attn_decode_step_workspace(int B, int n_ctx, int n_heads, int n_kv_heads, int dim);
+int zt_attn_decode_step(const float *q, const float *k_new, const float *v_new, float *k_cache, float *v_cache,
+                        float *out, const int *pos, int B, int n_ctx, int n_heads, int n_kv_heads, int dim,
+                        double theta, void *workspace, size_t workspace_bytes, hipStream_t stream);
+
 /* RMSNorm, src/norm.zig:18-47 on the device (the reference's src/cuda/norm.cu
  * kernel has no C entry point).  x/y [rows, cols], w [cols]; eps is
  * src/norm.zig:14's 1e-5 for the reference's behaviour.  rows == 0 launches
@@ -130,6 +145,13 @@ int zt_rmsnorm_forward(const float *x, const float *w, float *y, int rows, int c
  * (rope.zig:29). */
 int zt_rope_forward(const float *x, float *y, int rows, int cols, int pos, double theta,
                     int head_dim, hipStream_t stream);
+
+/* RoPE backward, src/autograd.zig:851-872 on the device: din = R^T dout at
+ * position pos + r (the gradient through zt_rope_forward), so an attention
+ * block's backward -- zt_attn_backward then this on dq and dk -- stays on the
+ * device.  Same layout and refusals as zt_rope_forward. */
+int zt_rope_backward(const float *dout, float *din, int rows, int cols, int pos, double theta, int head_dim,
+                     hipStream_t stream);
 
 /* Seeded synthetic inputs (splitmix64 counter stream + Box-Muller): element i
  * depends only on (seed, i).  normal: mean + sigma*z; uniform: [lo, hi). */

@@ -361,6 +361,49 @@ int zto_rope(const float *x, float *y, int rows, int cols, int pos, double theta
     return 0;
 }
 
+int zto_rope_backward(const float *dout, float *din, int rows, int cols, int pos, double theta, int head_dim) {
+    if (head_dim <= 0 || head_dim % 2 != 0) return 1;
+    if (cols % head_dim != 0) return 2;
+    const int half = head_dim / 2;
+    for (int r = 0; r < rows; ++r) {
+        const float *src = dout + (size_t)r * cols;
+        float *dst = din + (size_t)r * cols;
+        const double t = (double)(pos + r);
+        for (int h = 0; h < cols / head_dim; ++h) {
+            const int base = h * head_dim;
+            for (int i = 0; i < half; ++i) {
+                const double exponent = (double)(2 * i) / (double)head_dim; /* autograd.zig:861 */
+                const double angle = t / pow(theta, exponent);
+                const double c = cos(angle), s = sin(angle);
+                const double lo = (double)src[base + i], hi = (double)src[base + i + half];
+                dst[base + i] = (float)(lo * c + hi * s);        /* :867 */
+                dst[base + i + half] = (float)(hi * c - lo * s); /* :868 */
+            }
+        }
+    }
+    return 0;
+}
+
+int zto_decode_step(const float *q, const float *k_new, const float *v_new, float *k_cache, float *v_cache,
+                    float *out, const int *pos, int B, int n_ctx, int H, int Hkv, int D, double theta) {
+    if (!head_config_ok(H, Hkv, D) || D % 2 != 0) return 1;
+    for (int b = 0; b < B; ++b)
+        if (pos[b] < 0 || pos[b] >= n_ctx) return 2; /* kv_cache.zig:91: Full */
+    const size_t qs = (size_t)H * D, ks = (size_t)Hkv * D, cs = (size_t)n_ctx * ks;
+    float *q_pos = (float *)malloc(sizeof(float) * qs);
+    int rc = 0;
+    for (int b = 0; b < B && rc == 0; ++b) {
+        rc = zto_rope(q + b * qs, q_pos, 1, H * D, pos[b], theta, D);                                   /* decode.zig:244 */
+        if (!rc) rc = zto_rope(k_new + b * ks, k_cache + b * cs + (size_t)pos[b] * ks, 1, Hkv * D, pos[b], theta, D);
+        if (rc) break;
+        memcpy(v_cache + b * cs + (size_t)pos[b] * ks, v_new + b * ks, sizeof(float) * ks);            /* :259 */
+        const int nk = pos[b] + 1;
+        rc = zto_attn_step(q_pos, k_cache + b * cs, v_cache + b * cs, out + b * qs, &nk, 1, n_ctx, H, Hkv, D);
+    }
+    free(q_pos);
+    return rc;
+}
+
 uint64_t zto_splitmix64(uint64_t seed, uint64_t counter) {
     uint64_t z = seed + (counter + 1) * 0x9E3779B97F4A7C15ull;
     z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;

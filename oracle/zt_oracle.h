@@ -86,6 +86,17 @@ void zto_rmsnorm(const float *x, const float *w, float *y, int rows, int cols, d
  * Returns 1 on OddHeadDim, 2 on DimensionMismatch. */
 int zto_rope(const float *x, float *y, int rows, int cols, int pos, double theta, int head_dim);
 
+/* src/autograd.zig:851-872 (ropeBackward): din = R^T dout, the transposed
+ * half-split rotation at position pos + r.  Returns 1 / 2 as zto_rope. */
+int zto_rope_backward(const float *dout, float *din, int rows, int cols, int pos, double theta, int head_dim);
+
+/* One decode step per sequence, as src/decode.zig:244-270 orders it:
+ * q_pos = rope(q, pos), k_pos = rope(k_new, pos) (src/rope.zig:21-55), the
+ * cache append of (k_pos, v_new) at row pos (src/kv_cache.zig:88-95), then
+ * attnStep over pos + 1 keys.  The caches are updated in place. */
+int zto_decode_step(const float *q, const float *k_new, const float *v_new, float *k_cache, float *v_cache,
+                    float *out, const int *pos, int B, int n_ctx, int H, int Hkv, int D, double theta);
+
 /* Seeded inputs: splitmix64 counter stream -> Box-Muller.  Element i uses
  * the 64-bit outputs at counters 2i and 2i+1, so any element can be made on
  * its own.  out[i] = (float)(mean + sigma * z_i). */

@@ -32,6 +32,8 @@ def lib():
             "zto_attn_step_mt": (I, [P] * 5 + [I] * 6),
             "zto_rmsnorm": (None, [P, P, P, I, I, D]),
             "zto_rope": (I, [P, P, I, I, I, D, I]),
+            "zto_rope_backward": (I, [P, P, I, I, I, D, I]),
+            "zto_decode_step": (I, [P] * 7 + [I] * 5 + [D]),
             "zto_fill_normal": (None, [P, Z, U, D, D]),
             "zto_fill_uniform": (None, [P, Z, U, D, D]),
             "zto_splitmix64": (U, [U, U]),
@@ -129,6 +131,30 @@ def rope(x, rows, cols, pos, theta, head_dim):
     if rc:
         raise OracleRefused(rc)
     return y
+
+
+def rope_backward(dout, rows, cols, pos, theta, head_dim):
+    """src/autograd.zig:851-872."""
+    dout = _f32(dout)
+    din = np.zeros(rows * cols, np.float32)
+    rc = lib().zto_rope_backward(_p(dout), _p(din), rows, cols, pos, theta, head_dim)
+    if rc:
+        raise OracleRefused(rc)
+    return din
+
+
+def decode_step(q, k_new, v_new, k_cache, v_cache, pos, B, n_ctx, H, Hkv, D, theta=500000.0):
+    """src/decode.zig:244-270; returns (out, k_cache, v_cache) with the caches updated."""
+    q, k_new, v_new = _f32(q), _f32(k_new), _f32(v_new)
+    kc = np.array(k_cache, dtype=np.float32, copy=True).ravel()
+    vc = np.array(v_cache, dtype=np.float32, copy=True).ravel()
+    p = np.ascontiguousarray(pos, dtype=np.int32)
+    out = np.zeros(B * H * D, np.float32)
+    rc = lib().zto_decode_step(_p(q), _p(k_new), _p(v_new), _p(kc), _p(vc), _p(out), _p(p), B, n_ctx, H, Hkv, D,
+                               theta)
+    if rc:
+        raise OracleRefused(rc)
+    return out, kc, vc
 
 
 def fill_normal(n, seed, mean=0.0, sigma=1.0):

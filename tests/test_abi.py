@@ -137,11 +137,47 @@ def test_decode_refusals(zt, capfd):
     assert L.zt_attn_decode_workspace(0, 8, 4, 2, 32) == 0
 
 
-def test_rope_refusals(zt):
+def test_decode_refuses_misaligned_rows(zt, capfd):
+    # dim % 4 == 0 rows are read 16 bytes at a time; dim % 4 == 2 rows 8 at a time.
     L = zt.lib()
-    assert L.zt_rope_forward(NULL, NULL, 1, 3, 0, 5e5, 3, NULL) == 1
-    assert L.zt_rope_forward(NULL, NULL, 1, 6, 0, 5e5, 4, NULL) == 1
-    assert L.zt_rope_forward(NULL, NULL, 1, 0, 0, 5e5, 0, NULL) == 1
+    nk = (ctypes.c_int * 2)(5, 8)
+    ws = L.zt_attn_decode_workspace(2, 8, 4, 2, 32)
+    good, off8 = 0x10000, 0x10008
+    assert L.zt_attn_decode(good, off8, good, good, nk, 2, 8, 4, 2, 32, good, ws, NULL) == 1
+    assert "not 16-byte aligned" in capfd.readouterr().err
+    ws34 = L.zt_attn_decode_workspace(2, 8, 4, 2, 34)
+    assert L.zt_attn_decode(good, good, good, 0x10004, nk, 2, 8, 4, 2, 34, good, ws34, NULL) == 1
+    assert "not 8-byte aligned" in capfd.readouterr().err
+
+
+def test_decode_step_refusals(zt, capfd):
+    L = zt.lib()
+    B, n_ctx, H, Hkv, D = 2, 8, 4, 2, 32
+    ws = L.zt_attn_decode_step_workspace(B, n_ctx, H, Hkv, D)
+    assert ws >= L.zt_attn_decode_workspace(B, n_ctx, H, Hkv, D) + B * H * D * 4
+    p = 0x10000
+
+    def step(pos, theta=5e5, wsb=ws, kc=p, dim=D):
+        arr = (ctypes.c_int * B)(*pos)
+        return L.zt_attn_decode_step(p, p, p, kc, p, p, arr, B, n_ctx, H, Hkv, dim, ctypes.c_double(theta), p, wsb,
+                                     NULL)
+
+    assert step([3, 8]) == 1 and "position 8, outside the 8-row cache" in capfd.readouterr().err
+    assert step([-1, 0]) == 1 and "position -1" in capfd.readouterr().err
+    assert step([1, 2], theta=0.0) == 1 and "theta" in capfd.readouterr().err
+    assert step([1, 2], wsb=ws - 1) == 1 and "workspace" in capfd.readouterr().err
+    assert step([1, 2], kc=p + 8) == 1 and "aligned" in capfd.readouterr().err
+    assert step([1, 2], dim=31) == 1 and "head_dim 31" in capfd.readouterr().err
+    assert L.zt_attn_decode_step_workspace(0, n_ctx, H, Hkv, D) == 0
+
+
+@pytest.mark.parametrize("fn", ["zt_rope_forward", "zt_rope_backward"])
+def test_rope_refusals(zt, fn):
+    f = getattr(zt.lib(), fn)
+    assert f(NULL, NULL, 1, 3, 0, 5e5, 3, NULL) == 1
+    assert f(NULL, NULL, 1, 6, 0, 5e5, 4, NULL) == 1
+    assert f(NULL, NULL, 1, 0, 0, 5e5, 0, NULL) == 1
+    assert f(NULL, NULL, 0, 8, 0, 5e5, 4, NULL) == 0  # zero rows: nothing to launch
 
 
 # ------------------------------------------- holder (src/cuda/device.zig) --

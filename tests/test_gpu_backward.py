@@ -146,3 +146,23 @@ def test_backward_gate_catches_broken_references(gpu, zt, oracle):
         assert worst(attention_backward_f64(q, k, v, do, T, H, Hkv, D, variant)) > BWD_REL, variant
     # no_jacobian leaves dv untouched, as the reference's variant 3 does.
     assert rel_err(dv, attention_backward_f64(q, k, v, do, T, H, Hkv, D, "no_jacobian")[2]) <= BWD_REL
+
+
+@pytest.mark.parametrize("T,H,Hkv,D", [(96, 8, 2, 64), (40, 4, 4, 128), (17, 6, 3, 34)])
+def test_block_backward_through_rope_on_the_device(gpu, zt, oracle, threads, T, H, Hkv, D):
+    # blockBackward's attention segment (src/autograd.zig:559-569): attention
+    # backward on the rotated q, k, then ropeBackward at position 0 takes dq, dk
+    # back to the unrotated projections.  Both halves run on the device here.
+    (q, k, v, do), (dq, dk, dv, _, _, _) = _run(gpu, zt, 1, T, H, Hkv, D, rope=True)
+    dq_in, dk_in = gpu.empty(T * H * D, device="cuda"), gpu.empty(T * Hkv * D, device="cuda")
+    zt.rope_backward(gpu.from_numpy(dq).cuda(), dq_in, T, H * D, 0, THETA, D)
+    zt.rope_backward(gpu.from_numpy(dk).cuda(), dk_in, T, Hkv * D, 0, THETA, D)
+    gpu.cuda.synchronize()
+    rq, rk, rv = oracle.attention_backward(q, k, v, do, 1, T, H, Hkv, D, threads=threads)
+    want_q = oracle.rope_backward(rq, T, H * D, 0, THETA, D)
+    want_k = oracle.rope_backward(rk, T, Hkv * D, 0, THETA, D)
+    assert rel_err(host(dq_in), want_q) <= BWD_REL
+    assert rel_err(host(dk_in), want_k) <= BWD_REL
+    assert rel_err(dv, rv) <= BWD_REL
+    # The gradient before ropeBackward is not the answer (rows t > 0 rotate).
+    assert rel_err(dq, want_q) > 10 * BWD_REL

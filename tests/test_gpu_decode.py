@@ -1,11 +1,12 @@
-"""Decode-step parity on the GPU: zt_attn_decode (split-K) and the reference's
+"""Decode-step parity on the GPU: zt_attn_decode (split-K), the reference's
 own decode route (zt_attn_forward with T = 1, q_offset = n_keys - 1,
-src/decode.zig:462) against the CPU restatement of src/decode.zig:326-392,
-max |diff| <= 1e-4."""
+src/decode.zig:462) and zt_attn_decode_step (RoPE + device cache append +
+attention, src/decode.zig:244-270) against the CPU restatement of
+src/decode.zig:326-392, max |diff| <= 1e-4."""
 import numpy as np
 import pytest
 
-from gpuhelp import FWD_TOL, SEED_KC, SEED_Q, SEED_VC, dev_normal, host, max_abs
+from gpuhelp import FWD_TOL, SEED_K, SEED_KC, SEED_Q, SEED_V, SEED_VC, THETA, dev_normal, host, max_abs
 
 pytestmark = pytest.mark.gpu
 
@@ -80,3 +81,87 @@ def test_decode_refuses_bad_n_keys(gpu, zt):
     for bad in ([0, 5], [5, 17], [-1, 3]):
         with pytest.raises(zt.ZtRefused):
             zt.decode(q, kc, kc, out, bad, B, n_ctx, H, Hkv, D, ws)
+
+
+def _step_ws(gpu, zt, B, n_ctx, H, Hkv, D):
+    return gpu.empty(zt.decode_step_workspace_bytes(B, n_ctx, H, Hkv, D) // 4 + 1, device="cuda")
+
+
+def _same_rows(dev, ref, tol):
+    # Unwritten rows stay NaN on both sides; written rows agree to tol.
+    dev, ref = np.asarray(dev), np.asarray(ref)
+    assert np.array_equal(np.isnan(dev), np.isnan(ref))
+    ok = ~np.isnan(ref)
+    assert max_abs(dev[ok], ref[ok]) <= tol
+
+
+@pytest.mark.parametrize("B,n_ctx,H,Hkv,D,start,steps", [
+    (3, 40, 8, 2, 64, [0, 5, 17], 12),
+    (2, 24, 6, 3, 34, [0, 9], 15),
+    (1, 16, 4, 1, 256, [3], 13),
+    (70, 12, 4, 2, 32, None, 3),
+])
+def test_decode_step_fills_a_device_cache(gpu, zt, oracle, B, n_ctx, H, Hkv, D, start, steps):
+    # Rows below each sequence's start hold an earlier history; rows from the
+    # start on are NaN, so a row the step did not write, or one past pos that
+    # the attention read, would show.  Sequences sit at ragged positions.
+    start = start or [int(x) for x in np.random.default_rng(B).integers(0, n_ctx - steps + 1, size=B)]
+    rng = np.random.default_rng(n_ctx * 7 + D)
+    kh = np.full((B, n_ctx, Hkv * D), np.nan, np.float32)
+    vh = np.full((B, n_ctx, Hkv * D), np.nan, np.float32)
+    for b, p0 in enumerate(start):
+        kh[b, :p0] = rng.standard_normal((p0, Hkv * D))
+        vh[b, :p0] = rng.standard_normal((p0, Hkv * D))
+    kh, vh = kh.ravel(), vh.ravel()
+    kc, vc = gpu.from_numpy(kh.copy()).cuda(), gpu.from_numpy(vh.copy()).cuda()
+    ws = _step_ws(gpu, zt, B, n_ctx, H, Hkv, D)
+    for s in range(steps):
+        q = dev_normal(gpu, zt, B * H * D, SEED_Q + 0x100 * s)
+        k = dev_normal(gpu, zt, B * Hkv * D, SEED_K + 0x100 * s)
+        v = dev_normal(gpu, zt, B * Hkv * D, SEED_V + 0x100 * s)
+        out = gpu.full((B * H * D,), float("nan"), device="cuda")
+        pos = [p + s for p in start]
+        zt.decode_step(q, k, v, kc, vc, out, pos, B, n_ctx, H, Hkv, D, ws, THETA)
+        gpu.cuda.synchronize()
+        ref, kh, vh = oracle.decode_step(host(q), host(k), host(v), kh, vh, pos, B, n_ctx, H, Hkv, D, THETA)
+        assert max_abs(host(out), ref) <= FWD_TOL, (s, pos)
+    _same_rows(host(kc), kh, 2e-6)
+    _same_rows(host(vc), vh, 0.0)
+
+
+def test_decode_step_at_the_c4_shape(gpu, zt, oracle, threads):
+    # C4's cache (n_ctx 8192, 32 heads over 8, d 128) with 16 sequences at
+    # ragged positions up to the last row; the expectation composes the pinned
+    # restatements: rope on q and k at pos, the append, attnStep over pos + 1.
+    B, n_ctx, H, Hkv, D = 16, 8192, 32, 8, 128
+    pos = [n_ctx - 1] * 4 + [int(x) for x in np.random.default_rng(4).integers(0, n_ctx, size=B - 4)]
+    kc = dev_normal(gpu, zt, B * n_ctx * Hkv * D, SEED_KC)
+    vc = dev_normal(gpu, zt, B * n_ctx * Hkv * D, SEED_VC)
+    kh, vh = host(kc).reshape(B, n_ctx, Hkv * D), host(vc).reshape(B, n_ctx, Hkv * D)
+    q = dev_normal(gpu, zt, B * H * D, SEED_Q)
+    k = dev_normal(gpu, zt, B * Hkv * D, SEED_K)
+    v = dev_normal(gpu, zt, B * Hkv * D, SEED_V)
+    out = gpu.full((B * H * D,), float("nan"), device="cuda")
+    zt.decode_step(q, k, v, kc, vc, out, pos, B, n_ctx, H, Hkv, D, _step_ws(gpu, zt, B, n_ctx, H, Hkv, D), THETA)
+    gpu.cuda.synchronize()
+    qh, knh, vnh = host(q).reshape(B, H * D), host(k).reshape(B, Hkv * D), host(v).reshape(B, Hkv * D)
+    qr = np.stack([oracle.rope(qh[b], 1, H * D, pos[b], THETA, D) for b in range(B)])
+    for b in range(B):
+        kh[b, pos[b]] = oracle.rope(knh[b], 1, Hkv * D, pos[b], THETA, D)
+        vh[b, pos[b]] = vnh[b]
+    ref = oracle.attn_step(qr, kh, vh, [p + 1 for p in pos], B, n_ctx, H, Hkv, D, threads=threads)
+    assert max_abs(host(out), ref) <= FWD_TOL
+    assert max_abs(host(kc), kh.ravel()) <= 2e-6
+    assert np.array_equal(host(vc), vh.ravel())
+
+
+def test_decode_step_refuses_a_full_cache_and_writes_nothing(gpu, zt):
+    B, n_ctx, H, Hkv, D = 2, 8, 4, 2, 32
+    kc = gpu.zeros(B * n_ctx * Hkv * D, device="cuda")
+    vc = gpu.zeros(B * n_ctx * Hkv * D, device="cuda")
+    q, k = gpu.ones(B * H * D, device="cuda"), gpu.ones(B * Hkv * D, device="cuda")
+    out = gpu.zeros(B * H * D, device="cuda")
+    with pytest.raises(zt.ZtRefused):
+        zt.decode_step(q, k, k, kc, vc, out, [7, 8], B, n_ctx, H, Hkv, D, _step_ws(gpu, zt, B, n_ctx, H, Hkv, D))
+    gpu.cuda.synchronize()
+    assert float(kc.abs().sum()) == 0.0 and float(vc.abs().sum()) == 0.0 and float(out.abs().sum()) == 0.0

@@ -1,5 +1,5 @@
-"""RMSNorm (src/norm.zig:18-47) and RoPE (src/rope.zig:21-55) on the GPU
-against the CPU restatement.  RMSNorm gate: the reference kernel's 1e-5
+"""RMSNorm (src/norm.zig:18-47), RoPE (src/rope.zig:21-55) and its backward
+(src/autograd.zig:851-872) on the GPU against the CPU restatement.  RMSNorm gate: the reference kernel's 1e-5
 absolute (src/cuda/norm.cu:56); the f64 sum of squares differs from the
 reference's sequential sum only in association, so nearly every element is
 bit-identical."""
@@ -73,6 +73,20 @@ def test_rope_matches_twin(gpu, zt, oracle, rows, heads, hd, pos):
     gpu.cuda.synchronize()
     ref = oracle.rope(host(x), rows, cols, pos, THETA, hd)
     assert max_abs(host(y), ref) <= 2e-6
+
+
+@pytest.mark.parametrize("rows,heads,hd,pos", [(1, 32, 128, 8191), (64, 8, 64, 0), (33, 3, 34, 17), (7, 2, 256, 1000)])
+def test_rope_backward_matches_twin(gpu, zt, oracle, rows, heads, hd, pos):
+    # src/autograd.zig:851-872 on the device.
+    cols = heads * hd
+    x = dev_normal(gpu, zt, rows * cols, SEED_X)
+    y = gpu.full((rows * cols,), float("nan"), device="cuda")
+    zt.rope_backward(x, y, rows, cols, pos, THETA, hd)
+    gpu.cuda.synchronize()
+    ref = oracle.rope_backward(host(x), rows, cols, pos, THETA, hd)
+    assert max_abs(host(y), ref) <= 2e-6
+    if pos + rows > 1:  # the forward rotation is not the answer
+        assert max_abs(host(y), oracle.rope(host(x), rows, cols, pos, THETA, hd)) > 1e-3
 
 
 def test_rope_reference_known_answers(gpu, zt, golden):

@@ -278,6 +278,85 @@ def test_rope_reference_known_answers(oracle, golden):
             oracle.rope(np.ones(cols), 1, cols, 0, theta, hd)
 
 
+def _rotation_matrix(oracle, cols, pos, theta, head_dim):
+    # Columns of R are rope applied to the basis vectors: with one non-zero
+    # input, each output is a single f32-narrowed cos or sin, so R is exact to
+    # f32 rounding and independent of how rope_backward is written.
+    return np.stack([oracle.rope(np.eye(cols, dtype=np.float32)[j], 1, cols, pos, theta, head_dim)
+                     for j in range(cols)], axis=1).astype(np.float64)
+
+
+@pytest.mark.parametrize("cols,head_dim,pos", [(8, 8, 0), (8, 8, 3), (24, 8, 17), (64, 32, 1000), (12, 4, 9)])
+def test_rope_backward_is_the_transpose_of_rope(oracle, cols, head_dim, pos):
+    # src/autograd.zig:851-872: din = R^T dout, R the rotation rope applies.
+    theta = 500000.0
+    R = _rotation_matrix(oracle, cols, pos, theta, head_dim)
+    rng = np.random.default_rng(cols * 100 + pos)
+    y = _rand(rng, cols)
+    din = oracle.rope_backward(y, 1, cols, pos, theta, head_dim).astype(np.float64)
+    assert np.max(np.abs(din - R.T @ y.astype(np.float64))) <= 2e-6
+    if pos > 0:  # the forward rotation itself is not the answer (a sign slip would be)
+        assert np.max(np.abs(din - R @ y.astype(np.float64))) > 1e-3
+    # R orthogonal: backward undoes forward up to two f32 roundings.
+    x = _rand(rng, cols)
+    back = oracle.rope_backward(oracle.rope(x, 1, cols, pos, theta, head_dim), 1, cols, pos, theta, head_dim)
+    assert np.max(np.abs(back - x)) <= 1e-6
+
+
+def test_rope_backward_rows_advance_the_position(oracle):
+    rows, cols, hd, theta = 5, 16, 8, 10000.0
+    rng = np.random.default_rng(7)
+    dout = _rand(rng, rows, cols)
+    din = oracle.rope_backward(dout, rows, cols, 4, theta, hd).reshape(rows, cols)
+    for r in range(rows):
+        one = oracle.rope_backward(dout[r], 1, cols, 4 + r, theta, hd)
+        assert np.array_equal(din[r], one)
+    # Position 0: every angle is 0, so the gradient passes through unchanged.
+    assert np.array_equal(oracle.rope_backward(dout[0], 1, cols, 0, theta, hd), dout[0])
+
+
+def test_rope_backward_refusals(oracle):
+    with pytest.raises(oracle.OracleRefused):
+        oracle.rope_backward(np.ones(6), 1, 6, 0, 5e5, 3)
+    with pytest.raises(oracle.OracleRefused):
+        oracle.rope_backward(np.ones(6), 1, 6, 0, 5e5, 4)
+
+
+# ------------------------------------------------------------ decode step --
+
+@pytest.mark.parametrize("B,T,H,Hkv,D", [(2, 12, 4, 2, 32), (1, 9, 6, 3, 34), (3, 5, 2, 1, 64)])
+def test_decode_step_sequence_equals_the_causal_forward(oracle, B, T, H, Hkv, D):
+    # src/decode_test.zig:222-330: decoding a sequence token by token through a
+    # filling cache agrees with the full causal forward over rotated q and k.
+    theta = 500000.0
+    rng = np.random.default_rng(B * 100 + T)
+    q, k, v = _rand(rng, B, T, H * D), _rand(rng, B, T, Hkv * D), _rand(rng, B, T, Hkv * D)
+    kc = np.zeros((B, T, Hkv * D), np.float32)
+    vc = np.zeros((B, T, Hkv * D), np.float32)
+    outs = []
+    for t in range(T):
+        out, kc, vc = oracle.decode_step(q[:, t], k[:, t], v[:, t], kc, vc, [t] * B, B, T, H, Hkv, D, theta)
+        outs.append(out.reshape(B, H * D))
+    dec = np.stack(outs, axis=1)
+    qr = np.stack([oracle.rope(q[b], T, H * D, 0, theta, D) for b in range(B)])
+    kr = np.stack([oracle.rope(k[b], T, Hkv * D, 0, theta, D) for b in range(B)])
+    full = oracle.attention_forward(qr, kr, v, B, T, H, Hkv, D).reshape(B, T, H * D)
+    assert np.max(np.abs(dec - full)) <= 1e-5
+    assert np.array_equal(kc.reshape(B, T, -1), kr.reshape(B, T, -1))
+    assert np.array_equal(vc.reshape(B, T, -1), v)
+    # Unrotated keys would not agree: the check sees a missed rotation.
+    wrong = oracle.attention_forward(qr, k, v, B, T, H, Hkv, D).reshape(B, T, H * D)
+    assert np.max(np.abs(dec - wrong)) > 1e-3
+
+
+def test_decode_step_refuses_a_full_cache(oracle):
+    z = np.zeros(64, np.float32)
+    with pytest.raises(oracle.OracleRefused):
+        oracle.decode_step(z[:64], z[:32], z[:32], np.zeros(4 * 32), np.zeros(4 * 32), [4], 1, 4, 2, 1, 32)
+    with pytest.raises(oracle.OracleRefused):
+        oracle.decode_step(z[:64], z[:32], z[:32], np.zeros(4 * 32), np.zeros(4 * 32), [-1], 1, 4, 2, 1, 32)
+
+
 # ------------------------------------------------------------- generators --
 
 def test_generators_are_seeded_and_well_formed(oracle):

@@ -62,3 +62,16 @@ struct FillArgs {
     unsigned long long n, seed;
     double p0, p1;  // normal: mean, sigma; uniform: lo, hi
 };
+
+// One decode step's cache update: RoPE on q and the new k at each sequence's
+// position, the rotated k and the new v written into cache row pos[b].
+struct AppendArgs {
+    const float *q;      // [B, H*dim]   this step's query (before RoPE)
+    const float *k;      // [B, Hkv*dim] this step's key (before RoPE)
+    const float *v;      // [B, Hkv*dim]
+    float *q_pos;        // [B, H*dim]   rotated query
+    float *kc, *vc;      // [B, n_ctx, Hkv*dim] caches
+    int pos[ZT_DEC_MAXB];
+    int b_base, nb, n_ctx, H, Hkv, dim;
+    double theta;
+};

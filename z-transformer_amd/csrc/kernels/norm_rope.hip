@@ -93,6 +93,28 @@ ZT_RMS(16)
 extern "C" __global__ void __launch_bounds__(256) zt_rmsnorm_any(NormArgs a) { rms_any(a); }
 
 
+// Transposed rotation, src/autograd.zig:851-872: (lo c + hi s, hi c - lo s).
+extern "C" __global__ void __launch_bounds__(256) zt_rope_bwd(RopeArgs a) {
+    const int half = a.head_dim / 2;
+    const int heads = a.cols / a.head_dim;
+    const long long total = (long long)a.rows * heads * half;
+    for (long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+         e += (long long)gridDim.x * blockDim.x) {
+        const int i = (int)(e % half);
+        const long long rh = e / half;
+        const int h = (int)(rh % heads);
+        const int r = (int)(rh / heads);
+        const double t = (double)(a.pos + r);
+        const double exponent = (double)(2 * i) / (double)a.head_dim;
+        const double angle = t / pow(a.theta, exponent);
+        const double c = cos(angle), s = sin(angle);
+        const size_t base = (size_t)r * a.cols + (size_t)h * a.head_dim;
+        const double lo = (double)a.x[base + i], hi = (double)a.x[base + i + half];
+        a.y[base + i] = (float)(lo * c + hi * s);
+        a.y[base + i + half] = (float)(hi * c - lo * s);
+    }
+}
+
 extern "C" __global__ void __launch_bounds__(256) zt_rope(RopeArgs a) {
     const int half = a.head_dim / 2;
     const int heads = a.cols / a.head_dim;
@@ -114,6 +136,56 @@ extern "C" __global__ void __launch_bounds__(256) zt_rope(RopeArgs a) {
     }
 }
 
+
+// RoPE rotation of the pair (lo, hi) = (x[i], x[i + d/2]) at position t, as
+// src/rope.zig:37-50: f64 angle t / theta^(2i/d), f64 multiply-adds.
+DEVI void rope_pair(double t, int i, int head_dim, double theta, float lo_in, float hi_in, float *lo_out,
+                    float *hi_out) {
+    const double exponent = (double)(2 * i) / (double)head_dim;
+    const double angle = t / pow(theta, exponent);
+    const double c = cos(angle), s = sin(angle);
+    const double lo = (double)lo_in, hi = (double)hi_in;
+    *lo_out = (float)(lo * c - hi * s);
+    *hi_out = (float)(hi * c + lo * s);
+}
+
+// Decode-step cache update, one thread per element task: rotated q pairs,
+// rotated k pairs written to cache row pos[b], v elements copied to row pos[b]
+// (src/decode.zig:244-259: rope.forward on q and k at pos, cache append).
+extern "C" __global__ void __launch_bounds__(256) zt_rope_append(AppendArgs a) {
+    const int half = a.dim / 2;
+    const long long nq = (long long)a.nb * a.H * half;
+    const long long nk = (long long)a.nb * a.Hkv * half;
+    const long long nv = (long long)a.nb * a.Hkv * a.dim;
+    const size_t qld = (size_t)a.H * a.dim, kld = (size_t)a.Hkv * a.dim;
+    for (long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x; e < nq + nk + nv;
+         e += (long long)gridDim.x * blockDim.x) {
+        if (e < nq) {
+            const int i = (int)(e % half);
+            const long long bh = e / half;
+            const int h = (int)(bh % a.H), bl = (int)(bh / a.H);
+            const size_t o = (size_t)(a.b_base + bl) * qld + (size_t)h * a.dim;
+            rope_pair((double)a.pos[bl], i, a.dim, a.theta, a.q[o + i], a.q[o + i + half], &a.q_pos[o + i],
+                      &a.q_pos[o + i + half]);
+        } else if (e < nq + nk) {
+            const long long f = e - nq;
+            const int i = (int)(f % half);
+            const long long bh = f / half;
+            const int h = (int)(bh % a.Hkv), bl = (int)(bh / a.Hkv);
+            const int b = a.b_base + bl;
+            const size_t src = (size_t)b * kld + (size_t)h * a.dim;
+            const size_t dst = ((size_t)b * a.n_ctx + a.pos[bl]) * kld + (size_t)h * a.dim;
+            rope_pair((double)a.pos[bl], i, a.dim, a.theta, a.k[src + i], a.k[src + i + half], &a.kc[dst + i],
+                      &a.kc[dst + i + half]);
+        } else {
+            const long long f = e - nq - nk;
+            const int c = (int)(f % kld);
+            const int bl = (int)(f / kld);
+            const int b = a.b_base + bl;
+            a.vc[((size_t)b * a.n_ctx + a.pos[bl]) * kld + c] = a.v[(size_t)b * kld + c];
+        }
+    }
+}
 
 DEVI unsigned long long splitmix64(unsigned long long seed, unsigned long long ctr) {
     unsigned long long z = seed + (ctr + 1ull) * 0x9E3779B97F4A7C15ull;

@@ -21,6 +21,7 @@
 #include <mutex>
 #include <string>
 #include <unordered_map>
+#include <vector>
 
 #include "../../include/zt_attn.h"
 #include "kernels/args.h"
@@ -217,6 +218,20 @@ bool grid_ok(unsigned long long blocks) {
     return true;
 }
 
+// Rows are read with 16-byte vector loads when dim % 4 == 0 and with 8-byte
+// loads otherwise, so every tensor base (null ones aside) must be aligned to that.
+static bool rows_aligned(int dim, std::initializer_list<const void *> ptrs) {
+    const uintptr_t mask = (dim & 3) == 0 ? 15 : 7;
+    for (const void *p : ptrs) {
+        if (p && ((uintptr_t)p & mask)) {
+            fprintf(stderr, "zt_attn: tensor at %p is not %d-byte aligned, as head_dim %d rows need.\n", p,
+                    (int)mask + 1, dim);
+            return false;
+        }
+    }
+    return true;
+}
+
 int forward_impl(const float *q, const float *k, const float *v, float *out, int B, int T, int n_heads,
                  int n_kv_heads, int dim, int group_q, int max_tile, int q_offset, int n_keys, int kv_rows,
                  hipStream_t stream) {
@@ -252,6 +267,7 @@ int forward_impl(const float *q, const float *k, const float *v, float *out, int
         fprintf(stderr, "zt_attn: a null tensor pointer is not launchable.\n");
         return 1;
     }
+    if (!rows_aligned(dim, {q, k, v, out})) return 1;
     FwdArgs a{};
     a.q = q; a.k = k; a.v = v; a.out = out;
     a.B = B; a.T = T; a.H = n_heads; a.Hkv = n_kv_heads; a.dim = dim;
@@ -306,6 +322,7 @@ int backward_prepare(const float *q, const float *k, const float *v, const float
         fprintf(stderr, "zt_attn: a null tensor pointer is not launchable.\n");
         return 1;
     }
+    if (!rows_aligned(dim, {q, k, v, dout, dq, dk, dv})) return 1;
     *a = BwdArgs{};
     a->q = q; a->k = k; a->v = v; a->dout = dout;
     a->dq = dq; a->dk = dk; a->dv = dv;
@@ -471,6 +488,8 @@ int zt_attn_bwd_dkdv(const float *q, const float *k, const float *v, const float
                          const_cast<float *>(row_del), B, T, n_heads, n_kv_heads, dim, 64, 2, stream);
 }
 
+static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
 size_t zt_attn_decode_workspace(int B, int n_ctx, int n_heads, int n_kv_heads, int dim) {
     if (B < 1 || n_ctx < 1 || !zt_attn_dim_ok(dim) || n_heads <= 0 || n_kv_heads <= 0 ||
         n_heads % n_kv_heads != 0)
@@ -508,6 +527,7 @@ int zt_attn_decode(const float *q, const float *k_cache, const float *v_cache, f
         fprintf(stderr, "zt_attn: a null tensor pointer is not launchable.\n");
         return 1;
     }
+    if (!rows_aligned(dim, {q, k_cache, v_cache, out})) return 1;
     DeviceState *st = require_device();
     if (!st) return 1;
     const DecGeom g = decode_geom(B, n_ctx, n_heads, n_kv_heads, dim);
@@ -530,6 +550,70 @@ int zt_attn_decode(const float *q, const float *k_cache, const float *v_cache, f
         if (launch(st, "zt_dec_combine", (unsigned)(a.nb * n_heads), a, stream)) return 1;
     }
     return 0;
+}
+
+size_t zt_attn_decode_step_workspace(int B, int n_ctx, int n_heads, int n_kv_heads, int dim) {
+    const size_t dec = zt_attn_decode_workspace(B, n_ctx, n_heads, n_kv_heads, dim);
+    if (dec == 0) return 0;
+    return align256(dec) + (size_t)B * n_heads * dim * sizeof(float);  // + the rotated queries
+}
+
+int zt_attn_decode_step(const float *q, const float *k_new, const float *v_new, float *k_cache, float *v_cache,
+                        float *out, const int *pos, int B, int n_ctx, int n_heads, int n_kv_heads, int dim,
+                        double theta, void *workspace, size_t workspace_bytes, hipStream_t stream) {
+    if (B < 1 || n_ctx < 1) {
+        fprintf(stderr, "zt_attn: decode over %d sequences of %d cached rows is not launchable.\n", B, n_ctx);
+        return 1;
+    }
+    if (!zt_attn_dim_ok(dim)) return refuse_dim(dim);
+    if (check_group(n_heads, n_kv_heads)) return 1;
+    if (!pos) {
+        fprintf(stderr, "zt_attn: decode_step needs the host pos array.\n");
+        return 1;
+    }
+    for (int b = 0; b < B; ++b) {
+        if (pos[b] < 0 || pos[b] >= n_ctx) {  // src/kv_cache.zig:88-95: a full cache refuses
+            fprintf(stderr, "zt_attn: sequence %d appends at position %d, outside the %d-row cache.\n", b, pos[b],
+                    n_ctx);
+            return 1;
+        }
+    }
+    if (!(theta > 0.0)) {
+        fprintf(stderr, "zt_attn: RoPE theta %g is not usable.\n", theta);
+        return 1;
+    }
+    const size_t need = zt_attn_decode_step_workspace(B, n_ctx, n_heads, n_kv_heads, dim);
+    if (!workspace || workspace_bytes < need) {
+        fprintf(stderr, "zt_attn: decode_step workspace of %zu bytes is short of the %zu needed.\n",
+                workspace_bytes, need);
+        return 1;
+    }
+    if (!q || !k_new || !v_new || !k_cache || !v_cache || !out) {
+        fprintf(stderr, "zt_attn: a null tensor pointer is not launchable.\n");
+        return 1;
+    }
+    if (!rows_aligned(dim, {k_cache, v_cache, out})) return 1;
+    DeviceState *st = require_device();
+    if (!st) return 1;
+    const size_t dec_bytes = zt_attn_decode_workspace(B, n_ctx, n_heads, n_kv_heads, dim);
+    float *q_pos = reinterpret_cast<float *>(static_cast<char *>(workspace) + align256(dec_bytes));
+    AppendArgs ap{};
+    ap.q = q; ap.k = k_new; ap.v = v_new; ap.q_pos = q_pos; ap.kc = k_cache; ap.vc = v_cache;
+    ap.n_ctx = n_ctx; ap.H = n_heads; ap.Hkv = n_kv_heads; ap.dim = dim; ap.theta = theta;
+    std::vector<int> n_keys(B);
+    for (int b0 = 0; b0 < B; b0 += ZT_DEC_MAXB) {
+        ap.b_base = b0;
+        ap.nb = B - b0 < ZT_DEC_MAXB ? B - b0 : ZT_DEC_MAXB;
+        for (int i = 0; i < ap.nb; ++i) ap.pos[i] = pos[b0 + i];
+        const long long work = (long long)ap.nb * (n_heads + 2 * n_kv_heads) * dim;
+        long long blocks = (work + kThreads - 1) / kThreads;
+        if (blocks > 65536) blocks = 65536;
+        if (launch(st, "zt_rope_append", (unsigned)blocks, ap, stream)) return 1;
+    }
+    for (int b = 0; b < B; ++b) n_keys[b] = pos[b] + 1;
+    // Same stream: the attention reads the rows and the rotated queries just written.
+    return zt_attn_decode(q_pos, k_cache, v_cache, out, n_keys.data(), B, n_ctx, n_heads, n_kv_heads, dim,
+                          workspace, dec_bytes, stream);
 }
 
 int zt_rmsnorm_forward(const float *x, const float *w, float *y, int rows, int cols, double eps,
@@ -563,8 +647,8 @@ int zt_rmsnorm_forward(const float *x, const float *w, float *y, int rows, int c
     return launch(st, name, (unsigned)rows, a, stream);
 }
 
-int zt_rope_forward(const float *x, float *y, int rows, int cols, int pos, double theta, int head_dim,
-                    hipStream_t stream) {
+static int rope_impl(const char *name, const float *x, float *y, int rows, int cols, int pos, double theta,
+                     int head_dim, hipStream_t stream) {
     if (head_dim <= 0 || head_dim % 2 != 0) {
         fprintf(stderr, "zt_rope: head_dim %d is odd or not positive.\n", head_dim);
         return 1;
@@ -588,7 +672,17 @@ int zt_rope_forward(const float *x, float *y, int rows, int cols, int pos, doubl
     RopeArgs a{x, y, rows, cols, pos, head_dim, theta};
     long long blocks = (work + kThreads - 1) / kThreads;
     if (blocks > 65536) blocks = 65536;
-    return launch(st, "zt_rope", (unsigned)blocks, a, stream);
+    return launch(st, name, (unsigned)blocks, a, stream);
+}
+
+int zt_rope_forward(const float *x, float *y, int rows, int cols, int pos, double theta, int head_dim,
+                    hipStream_t stream) {
+    return rope_impl("zt_rope", x, y, rows, cols, pos, theta, head_dim, stream);
+}
+
+int zt_rope_backward(const float *dout, float *din, int rows, int cols, int pos, double theta, int head_dim,
+                     hipStream_t stream) {
+    return rope_impl("zt_rope_bwd", dout, din, rows, cols, pos, theta, head_dim, stream);
 }
 
 static int fill_impl(const char *name, float *dst, size_t n, uint64_t seed, double p0, double p1,
@@ -633,9 +727,10 @@ int zt_attn_plan(int B, int T, int n_heads, int n_kv_heads, int dim, int max_til
     DeviceState *st2 = nullptr;
     unsigned ba = 0, bb = 0, ta = 0, tb = 0;
     char na[64], nb[64];
-    // Shape-only planning: the pointers are placeholders that are never used.
-    float dummy = 0.f;
-    if (backward_prepare(&dummy, &dummy, &dummy, &dummy, &dummy, &dummy, &dummy, &dummy, &dummy, &dummy, B, T,
+    // Shape-only planning: the pointers are placeholders that are never
+    // dereferenced, aligned as a device allocation is so the choice matches a real call.
+    alignas(256) static float dummy[4];
+    if (backward_prepare(dummy, dummy, dummy, dummy, dummy, dummy, dummy, dummy, dummy, dummy, B, T,
                          n_heads, n_kv_heads, dim, max_tile, &a, &st2, na, nb, &ba, &bb, &ta, &tb))
         return 1;
     snprintf(dq, len, "%s", na);

@@ -19,8 +19,8 @@ ABI_SYMBOLS = [
     "zt_attn_dim_ok", "zt_attn_forward_shmem", "zt_attn_bwd_dq_shmem", "zt_attn_bwd_dkdv_shmem",
     "zt_attn_forward", "zt_attn_backward",
     "zt_attn_forward_batched", "zt_attn_backward_batched", "zt_attn_bwd_dq", "zt_attn_bwd_dkdv",
-    "zt_attn_decode_workspace", "zt_attn_decode",
-    "zt_rmsnorm_forward", "zt_rope_forward", "zt_fill_normal", "zt_fill_uniform", "zt_attn_version",
+    "zt_attn_decode_workspace", "zt_attn_decode", "zt_attn_decode_step_workspace", "zt_attn_decode_step",
+    "zt_rmsnorm_forward", "zt_rope_forward", "zt_rope_backward", "zt_fill_normal", "zt_fill_uniform", "zt_attn_version",
     "zt_attn_lds_limit", "zt_attn_plan",
 ]
 HOLDER_SYMBOLS = [
@@ -62,8 +62,11 @@ def lib():
             "zt_attn_bwd_dkdv": (I, [P] * 9 + [I] * 5 + [P]),
             "zt_attn_decode_workspace": (Z, [I, I, I, I, I]),
             "zt_attn_decode": (I, [P, P, P, P, P, I, I, I, I, I, P, Z, P]),
+            "zt_attn_decode_step_workspace": (Z, [I, I, I, I, I]),
+            "zt_attn_decode_step": (I, [P] * 7 + [I] * 5 + [D, P, Z, P]),
             "zt_rmsnorm_forward": (I, [P, P, P, I, I, D, P]),
             "zt_rope_forward": (I, [P, P, I, I, I, D, I, P]),
+            "zt_rope_backward": (I, [P, P, I, I, I, D, I, P]),
             "zt_fill_normal": (I, [P, Z, U64, D, D, P]),
             "zt_fill_uniform": (I, [P, Z, U64, D, D, P]),
             "zt_attn_version": (ctypes.c_char_p, []),
@@ -167,6 +170,22 @@ def decode(q, k_cache, v_cache, out, n_keys, B, n_ctx, n_heads, n_kv_heads, dim,
     _check(rc, "zt_attn_decode")
 
 
+def decode_step_workspace_bytes(B, n_ctx, n_heads, n_kv_heads, dim):
+    return lib().zt_attn_decode_step_workspace(B, n_ctx, n_heads, n_kv_heads, dim)
+
+
+def decode_step(q, k_new, v_new, k_cache, v_cache, out, pos, B, n_ctx, n_heads, n_kv_heads, dim, workspace,
+                theta=500000.0, stream=None):
+    """pos: a sequence of B ints (host), the position each sequence appends at."""
+    _f32_cuda(q, k_new, v_new, k_cache, v_cache, out)
+    arr = (ctypes.c_int * B)(*[int(x) for x in pos])
+    nbytes = workspace.numel() * workspace.element_size()
+    rc = lib().zt_attn_decode_step(_ptr(q), _ptr(k_new), _ptr(v_new), _ptr(k_cache), _ptr(v_cache), _ptr(out), arr,
+                                   B, n_ctx, n_heads, n_kv_heads, dim, theta, _ptr(workspace), nbytes,
+                                   _stream(stream))
+    _check(rc, "zt_attn_decode_step")
+
+
 def rmsnorm(x, w, y, rows, cols, eps=1e-5, stream=None):
     _f32_cuda(x, w, y)
     _check(lib().zt_rmsnorm_forward(_ptr(x), _ptr(w), _ptr(y), rows, cols, eps, _stream(stream)), "zt_rmsnorm_forward")
@@ -183,6 +202,12 @@ def plan(B, T, n_heads, n_kv_heads, dim, max_tile=64):
     bufs = [ctypes.create_string_buffer(64) for _ in range(3)]
     _check(lib().zt_attn_plan(B, T, n_heads, n_kv_heads, dim, max_tile, *bufs, 64), "zt_attn_plan")
     return tuple(b.value.decode() for b in bufs)
+
+
+def rope_backward(dout, din, rows, cols, pos, theta, head_dim, stream=None):
+    _f32_cuda(dout, din)
+    _check(lib().zt_rope_backward(_ptr(dout), _ptr(din), rows, cols, pos, theta, head_dim, _stream(stream)),
+           "zt_rope_backward")
 
 
 def fill_normal(t, seed, mean=0.0, sigma=1.0, stream=None):
