@@ -82,8 +82,14 @@ def main():
     B, T, H, Hkv, D = 1, 4096, 32, 8, 128
     q0, k0 = normal(B * T * H * D, SEEDS["q"]), normal(B * T * Hkv * D, SEEDS["k"])
     q, k = torch.empty_like(q0), torch.empty_like(k0)
-    zt.rope(q0, q, B * T, H * D, 0, THETA, D)
-    zt.rope(k0, k, B * T, Hkv * D, 0, THETA, D)
+
+    def rope_qk():  # src/model.zig:372-377: q and k rotated at position 0, one launch
+        zt.rope_qk(q0, k0, q, k, B, T, H, Hkv, D, 0, THETA)
+
+    rope_qk()
+    t_rope = event_time(torch, rope_qk, 10)
+    rope_bytes = 2 * (q.numel() + k.numel()) * 4
+    log(f"C3 RoPE q+k: {t_rope * 1e3:.1f} us, {rope_bytes / (t_rope * 1e-3) / 1e9:.0f} GB/s")
     del q0, k0
     v, do = normal(B * T * Hkv * D, SEEDS["v"]), normal(B * T * H * D, SEEDS["do"])
     out, dq = torch.empty_like(q), torch.empty_like(q)
@@ -269,6 +275,8 @@ def main():
                    "GB/s": round(dec_gbs, 1), "bytes": dec_bytes, "frac_hbm": round(dec_gbs / PEAK_HBM, 4),
                    "step_us": round(t_step * 1e3, 2), "step_GB/s": round(step_gbs, 1)},
         "rmsnorm": norm,
+        "rope_qk": {"workload": "C3 q and k, position 0", "us": round(t_rope * 1e3, 2), "bytes": rope_bytes,
+                    "GB/s": round(rope_bytes / (t_rope * 1e-3) / 1e9, 1)},
         "hbm_copy": {"bytes": 2 * (1 << 30), "GB/s": round(copy_gbs, 1), "frac_hbm": round(copy_gbs / PEAK_HBM, 4)},
     }
     print(json.dumps(line), flush=True)

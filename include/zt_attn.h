@@ -153,6 +153,19 @@ int zt_rope_forward(const float *x, float *y, int rows, int cols, int pos, doubl
 int zt_rope_backward(const float *dout, float *din, int rows, int cols, int pos, double theta, int head_dim,
                      hipStream_t stream);
 
+/* RoPE of q and k in one launch, as the model rotates both before attention
+ * (src/model.zig:372-377; each is src/rope.zig:21-55): q/q_out [B, T, n_heads*head_dim],
+ * k/k_out [B, T, n_kv_heads*head_dim], row t of every sequence at position pos + t.
+ * One f64 angle per (position, pair) serves every head of both tensors.
+ * In-place (q_out == q, k_out == k) is allowed.  No reference counterpart. */
+int zt_rope_qk_forward(const float *q, const float *k, float *q_out, float *k_out, int B, int T, int n_heads,
+                       int n_kv_heads, int head_dim, int pos, double theta, hipStream_t stream);
+
+/* The transpose, for dq and dk together (src/autograd.zig:566-569 applies
+ * ropeBackward to each).  No reference counterpart. */
+int zt_rope_qk_backward(const float *dq, const float *dk, float *dq_out, float *dk_out, int B, int T,
+                        int n_heads, int n_kv_heads, int head_dim, int pos, double theta, hipStream_t stream);
+
 /* Seeded synthetic inputs (splitmix64 counter stream + Box-Muller): element i
  * depends only on (seed, i).  normal: mean + sigma*z; uniform: [lo, hi). */
 int zt_fill_normal(float *dst, size_t n, uint64_t seed, double mean, double sigma, hipStream_t stream);

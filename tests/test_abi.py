@@ -171,6 +171,21 @@ def test_decode_step_refusals(zt, capfd):
     assert L.zt_attn_decode_step_workspace(0, n_ctx, H, Hkv, D) == 0
 
 
+@pytest.mark.parametrize("fn", ["zt_rope_qk_forward", "zt_rope_qk_backward"])
+def test_rope_qk_refusals(zt, capfd, fn):
+    f = getattr(zt.lib(), fn)
+    p = 0x10000
+    assert f(p, p, p, p, 1, 4, 4, 2, 3, 0, ctypes.c_double(5e5), NULL) == 1
+    assert "head_dim 3" in capfd.readouterr().err
+    assert f(p, p, p, p, -1, 4, 4, 2, 8, 0, ctypes.c_double(5e5), NULL) == 1
+    assert f(p, p, p, p, 1, 4, 4, 2, 8, -2, ctypes.c_double(5e5), NULL) == 1
+    assert f(p, p, p, p, 1, 4, 4, 2, 8, 0, ctypes.c_double(0.0), NULL) == 1
+    assert "theta" in capfd.readouterr().err
+    assert f(p, NULL, p, p, 1, 4, 4, 2, 8, 0, ctypes.c_double(5e5), NULL) == 1
+    assert "null" in capfd.readouterr().err
+    assert f(NULL, NULL, NULL, NULL, 0, 4, 4, 2, 8, 0, ctypes.c_double(5e5), NULL) == 0  # no rows
+
+
 @pytest.mark.parametrize("fn", ["zt_rope_forward", "zt_rope_backward"])
 def test_rope_refusals(zt, fn):
     f = getattr(zt.lib(), fn)

@@ -69,7 +69,8 @@ def test_backward_any_tile_cap(gpu, zt, oracle, max_tile):
 
 
 @pytest.mark.parametrize("env", [
-    {"ZT_ATTN_W8": "1"}, {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "0"}, {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "1"},
+    {"ZT_ATTN_W8": "1"}, {"ZT_ATTN_W8": "1", "ZT_ATTN_PF": "1"},
+    {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "0"}, {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "1"},
     {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "0", "ZT_ATTN_HS": "4"}, {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "1", "ZT_ATTN_HS": "4"},
     {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "0", "ZT_ATTN_HS": "1"}, {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "1", "ZT_ATTN_HS": "1"},
 ])
@@ -78,6 +79,23 @@ def test_backward_every_dkdv_variant(gpu, zt, oracle, threads, monkeypatch, env,
     """Each dk/dv kernel variant (eight-wave, register-staged, asynchronously
     staged; 1/2/4-way head splits), forced through the library's tuning
     variables, matches the twin."""
+    for k_, v_ in env.items():
+        monkeypatch.setenv(k_, v_)
+    (q, k, v, do), (dq, dk, dv, *_) = _run(gpu, zt, B, T, H, Hkv, D)
+    rq, rk, rv = oracle.attention_backward(q, k, v, do, B, T, H, Hkv, D, threads=threads)
+    assert max(rel_err(dq, rq), rel_err(dk, rk), rel_err(dv, rv)) <= BWD_REL
+
+
+@pytest.mark.parametrize("env", [
+    {"ZT_ATTN_BK": "32", "ZT_ATTN_QPF": "1", "ZT_ATTN_DQ_W": "4"},
+    {"ZT_ATTN_BK": "32", "ZT_ATTN_QPF": "1", "ZT_ATTN_DQ_W": "8"},
+    {"ZT_ATTN_BK": "32", "ZT_ATTN_QPF": "0", "ZT_ATTN_DQ_W": "8"},
+    {"ZT_ATTN_BK": "64", "ZT_ATTN_QPF": "0", "ZT_ATTN_DQ_W": "4"},
+])
+@pytest.mark.parametrize("B,T,H,Hkv,D", [(1, 200, 8, 2, 128), (2, 75, 4, 1, 64), (1, 61, 6, 3, 66)])
+def test_backward_every_dq_variant(gpu, zt, oracle, threads, monkeypatch, env, B, T, H, Hkv, D):
+    """Each dq kernel variant (four or eight waves, 32- or 64-key tiles, with
+    and without register prefetch of the next K/V tile) matches the twin."""
     for k_, v_ in env.items():
         monkeypatch.setenv(k_, v_)
     (q, k, v, do), (dq, dk, dv, *_) = _run(gpu, zt, B, T, H, Hkv, D)

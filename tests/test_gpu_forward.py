@@ -58,6 +58,21 @@ def test_forward_both_key_tiles(gpu, zt, oracle, monkeypatch, bk, B, T, H, Hkv, 
     assert max_abs(out, ref) <= FWD_TOL
 
 
+@pytest.mark.parametrize("env", [{"ZT_ATTN_FPF": "1", "ZT_ATTN_FWD_W": "4"}, {"ZT_ATTN_FPF": "1", "ZT_ATTN_FWD_W": "8"},
+                                 {"ZT_ATTN_FPF": "0", "ZT_ATTN_FWD_W": "4"}, {"ZT_ATTN_FPF": "0", "ZT_ATTN_FWD_W": "8"}])
+@pytest.mark.parametrize("B,T,H,Hkv,D", [(1, 150, 8, 2, 128), (2, 70, 4, 4, 256), (1, 99, 6, 3, 66), (1, 45, 4, 1, 32)])
+def test_forward_every_variant(gpu, zt, oracle, monkeypatch, env, B, T, H, Hkv, D):
+    """Four- and eight-wave workgroups, with and without register prefetch of
+    the next K/V tile, forced through the library's tuning variables."""
+    monkeypatch.setenv("ZT_ATTN_BK", "32")
+    for k_, v_ in env.items():
+        monkeypatch.setenv(k_, v_)
+    q, k, v = _inputs(gpu, zt, B, T, H, Hkv, D)
+    out = _run(gpu, zt, q, k, v, B, T, H, Hkv, D)
+    ref = oracle.attention_forward(host(q), host(k), host(v), B, T, H, Hkv, D)
+    assert max_abs(out, ref) <= FWD_TOL
+
+
 @pytest.mark.parametrize("max_tile", [1, 32, 64, 1024])
 def test_forward_any_tile_cap(gpu, zt, oracle, max_tile):
     B, T, H, Hkv, D = 1, 77, 4, 2, 64

@@ -89,6 +89,26 @@ def test_rope_backward_matches_twin(gpu, zt, oracle, rows, heads, hd, pos):
         assert max_abs(host(y), oracle.rope(host(x), rows, cols, pos, THETA, hd)) > 1e-3
 
 
+@pytest.mark.parametrize("B,T,H,Hkv,hd,pos", [(1, 4096, 32, 8, 128, 0), (3, 50, 6, 2, 34, 7), (2, 9, 4, 4, 256, 100)])
+@pytest.mark.parametrize("backward", [False, True])
+def test_rope_qk_matches_twin(gpu, zt, oracle, B, T, H, Hkv, hd, pos, backward):
+    # q and k in one launch; every sequence restarts at pos (src/model.zig:372-377).
+    q = dev_normal(gpu, zt, B * T * H * hd, SEED_X)
+    k = dev_normal(gpu, zt, B * T * Hkv * hd, SEED_W)
+    qh, kh = host(q).reshape(B, T * H * hd), host(k).reshape(B, T * Hkv * hd)
+    qo, ko = gpu.full_like(q, float("nan")), gpu.full_like(k, float("nan"))
+    zt.rope_qk(q, k, qo, ko, B, T, H, Hkv, hd, pos, THETA, backward=backward)
+    zt.rope_qk(q, k, q, k, B, T, H, Hkv, hd, pos, THETA, backward=backward)  # in place
+    gpu.cuda.synchronize()
+    fn = oracle.rope_backward if backward else oracle.rope
+    want_q = np.concatenate([fn(qh[b], T, H * hd, pos, THETA, hd) for b in range(B)])
+    want_k = np.concatenate([fn(kh[b], T, Hkv * hd, pos, THETA, hd) for b in range(B)])
+    for got_q, got_k in ((qo, ko), (q, k)):
+        assert max_abs(host(got_q), want_q) <= 2e-6
+        assert max_abs(host(got_k), want_k) <= 2e-6
+    assert np.mean(host(qo) == want_q) >= 0.999  # separate f64 roundings, as the reference
+
+
 def test_rope_reference_known_answers(gpu, zt, golden):
     for c in golden["rope"]:
         x = gpu.tensor(np.float32(c["x"]), device="cuda")

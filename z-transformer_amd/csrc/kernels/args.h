@@ -26,6 +26,7 @@ struct BwdArgs {
     float scale, scale_log2e;
 };
 
+#define ZT_MAX_DIM 256  // the widest head the library admits
 #define ZT_DEC_MAXB 64  // sequences per decode launch (n_keys travels in the arguments)
 
 struct DecArgs {
@@ -50,10 +51,13 @@ struct NormArgs {
     double eps;
 };
 
+// RoPE over up to two row-aligned tensors sharing positions (q and k of one
+// batch): tensor 1 has heads1 heads per row, tensor 2 heads2 (0 = absent).
+// Row r sits at position pos + r % seq_len.
 struct RopeArgs {
-    const float *x;
-    float *y;
-    int rows, cols, pos, head_dim;
+    const float *x1, *x2;
+    float *y1, *y2;
+    int rows, seq_len, heads1, heads2, pos, head_dim;
     double theta;
 };
 

@@ -27,7 +27,7 @@
 #include "args.h"
 
 
-template <int DP, int BK, int NW>
+template <int DP, int BK, int NW, bool PF = false>
 __device__ __forceinline__ void bwd_dq_body(const BwdArgs &a) {
     constexpr int LW = DP + 4, DQ = DP / 4, NT = DP / 16, NJ = BK / 16;
     __shared__ float Ks[BK * LW];
@@ -63,12 +63,53 @@ __device__ __forceinline__ void bwd_dq_body(const BwdArgs &a) {
     const int kend_wg = min(a.T, wg_row0 + 16 * RB);
     const int kend_w = row0 < a.T ? min(a.T, row0 + 16) : 0;
 
+    // Register prefetch (PF) of the next K/V tile, as in the forward.
+    constexpr int NTH = 64 * NW, CPR = DP / 4;
+    constexpr int NPF = PF ? 2 * BK * CPR / NTH : 1;
+    static_assert(!PF || (2 * BK * CPR) % NTH == 0, "prefetch split");
+    f4 pf[NPF];
+    auto fetch = [&](int k0) {
+#pragma unroll
+        for (int n = 0; n < NPF; ++n) {
+            const int e = tid + n * NTH;
+            const int arr = e / (BK * CPR), r = (e / CPR) % BK, c = (e % CPR) * 4;
+            const int key = k0 + r;
+            const float *src = (arr ? vb : kb) + (size_t)key * kld + c;
+            f4 x = zero4();
+            if (key < a.T && c < a.dim) {
+                if (vec4) {
+                    x = *reinterpret_cast<const f4 *>(src);
+                } else {
+                    const f2 lo = *reinterpret_cast<const f2 *>(src);
+                    x.x = lo.x; x.y = lo.y;
+                    if (c + 2 < a.dim) {
+                        const f2 hi = *reinterpret_cast<const f2 *>(src + 2);
+                        x.z = hi.x; x.w = hi.y;
+                    }
+                }
+            }
+            pf[n] = x;
+        }
+    };
+    if constexpr (PF) fetch(0);
+
     for (int k0 = 0; k0 < kend_wg; k0 += BK) {
         __syncthreads();
-        const int nvalid = min(BK, a.T - k0);
-        stage_rows<DP, LW, 64 * NW>(Ks, kb + (size_t)k0 * kld, kld, BK, nvalid, a.dim, vec4, tid);
-        stage_rows<DP, LW, 64 * NW>(Vs, vb + (size_t)k0 * kld, kld, BK, nvalid, a.dim, vec4, tid);
-        __syncthreads();
+        if constexpr (PF) {
+#pragma unroll
+            for (int n = 0; n < NPF; ++n) {
+                const int e = tid + n * NTH;
+                const int arr = e / (BK * CPR), r = (e / CPR) % BK, c = (e % CPR) * 4;
+                *reinterpret_cast<f4 *>((arr ? Vs : Ks) + r * LW + c) = pf[n];
+            }
+            __syncthreads();
+            if (k0 + BK < kend_wg) fetch(k0 + BK);
+        } else {
+            const int nvalid = min(BK, a.T - k0);
+            stage_rows<DP, LW, NTH>(Ks, kb + (size_t)k0 * kld, kld, BK, nvalid, a.dim, vec4, tid);
+            stage_rows<DP, LW, NTH>(Vs, vb + (size_t)k0 * kld, kld, BK, nvalid, a.dim, vec4, tid);
+            __syncthreads();
+        }
         if (k0 >= kend_w) continue;
 
         // S^T and dP^T for every 16-key sub-block.  Up to d = 192 the 2 * NJ
@@ -142,12 +183,12 @@ __device__ __forceinline__ void bwd_dq_body(const BwdArgs &a) {
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk) {
                 const float pv = s[j][kk], pd = dp[j][kk];
-                const float *krow = Ks + (16 * j + 4 * grp + kk) * LW + l16;
+                float kx[NT];  // K^T rows, row-owner layout: K[key][l16 * NT + i]
+                lds_run<NT>(kx, Ks + (16 * j + 4 * grp + kk) * LW + l16 * NT);
 #pragma unroll
                 for (int i = 0; i < NT; ++i) {
-                    const float kx = krow[16 * i];
-                    a0[i] = mfma16(kx, pv, a0[i]);
-                    a1[i] = mfma16(kx, pd, a1[i]);
+                    a0[i] = mfma16(kx[i], pv, a0[i]);
+                    a1[i] = mfma16(kx[i], pd, a1[i]);
                 }
             }
         }
@@ -159,7 +200,9 @@ __device__ __forceinline__ void bwd_dq_body(const BwdArgs &a) {
     if (row_ok) {
         float *dqrow = a.dq + qoff + (size_t)my_row * qld;
 #pragma unroll
-        for (int i = 0; i < NT; ++i) store4(dqrow, 16 * i + 4 * grp, a.dim, vec4, (a1[i] - delta * a0[i]) * f);
+        for (int i = 0; i < NT; ++i) a1[i] = a1[i] - delta * a0[i];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) store_run<NT>(dqrow, (4 * grp + r) * NT, a.dim, vec4, a1, r, f);
         if (grp == 0) {
             const size_t o = ((size_t)b * a.T + my_row) * a.H + h;
             a.row_max[o] = m * 0.69314718055994531f;  // back to natural units
@@ -169,7 +212,7 @@ __device__ __forceinline__ void bwd_dq_body(const BwdArgs &a) {
     }
 }
 
-template <int DP, int HS, int KW>
+template <int DP, int HS, int KW, bool PF = false>
 __device__ __forceinline__ void bwd_dkdv_body(const BwdArgs &a) {
     constexpr int LW = DP + 4, DQ = DP / 4, NT = DP / 16, NTH = 64 * KW * HS;
     constexpr int BQ = 16;
@@ -208,35 +251,108 @@ __device__ __forceinline__ void bwd_dkdv_body(const BwdArgs &a) {
     float *qs = Qs + hs * BQ * LW;
     float *ds = Ds + hs * BQ * LW;
     float *st = St + hs * BQ * 4;
-    for (int hi = 0; hi < hpp; ++hi) {
-        for (int t0 = wg_s0; t0 < a.T; t0 += BQ) {
-            __syncthreads();
-            // Stage Q, dO rows [t0, t0+16) for every part's head.
-            {
-                const int nvalid = min(BQ, a.T - t0);
-                for (int part = 0; part < HS; ++part) {
-                    const int hh = kvh * group + part * hpp + hi;
-                    const size_t off = (size_t)b * a.T * qld + (size_t)t0 * qld + (size_t)hh * a.dim;
-                    stage_rows<DP, LW, NTH>(Qs + part * BQ * LW, a.q + off, qld, BQ, nvalid, a.dim, vec4, tid);
-                    stage_rows<DP, LW, NTH>(Ds + part * BQ * LW, a.dout + off, qld, BQ, nvalid, a.dim, vec4, tid);
-                }
-                if (tid < HS * BQ) {
-                    const int part = tid / BQ, r = tid % BQ, t = t0 + r;
-                    const int hh = kvh * group + part * hpp + hi;
-                    float m2 = 0.f, il = 0.f, de = 0.f;
-                    if (t < a.T) {
-                        const size_t o = ((size_t)b * a.T + t) * a.H + hh;
-                        m2 = a.row_max[o] * kLog2e;
-                        il = 1.f / a.row_den[o];
-                        de = a.row_del[o];
+    // Stages: (head of each part hi, 16-row tile t0 of the suffix t >= wg_s0),
+    // the tiles walked from the last row down so that the workgroups resident
+    // at one time -- which all reach the end of the sequence -- read the same
+    // Q/dO rows together and share them in L2.
+    const int n_t = (a.T - wg_s0 + BQ - 1) / BQ;
+    const int n_stage = hpp * n_t;
+    auto tile_row = [&](int stg) { return wg_s0 + (n_t - 1 - stg % n_t) * BQ; };
+
+    // Register prefetch (PF): thread tid holds float4 chunks e = tid + n * NTH
+    // of the stage's HS x {Q, dO} x 16 x DP block and one row's statistics;
+    // they are loaded while the previous stage computes and written to LDS
+    // after the next barrier.  Rows >= T and columns >= dim load as zero.
+    constexpr int CPR = DP / 4;
+    constexpr int NPF = PF ? HS * 2 * BQ * CPR / NTH : 1;
+    static_assert(!PF || (HS * 2 * BQ * CPR) % NTH == 0, "prefetch split");
+    f4 pf[NPF];
+    float pm2 = 0.f, pil = 0.f, pde = 0.f;
+    auto fetch = [&](int stg) {
+        const int hi = stg / n_t, t0 = tile_row(stg);
+#pragma unroll
+        for (int n = 0; n < NPF; ++n) {
+            const int e = tid + n * NTH;
+            const int part = e / (2 * BQ * CPR), arr = (e / (BQ * CPR)) & 1;
+            const int r = (e / CPR) % BQ, c = (e % CPR) * 4;
+            const int hh = kvh * group + part * hpp + hi, t = t0 + r;
+            const float *src = (arr ? a.dout : a.q) + (size_t)b * a.T * qld + (size_t)t * qld + (size_t)hh * a.dim + c;
+            f4 x = zero4();
+            if (t < a.T && c < a.dim) {
+                if (vec4) {
+                    x = *reinterpret_cast<const f4 *>(src);
+                } else {
+                    const f2 lo = *reinterpret_cast<const f2 *>(src);
+                    x.x = lo.x; x.y = lo.y;
+                    if (c + 2 < a.dim) {
+                        const f2 hi2 = *reinterpret_cast<const f2 *>(src + 2);
+                        x.z = hi2.x; x.w = hi2.y;
                     }
-                    St[(part * BQ + r) * 4 + 0] = m2;
-                    St[(part * BQ + r) * 4 + 1] = il;
-                    St[(part * BQ + r) * 4 + 2] = de;
                 }
             }
+            pf[n] = x;
+        }
+        if (tid < HS * BQ) {
+            const int part = tid / BQ, t = t0 + tid % BQ;
+            const int hh = kvh * group + part * hpp + hi;
+            pm2 = 0.f; pil = 0.f; pde = 0.f;
+            if (t < a.T) {
+                const size_t o = ((size_t)b * a.T + t) * a.H + hh;
+                pm2 = a.row_max[o] * kLog2e;
+                pil = 1.f / a.row_den[o];
+                pde = a.row_del[o];
+            }
+        }
+    };
+    auto put = [&]() {
+#pragma unroll
+        for (int n = 0; n < NPF; ++n) {
+            const int e = tid + n * NTH;
+            const int part = e / (2 * BQ * CPR), arr = (e / (BQ * CPR)) & 1;
+            const int r = (e / CPR) % BQ, c = (e % CPR) * 4;
+            *reinterpret_cast<f4 *>((arr ? Ds : Qs) + (part * BQ + r) * LW + c) = pf[n];
+        }
+        if (tid < HS * BQ) {
+            St[tid * 4 + 0] = pm2;
+            St[tid * 4 + 1] = pil;
+            St[tid * 4 + 2] = pde;
+        }
+    };
+    if constexpr (PF) fetch(0);
+
+    for (int stg = 0; stg < n_stage; ++stg) {
+        const int hi = stg / n_t, t0 = tile_row(stg);
+        __syncthreads();
+        if constexpr (PF) {
+            put();
             __syncthreads();
-            if (t0 + 15 < s0 || s0 >= a.T) continue;  // wave-uniform: no visible pair
+            if (stg + 1 < n_stage) fetch(stg + 1);
+        } else {
+            // Stage Q, dO rows [t0, t0+16) for every part's head.
+            const int nvalid = min(BQ, a.T - t0);
+            for (int part = 0; part < HS; ++part) {
+                const int hh = kvh * group + part * hpp + hi;
+                const size_t off = (size_t)b * a.T * qld + (size_t)t0 * qld + (size_t)hh * a.dim;
+                stage_rows<DP, LW, NTH>(Qs + part * BQ * LW, a.q + off, qld, BQ, nvalid, a.dim, vec4, tid);
+                stage_rows<DP, LW, NTH>(Ds + part * BQ * LW, a.dout + off, qld, BQ, nvalid, a.dim, vec4, tid);
+            }
+            if (tid < HS * BQ) {
+                const int part = tid / BQ, r = tid % BQ, t = t0 + r;
+                const int hh = kvh * group + part * hpp + hi;
+                float m2 = 0.f, il = 0.f, de = 0.f;
+                if (t < a.T) {
+                    const size_t o = ((size_t)b * a.T + t) * a.H + hh;
+                    m2 = a.row_max[o] * kLog2e;
+                    il = 1.f / a.row_den[o];
+                    de = a.row_del[o];
+                }
+                St[(part * BQ + r) * 4 + 0] = m2;
+                St[(part * BQ + r) * 4 + 1] = il;
+                St[(part * BQ + r) * 4 + 2] = de;
+            }
+            __syncthreads();
+        }
+        if (t0 + 15 < s0 || s0 >= a.T) continue;  // wave-uniform: no visible pair
 
             f4 s = zero4(), dp = zero4();
             {
@@ -269,16 +385,16 @@ __device__ __forceinline__ void bwd_dkdv_body(const BwdArgs &a) {
             }
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk) {
-                const float *drow = ds + (4 * grp + kk) * LW + l16;
-                const float *qrow = qs + (4 * grp + kk) * LW + l16;
+                float dx[NT], qx[NT];  // dO^T, Q^T rows in the row-owner layout
+                lds_run<NT>(dx, ds + (4 * grp + kk) * LW + l16 * NT);
+                lds_run<NT>(qx, qs + (4 * grp + kk) * LW + l16 * NT);
                 const float pv = p[kk], dv = dsv[kk];
 #pragma unroll
                 for (int i = 0; i < NT; ++i) {
-                    dva[i] = mfma16(drow[16 * i], pv, dva[i]);
-                    dka[i] = mfma16(qrow[16 * i], dv, dka[i]);
+                    dva[i] = mfma16(dx[i], pv, dva[i]);
+                    dka[i] = mfma16(qx[i], dv, dka[i]);
                 }
             }
-        }
     }
 
     // Sum the head-split partials in a fixed order (part 0 + 1 + ...).
@@ -303,9 +419,9 @@ __device__ __forceinline__ void bwd_dkdv_body(const BwdArgs &a) {
         float *dkrow = a.dk + kvoff + (size_t)my_key * kld;
         float *dvrow = a.dv + kvoff + (size_t)my_key * kld;
 #pragma unroll
-        for (int i = 0; i < NT; ++i) {
-            store4(dkrow, 16 * i + 4 * grp, a.dim, vec4, dka[i] * a.scale);
-            store4(dvrow, 16 * i + 4 * grp, a.dim, vec4, dva[i]);
+        for (int r = 0; r < 4; ++r) {
+            store_run<NT>(dkrow, (4 * grp + r) * NT, a.dim, vec4, dka, r, a.scale);
+            store_run<NT>(dvrow, (4 * grp + r) * NT, a.dim, vec4, dva, r, 1.f);
         }
     }
 }
@@ -427,11 +543,13 @@ __device__ __forceinline__ void bwd_dkdv_dma_body(const BwdArgs &a) {
             for (int kk = 0; kk < 4; ++kk) {
                 const int tr = 4 * grp + kk;
                 const float pv = p[kk], dv = dsv[kk];
+                float dx[NT], qx[NT];  // dO^T, Q^T rows in the row-owner layout
+                lds_run_swz<NT, CPR>(dx, ds, tr, l16 * NT);
+                lds_run_swz<NT, CPR>(qx, qs, tr, l16 * NT);
 #pragma unroll
                 for (int i = 0; i < NT; ++i) {
-                    const int off = tr * DP + 4 * swz<CPR>(4 * i + (l16 >> 2), tr) + (l16 & 3);
-                    dva[i] = mfma16(ds[off], pv, dva[i]);
-                    dka[i] = mfma16(qs[off], dv, dka[i]);
+                    dva[i] = mfma16(dx[i], pv, dva[i]);
+                    dka[i] = mfma16(qx[i], dv, dka[i]);
                 }
             }
         }
@@ -460,9 +578,9 @@ __device__ __forceinline__ void bwd_dkdv_dma_body(const BwdArgs &a) {
         float *dkrow = a.dk + kvoff + (size_t)my_key * kld;
         float *dvrow = a.dv + kvoff + (size_t)my_key * kld;
 #pragma unroll
-        for (int i = 0; i < NT; ++i) {
-            *reinterpret_cast<f4 *>(dkrow + 16 * i + 4 * grp) = dka[i] * a.scale;
-            *reinterpret_cast<f4 *>(dvrow + 16 * i + 4 * grp) = dva[i];
+        for (int r = 0; r < 4; ++r) {
+            store_run<NT>(dkrow, (4 * grp + r) * NT, DP, true, dka, r, a.scale);
+            store_run<NT>(dvrow, (4 * grp + r) * NT, DP, true, dva, r, 1.f);
         }
     }
 }
@@ -478,6 +596,15 @@ __device__ __forceinline__ void bwd_dkdv_dma_body(const BwdArgs &a) {
     extern "C" __global__ void __launch_bounds__(512) zt_bwd_dq8_d##DP##_k##BK(BwdArgs a) {      \
         bwd_dq_body<DP, BK, 8>(a);                                                                 \
     }
+// Register-prefetched dq (32-key tiles), four and eight waves.
+#define ZT_BWD_DQ_PF(DP)                                                                           \
+    extern "C" __global__ void __launch_bounds__(256, (DP) <= 192 ? 2 : 1)                        \
+        zt_bwd_dqp_d##DP##_k32(BwdArgs a) {                                                        \
+        bwd_dq_body<DP, 32, 4, true>(a);                                                           \
+    }                                                                                              \
+    extern "C" __global__ void __launch_bounds__(512) zt_bwd_dq8p_d##DP##_k32(BwdArgs a) {       \
+        bwd_dq_body<DP, 32, 8, true>(a);                                                           \
+    }
 #define ZT_BWD_DKDV(DP, HS)                                                                        \
     extern "C" __global__ void __launch_bounds__(256) zt_bwd_dkdv_d##DP##_hs##HS(BwdArgs a) {   \
         bwd_dkdv_body<DP, HS, 4 / HS>(a);                                                          \
@@ -486,13 +613,16 @@ __device__ __forceinline__ void bwd_dkdv_dma_body(const BwdArgs &a) {
 #define ZT_BWD_DKDV8(DP)                                                                           \
     extern "C" __global__ void __launch_bounds__(512) zt_bwd_dkdv8_d##DP##_hs2(BwdArgs a) {     \
         bwd_dkdv_body<DP, 2, 4>(a);                                                                \
+    }                                                                                              \
+    extern "C" __global__ void __launch_bounds__(512) zt_bwd_dkdv8p_d##DP##_hs2(BwdArgs a) {    \
+        bwd_dkdv_body<DP, 2, 4, true>(a);                                                          \
     }
 #define ZT_BWD_DKDV_DMA(DP, HS)                                                                    \
     extern "C" __global__ void __launch_bounds__(256) zt_bwd_dkdv_dma_d##DP##_hs##HS(BwdArgs a) { \
         bwd_dkdv_dma_body<DP, HS>(a);                                                              \
     }
 #define ZT_BWD_ALL(DP)                                                                             \
-    ZT_BWD_DQ(DP, 32) ZT_BWD_DQ(DP, 64) ZT_BWD_DKDV(DP, 1) ZT_BWD_DKDV(DP, 2) ZT_BWD_DKDV8(DP)    \
+    ZT_BWD_DQ(DP, 32) ZT_BWD_DQ(DP, 64) ZT_BWD_DQ_PF(DP) ZT_BWD_DKDV(DP, 1) ZT_BWD_DKDV(DP, 2) ZT_BWD_DKDV8(DP)    \
     ZT_BWD_DKDV_DMA(DP, 1) ZT_BWD_DKDV_DMA(DP, 2)
 
 ZT_BWD_ALL(32)

@@ -21,15 +21,15 @@
 #include "args.h"
 
 
-template <int DP, int BK, int NW>
+template <int DP, int BK, int NW, bool PF>
 __device__ __forceinline__ void attn_fwd_body(const FwdArgs &a) {
     constexpr int LW = DP + 4;  // LDS row stride: +16 B spreads row starts over banks
     constexpr int DQ = DP / 4;  // d values per lane group
     constexpr int NT = DP / 16; // 16-wide column tiles of the output
     constexpr int NJ = BK / 16; // 16-key sub-blocks per LDS tile
-    constexpr int LT = BK + 4;  // row stride of the transposed V tile
+    constexpr int NTH = 64 * NW;
     __shared__ float Ks[BK * LW];
-    __shared__ float Vt[DP * LT];  // V^T: column n of the tile is row n here
+    __shared__ float Vs[BK * LW];
 
     const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, grp = lane >> 4, w = tid >> 6;
     const int RB = NW / a.HW;  // 16-row blocks per head in this workgroup
@@ -60,12 +60,56 @@ __device__ __forceinline__ void attn_fwd_body(const FwdArgs &a) {
     const int kend_wg = min(a.n_keys, a.q_offset + min(a.T, wg_row0 + 16 * RB));
     const int kend_w = row0 < a.T ? min(a.n_keys, a.q_offset + min(a.T, row0 + 16)) : 0;
 
+    // Register prefetch (PF): thread tid holds float4 chunks e = tid + n * NTH
+    // of the next K/V tile (2 x BK x DP floats), loaded while the current tile
+    // computes and written to LDS after the next barrier.  Keys >= n_keys and
+    // columns >= dim load as zero.
+    constexpr int CPR = DP / 4;
+    constexpr int NPF = PF ? 2 * BK * CPR / NTH : 1;
+    static_assert(!PF || (2 * BK * CPR) % NTH == 0, "prefetch split");
+    f4 pf[NPF];
+    auto fetch = [&](int k0) {
+#pragma unroll
+        for (int n = 0; n < NPF; ++n) {
+            const int e = tid + n * NTH;
+            const int arr = e / (BK * CPR), r = (e / CPR) % BK, c = (e % CPR) * 4;
+            const int key = k0 + r;
+            const float *src = (arr ? vb : kb) + (size_t)key * kld + c;
+            f4 x = zero4();
+            if (key < a.n_keys && c < a.dim) {
+                if (vec4) {
+                    x = *reinterpret_cast<const f4 *>(src);
+                } else {
+                    const f2 lo = *reinterpret_cast<const f2 *>(src);
+                    x.x = lo.x; x.y = lo.y;
+                    if (c + 2 < a.dim) {
+                        const f2 hi = *reinterpret_cast<const f2 *>(src + 2);
+                        x.z = hi.x; x.w = hi.y;
+                    }
+                }
+            }
+            pf[n] = x;
+        }
+    };
+    if constexpr (PF) fetch(0);
+
     for (int k0 = 0; k0 < kend_wg; k0 += BK) {
         __syncthreads();
-        const int nvalid = min(BK, a.n_keys - k0);
-        stage_rows<DP, LW, 64 * NW>(Ks, kb + (size_t)k0 * kld, kld, BK, nvalid, a.dim, vec4, tid);
-        stage_rows_t<DP, LT, 64 * NW>(Vt, vb + (size_t)k0 * kld, kld, BK, nvalid, a.dim, vec4, tid);
-        __syncthreads();
+        if constexpr (PF) {
+#pragma unroll
+            for (int n = 0; n < NPF; ++n) {
+                const int e = tid + n * NTH;
+                const int arr = e / (BK * CPR), r = (e / CPR) % BK, c = (e % CPR) * 4;
+                *reinterpret_cast<f4 *>((arr ? Vs : Ks) + r * LW + c) = pf[n];
+            }
+            __syncthreads();
+            if (k0 + BK < kend_wg) fetch(k0 + BK);
+        } else {
+            const int nvalid = min(BK, a.n_keys - k0);
+            stage_rows<DP, LW, NTH>(Ks, kb + (size_t)k0 * kld, kld, BK, nvalid, a.dim, vec4, tid);
+            stage_rows<DP, LW, NTH>(Vs, vb + (size_t)k0 * kld, kld, BK, nvalid, a.dim, vec4, tid);
+            __syncthreads();
+        }
         if (k0 >= kend_w) continue;  // wave-uniform: nothing here is visible to this wave
 
         // Scores for every 16-key sub-block, the NJ accumulation chains
@@ -117,15 +161,13 @@ __device__ __forceinline__ void attn_fwd_body(const FwdArgs &a) {
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
             if (k0 + 16 * j >= kend_w) continue;
-            // A operand V^T[n = 16 i + l16][key = 16 j + 4 grp + kk], kk = 0..3: one 128-bit read.
-            const float *vcol = Vt + l16 * LT + 16 * j + 4 * grp;
 #pragma unroll
-            for (int i = 0; i < NT; ++i) {
-                const f4 vx = *reinterpret_cast<const f4 *>(vcol + 16 * i * LT);
-                o[i] = mfma16(vx.x, s[j][0], o[i]);
-                o[i] = mfma16(vx.y, s[j][1], o[i]);
-                o[i] = mfma16(vx.z, s[j][2], o[i]);
-                o[i] = mfma16(vx.w, s[j][3], o[i]);
+            for (int kk = 0; kk < 4; ++kk) {
+                // A operand V^T in the row-owner layout: V[key 16 j + 4 grp + kk][l16 * NT + i].
+                float vx[NT];
+                lds_run<NT>(vx, Vs + (16 * j + 4 * grp + kk) * LW + l16 * NT);
+#pragma unroll
+                for (int i = 0; i < NT; ++i) o[i] = mfma16(vx[i], s[j][kk], o[i]);
             }
         }
     }
@@ -134,16 +176,24 @@ __device__ __forceinline__ void attn_fwd_body(const FwdArgs &a) {
     if (my_row < a.T) {
         float *orow = a.out + (size_t)b * a.T * qld + (size_t)my_row * qld + (size_t)h * a.dim;
 #pragma unroll
-        for (int i = 0; i < NT; ++i) store4(orow, 16 * i + 4 * grp, a.dim, vec4, o[i] * inv);
+        for (int r = 0; r < 4; ++r) store_run<NT>(orow, (4 * grp + r) * NT, a.dim, vec4, o, r, inv);
     }
 }
 
 #define ZT_FWD(DP, BK)                                                                             \
     extern "C" __global__ void __launch_bounds__(256) zt_fwd_d##DP##_k##BK(FwdArgs a) {          \
-        attn_fwd_body<DP, BK, 4>(a);                                                               \
+        attn_fwd_body<DP, BK, 4, false>(a);                                                        \
     }                                                                                              \
     extern "C" __global__ void __launch_bounds__(512) zt_fwd8_d##DP##_k##BK(FwdArgs a) {         \
-        attn_fwd_body<DP, BK, 8>(a);                                                               \
+        attn_fwd_body<DP, BK, 8, false>(a);                                                        \
+    }
+// Register-prefetched variants (32-key tiles).
+#define ZT_FWD_PF(DP)                                                                              \
+    extern "C" __global__ void __launch_bounds__(256) zt_fwdp_d##DP##_k32(FwdArgs a) {           \
+        attn_fwd_body<DP, 32, 4, true>(a);                                                         \
+    }                                                                                              \
+    extern "C" __global__ void __launch_bounds__(512, (DP) <= 128 ? 4 : 1) zt_fwd8p_d##DP##_k32(FwdArgs a) { \
+        attn_fwd_body<DP, 32, 8, true>(a);                                                         \
     }
 
 ZT_FWD(32, 32) ZT_FWD(32, 64)
@@ -154,3 +204,5 @@ ZT_FWD(160, 32) ZT_FWD(160, 64)
 ZT_FWD(192, 32) ZT_FWD(192, 64)
 ZT_FWD(224, 32) ZT_FWD(224, 64)
 ZT_FWD(256, 32) ZT_FWD(256, 64)
+ZT_FWD_PF(32) ZT_FWD_PF(64) ZT_FWD_PF(96) ZT_FWD_PF(128)
+ZT_FWD_PF(160) ZT_FWD_PF(192) ZT_FWD_PF(224) ZT_FWD_PF(256)

@@ -11,6 +11,12 @@
 //     owns d in [grp*DP/4, (grp+1)*DP/4); k-step kk uses d = grp*DP/4 + kk.  A
 //     sum is order-free across k-steps, so each lane then reads DP/4
 //     contiguous floats of a row (128-bit loads) instead of a strided column.
+//   * Products whose output rows run over the head dimension (O^T, dq^T, dK^T,
+//     dV^T) use the "row-owner" layout: output row i (0..15) of column tile it
+//     (0..NT-1, NT = DP/16) is d = i * NT + it.  The A operand a lane needs for
+//     one k-step -- row i = l16 of every tile -- is then NT consecutive floats
+//     of one row-major LDS row (128- or 64-bit reads, lds_run), and accumulator
+//     row 4*grp + r holds NT consecutive d of one output row (store_run).
 //   * Scores are kept transposed (keys on the M axis, queries on the N axis):
 //     the C layout of S^T (lane = query column, 4 key rows per register group)
 //     is then exactly the B-operand layout the P.V product needs, with key
@@ -80,6 +86,44 @@ DEVI void store4(float *row, int c0, int dim, bool vec4, f4 x) {
     }
 }
 
+// Reads the NT floats p[0..NT) (the row-owner A operand): 128-bit reads when
+// NT % 4 == 0 (p then 16-byte aligned), else 64-bit reads.
+template <int NT>
+DEVI void lds_run(float (&x)[NT], const float *p) {
+    if constexpr (NT % 4 == 0) {
+#pragma unroll
+        for (int i = 0; i < NT; i += 4) {
+            const f4 v = *reinterpret_cast<const f4 *>(p + i);
+            x[i] = v.x; x[i + 1] = v.y; x[i + 2] = v.z; x[i + 3] = v.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < NT; i += 2) {
+            const f2 v = *reinterpret_cast<const f2 *>(p + i);
+            x[i] = v.x; x[i + 1] = v.y;
+        }
+    }
+}
+
+// Stores row r of row-owner accumulators, acc[it][r] * mul for it = 0..NT-1,
+// to row[c0 .. c0 + NT), c0 = (4 grp + r) * NT; columns >= dim are dropped.
+// 128-bit stores when rows are 16-byte aligned (vec4) and NT % 4 == 0, else
+// 64-bit stores (dim and c0 are even, so a pair never straddles dim).
+template <int NT>
+DEVI void store_run(float *row, int c0, int dim, bool vec4, const f4 (&acc)[NT], int r, float mul) {
+    if (NT % 4 == 0 && vec4) {
+#pragma unroll
+        for (int i = 0; i < NT; i += 4)
+            if (c0 + i < dim)
+                *reinterpret_cast<f4 *>(row + c0 + i) =
+                    f4{acc[i][r], acc[i + 1][r], acc[i + 2][r], acc[i + 3][r]} * mul;
+    } else {
+#pragma unroll
+        for (int i = 0; i < NT; i += 2)
+            if (c0 + i < dim) *reinterpret_cast<f2 *>(row + c0 + i) = f2{acc[i][r], acc[i + 1][r]} * mul;
+    }
+}
+
 // Cooperative copy of `rows` rows x DP columns (global row stride `ld`
 // floats) into LDS rows of stride LDSW floats.  Rows >= nvalid and columns
 // >= dim are written as zero.  NT threads take part.
@@ -122,6 +166,26 @@ DEVI void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 // XOR stays inside an aligned group of M+1 chunks, so a row maps onto itself.
 template <int CPR>
 DEVI int swz(int chunk, int row) { return chunk ^ (row & (CPR % 16 == 0 ? 15 : 7)); }
+
+// Same from a swizzled unpadded tile (see swz): columns [c0, c0 + NT) of row r.
+template <int NT, int CPR>
+DEVI void lds_run_swz(float (&x)[NT], const float *tile, int r, int c0) {
+    const float *rowp = tile + r * CPR * 4;
+    if constexpr (NT % 4 == 0) {
+#pragma unroll
+        for (int i = 0; i < NT; i += 4) {
+            const f4 v = *reinterpret_cast<const f4 *>(rowp + 4 * swz<CPR>((c0 + i) >> 2, r));
+            x[i] = v.x; x[i + 1] = v.y; x[i + 2] = v.z; x[i + 3] = v.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < NT; i += 2) {
+            const int c = c0 + i;  // even: a 64-bit read never leaves its 16-byte chunk
+            const f2 v = *reinterpret_cast<const f2 *>(rowp + 4 * swz<CPR>(c >> 2, r) + (c & 3));
+            x[i] = v.x; x[i + 1] = v.y;
+        }
+    }
+}
 
 // Cooperative copy of `rows` rows x DP columns into LDS TRANSPOSED: element
 // (r, c) lands at lds[c * LT + r] (LT = rows + 4).  Consecutive lanes take

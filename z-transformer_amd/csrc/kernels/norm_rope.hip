@@ -8,9 +8,14 @@
 // norm.zig:41 narrows it, then y = x / rms * w with an IEEE f32 divide and an
 // f32 multiply (norm.zig:44).  Bound: HBM (8 bytes per element + the gain).
 //
-// zt_rope: src/rope.zig:21-55 (half-split pairs i <-> i + d/2, f64 angle
-// t / theta^(2i/d), f64 multiply-adds, one narrowing).  Used to prepare
-// RoPE-rotated inputs.
+// zt_rope / zt_rope_bwd: src/rope.zig:21-55 and its transpose
+// src/autograd.zig:851-872 (half-split pairs i <-> i + d/2, f64 angle
+// t / theta^(2i/d), f64 products, one narrowing).  The angle depends on
+// (position, i) only, so one thread computes pow, cos and sin once and applies
+// them to pair i of every head of the row -- of q and k together when both are
+// given -- which keeps the f64 transcendentals off the critical path and the
+// kernel near HBM speed.  Products and sums are kept as separate roundings
+// (no fused multiply-add), as the reference computes them.
 //
 // zt_fill_normal / zt_fill_uniform: counter-based splitmix64 -> Box-Muller,
 // element i from counters 2i and 2i+1, so a buffer of any size is filled in
@@ -93,97 +98,86 @@ ZT_RMS(16)
 extern "C" __global__ void __launch_bounds__(256) zt_rmsnorm_any(NormArgs a) { rms_any(a); }
 
 
-// Transposed rotation, src/autograd.zig:851-872: (lo c + hi s, hi c - lo s).
-extern "C" __global__ void __launch_bounds__(256) zt_rope_bwd(RopeArgs a) {
-    const int half = a.head_dim / 2;
-    const int heads = a.cols / a.head_dim;
-    const long long total = (long long)a.rows * heads * half;
-    for (long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x; e < total;
-         e += (long long)gridDim.x * blockDim.x) {
-        const int i = (int)(e % half);
-        const long long rh = e / half;
-        const int h = (int)(rh % heads);
-        const int r = (int)(rh / heads);
-        const double t = (double)(a.pos + r);
-        const double exponent = (double)(2 * i) / (double)a.head_dim;
-        const double angle = t / pow(a.theta, exponent);
-        const double c = cos(angle), s = sin(angle);
-        const size_t base = (size_t)r * a.cols + (size_t)h * a.head_dim;
-        const double lo = (double)a.x[base + i], hi = (double)a.x[base + i + half];
-        a.y[base + i] = (float)(lo * c + hi * s);
-        a.y[base + i + half] = (float)(hi * c - lo * s);
-    }
-}
+#pragma clang fp contract(off)
 
-extern "C" __global__ void __launch_bounds__(256) zt_rope(RopeArgs a) {
-    const int half = a.head_dim / 2;
-    const int heads = a.cols / a.head_dim;
-    const long long total = (long long)a.rows * heads * half;
-    for (long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x; e < total;
-         e += (long long)gridDim.x * blockDim.x) {
-        const int i = (int)(e % half);
-        const long long rh = e / half;
-        const int h = (int)(rh % heads);
-        const int r = (int)(rh / heads);
-        const double t = (double)(a.pos + r);
-        const double exponent = (double)(2 * i) / (double)a.head_dim;
-        const double angle = t / pow(a.theta, exponent);
-        const double c = cos(angle), s = sin(angle);
-        const size_t base = (size_t)r * a.cols + (size_t)h * a.head_dim;
-        const double lo = (double)a.x[base + i], hi = (double)a.x[base + i + half];
-        a.y[base + i] = (float)(lo * c - hi * s);
-        a.y[base + i + half] = (float)(hi * c + lo * s);
-    }
-}
-
-
-// RoPE rotation of the pair (lo, hi) = (x[i], x[i + d/2]) at position t, as
-// src/rope.zig:37-50: f64 angle t / theta^(2i/d), f64 multiply-adds.
-DEVI void rope_pair(double t, int i, int head_dim, double theta, float lo_in, float hi_in, float *lo_out,
-                    float *hi_out) {
+// cos and sin of the RoPE angle of pair i at position t (src/rope.zig:40-43).
+DEVI void rope_angle(double t, int i, int head_dim, double theta, double *c, double *s) {
     const double exponent = (double)(2 * i) / (double)head_dim;
     const double angle = t / pow(theta, exponent);
-    const double c = cos(angle), s = sin(angle);
-    const double lo = (double)lo_in, hi = (double)hi_in;
-    *lo_out = (float)(lo * c - hi * s);
-    *hi_out = (float)(hi * c + lo * s);
+    *c = cos(angle);
+    *s = sin(angle);
 }
 
-// Decode-step cache update, one thread per element task: rotated q pairs,
-// rotated k pairs written to cache row pos[b], v elements copied to row pos[b]
-// (src/decode.zig:244-259: rope.forward on q and k at pos, cache append).
-extern "C" __global__ void __launch_bounds__(256) zt_rope_append(AppendArgs a) {
-    const int half = a.dim / 2;
-    const long long nq = (long long)a.nb * a.H * half;
-    const long long nk = (long long)a.nb * a.Hkv * half;
-    const long long nv = (long long)a.nb * a.Hkv * a.dim;
-    const size_t qld = (size_t)a.H * a.dim, kld = (size_t)a.Hkv * a.dim;
-    for (long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x; e < nq + nk + nv;
+// Rotates the pair (lo, hi): forward (rope.zig:47-48) lo c - hi s, hi c + lo s;
+// backward, the transpose (autograd.zig:867-868), lo c + hi s, hi c - lo s.
+template <bool BWD>
+DEVI void rope_rotate(double c, double s, const float *x, float *y, int half) {
+    const double lo = (double)x[0], hi = (double)x[half];
+    const double lc = lo * c, hs = hi * s, hc = hi * c, ls = lo * s;
+    y[0] = (float)(BWD ? lc + hs : lc - hs);
+    y[half] = (float)(BWD ? hc - ls : hc + ls);
+}
+
+template <bool BWD>
+DEVI void rope_rows(const RopeArgs &a) {
+    const int half = a.head_dim / 2;
+    const size_t ld1 = (size_t)a.heads1 * a.head_dim, ld2 = (size_t)a.heads2 * a.head_dim;
+    const long long total = (long long)a.rows * half;
+    for (long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x; e < total;
          e += (long long)gridDim.x * blockDim.x) {
-        if (e < nq) {
-            const int i = (int)(e % half);
-            const long long bh = e / half;
-            const int h = (int)(bh % a.H), bl = (int)(bh / a.H);
-            const size_t o = (size_t)(a.b_base + bl) * qld + (size_t)h * a.dim;
-            rope_pair((double)a.pos[bl], i, a.dim, a.theta, a.q[o + i], a.q[o + i + half], &a.q_pos[o + i],
-                      &a.q_pos[o + i + half]);
-        } else if (e < nq + nk) {
-            const long long f = e - nq;
-            const int i = (int)(f % half);
-            const long long bh = f / half;
-            const int h = (int)(bh % a.Hkv), bl = (int)(bh / a.Hkv);
-            const int b = a.b_base + bl;
-            const size_t src = (size_t)b * kld + (size_t)h * a.dim;
-            const size_t dst = ((size_t)b * a.n_ctx + a.pos[bl]) * kld + (size_t)h * a.dim;
-            rope_pair((double)a.pos[bl], i, a.dim, a.theta, a.k[src + i], a.k[src + i + half], &a.kc[dst + i],
-                      &a.kc[dst + i + half]);
+        const int i = (int)(e % half);
+        const int r = (int)(e / half);
+        double c, s;
+        rope_angle((double)(a.pos + r % a.seq_len), i, a.head_dim, a.theta, &c, &s);
+        const float *x1 = a.x1 + (size_t)r * ld1 + i;
+        float *y1 = a.y1 + (size_t)r * ld1 + i;
+        for (int h = 0; h < a.heads1; ++h)
+            rope_rotate<BWD>(c, s, x1 + (size_t)h * a.head_dim, y1 + (size_t)h * a.head_dim, half);
+        const float *x2 = a.x2 + (size_t)r * ld2 + i;
+        float *y2 = a.y2 + (size_t)r * ld2 + i;
+        for (int h = 0; h < a.heads2; ++h)
+            rope_rotate<BWD>(c, s, x2 + (size_t)h * a.head_dim, y2 + (size_t)h * a.head_dim, half);
+    }
+}
+
+extern "C" __global__ void __launch_bounds__(256) zt_rope(RopeArgs a) { rope_rows<false>(a); }
+extern "C" __global__ void __launch_bounds__(256) zt_rope_bwd(RopeArgs a) { rope_rows<true>(a); }
+
+// Decode-step cache update (src/decode.zig:244-259: rope.forward on q and k
+// at pos, cache append).  A sequence's work -- (H + Hkv) * d/2 pair rotations
+// and Hkv * d copies of the new v into cache row pos[b] -- is cut into
+// 256-task blocks, blockIdx.x = sequence * blocks_per_seq + piece.  Each block
+// first tabulates cos / sin of its sequence's d/2 angles in LDS (one f64 pow,
+// cos, sin per pair), then every thread does one task, so the launch is wide
+// and a thread's loads do not queue behind one another.
+extern "C" __global__ void __launch_bounds__(256) zt_rope_append(AppendArgs a) {
+    __shared__ double tab_c[ZT_MAX_DIM / 2], tab_s[ZT_MAX_DIM / 2];
+    const int half = a.dim / 2;
+    const int n_rot = (a.H + a.Hkv) * half;
+    const int tasks = n_rot + a.Hkv * a.dim;
+    const int per_seq = (tasks + 255) / 256;
+    const int bl = blockIdx.x / per_seq, piece = blockIdx.x % per_seq;
+    if (bl >= a.nb) return;  // block-uniform
+    const int b = a.b_base + bl;
+    const int pos = a.pos[bl];
+    for (int i = threadIdx.x; i < half; i += blockDim.x) rope_angle((double)pos, i, a.dim, a.theta, &tab_c[i], &tab_s[i]);
+    __syncthreads();
+    const int j = piece * 256 + threadIdx.x;
+    if (j >= tasks) return;
+    const size_t qld = (size_t)a.H * a.dim, kld = (size_t)a.Hkv * a.dim;
+    if (j < n_rot) {
+        const int h = j / half, i = j % half;
+        if (h < a.H) {
+            const size_t o = (size_t)b * qld + (size_t)h * a.dim + i;
+            rope_rotate<false>(tab_c[i], tab_s[i], a.q + o, a.q_pos + o, half);
         } else {
-            const long long f = e - nq - nk;
-            const int c = (int)(f % kld);
-            const int bl = (int)(f / kld);
-            const int b = a.b_base + bl;
-            a.vc[((size_t)b * a.n_ctx + a.pos[bl]) * kld + c] = a.v[(size_t)b * kld + c];
+            const size_t col = (size_t)(h - a.H) * a.dim + i;
+            rope_rotate<false>(tab_c[i], tab_s[i], a.k + (size_t)b * kld + col,
+                               a.kc + ((size_t)b * a.n_ctx + pos) * kld + col, half);
         }
+    } else {
+        const int c = j - n_rot;
+        a.vc[((size_t)b * a.n_ctx + pos) * kld + c] = a.v[(size_t)b * kld + c];
     }
 }
 

@@ -35,7 +35,7 @@ extern const unsigned char zt_co_misc[], zt_co_misc_end[];
 
 namespace {
 
-constexpr int kMinDim = 32, kMaxDim = 256;
+constexpr int kMinDim = 32, kMaxDim = ZT_MAX_DIM;
 constexpr int kMaxDevices = 64;
 constexpr int kThreads = 256;
 
@@ -139,17 +139,19 @@ int pad32(int dim) { return (dim + 31) / 32 * 32; }
 int heads_per_wg(int group) { return group % 4 == 0 ? 4 : (group % 2 == 0 ? 2 : 1); }
 
 // Key tile (keys staged in LDS per step) for a width and a caller cap: 64 or
-// 32.  Measured on MI355X (C2/C3/C5 shapes): the dq kernel prefers 64 keys;
-// the forward prefers 64 only at d <= 64 -- above that the 32-key tile keeps
-// one more workgroup resident per CU (C5, d = 256: 0.84 ms vs 1.11 ms).
+// 32.  Measured on MI355X (C2/C3/C5 shapes): the dq kernel takes 32 keys with
+// the next tile prefetched into registers (C3 2.43 -> 2.23 ms, C2 0.132 ->
+// 0.119 ms, C5 1.74 -> 1.65 ms against 64 keys without); the forward prefers
+// 64 only at d <= 64 -- above that the 32-key tile keeps one more workgroup
+// resident per CU (C5, d = 256: 0.84 ms vs 1.11 ms).
 enum class Tiled { Forward, Dq };
 int key_tile(Tiled which, int dp, int max_tile) {
-    const int dflt = (which == Tiled::Forward && dp > 64) ? 32 : 64;
+    const int dflt = (which == Tiled::Forward && dp <= 64) ? 64 : 32;
     const int preferred = env_choice("ZT_ATTN_BK", dflt, {32, 64});
     return max_tile >= 64 ? preferred : 32;
 }
-// LDS per workgroup: forward = K tile + transposed V tile; dq = K and V tiles.
-size_t fwd_tile_bytes(int dp, int bk) { return ((size_t)bk * (dp + 4) + (size_t)dp * (bk + 4)) * sizeof(float); }
+// LDS per workgroup: K and V tiles, row-major with a 4-float pad.
+size_t fwd_tile_bytes(int dp, int bk) { return (size_t)2 * bk * (dp + 4) * sizeof(float); }
 size_t kv_tile_bytes(int dp, int bk) { return (size_t)2 * bk * (dp + 4) * sizeof(float); }
 
 // Waves per forward / dq workgroup (4 or 8): eight waves share each staged K/V
@@ -157,6 +159,18 @@ size_t kv_tile_bytes(int dp, int bk) { return (size_t)2 * bk * (dp + 4) * sizeof
 // gains when four query heads share a kv group (C3 1.39 -> 1.33 ms, C5 0.84 ->
 // 0.76 ms) and loses for MHA (C2); the dq kernel loses at every shape tried.
 int fwd_waves(int hw) { return env_choice("ZT_ATTN_FWD_W", hw == 4 ? 8 : 4, {4, 8}); }
+
+// Forward kernel name: waves per workgroup, key tile, and for 32-key tiles the
+// register-prefetched variant (ZT_ATTN_FPF; default with eight waves, where
+// it measured C3 1.315 -> 1.225 ms and C5 0.758 -> 0.630 ms; with four waves
+// the prefetch registers cost occupancy and it loses).
+void fwd_kernel_name(char *name, size_t len, int dp, int bk, int nw) {
+    const bool pf = bk == 32 && env_choice("ZT_ATTN_FPF", nw == 8 ? 1 : 0, {0, 1}) == 1;
+    if (pf)
+        snprintf(name, len, nw == 8 ? "zt_fwd8p_d%d_k32" : "zt_fwdp_d%d_k32", dp);
+    else
+        snprintf(name, len, nw == 8 ? "zt_fwd8_d%d_k%d" : "zt_fwd_d%d_k%d", dp, bk);
+}
 int dq_waves(int dp) {
     const int w = env_choice("ZT_ATTN_DQ_W", 4, {4, 8});
     return dp > 192 ? 4 : w;  // eight-wave dq spills above d = 192
@@ -281,7 +295,7 @@ int forward_impl(const float *q, const float *k, const float *v, float *out, int
     const unsigned long long blocks = (unsigned long long)a.n_row_tiles * a.n_head_blocks * B;
     if (!grid_ok(blocks)) return 1;
     char name[64];
-    snprintf(name, sizeof name, nw == 8 ? "zt_fwd8_d%d_k%d" : "zt_fwd_d%d_k%d", dp, bk);
+    fwd_kernel_name(name, sizeof name, dp, bk, nw);
     return launch(st, name, (unsigned)blocks, a, stream, 64u * nw);
 }
 
@@ -355,10 +369,15 @@ int backward_prepare(const float *q, const float *k, const float *v, const float
     a->scale_log2e = (float)(1.4426950408889634 / std::sqrt((double)dim));
     const unsigned long long blocks_a = (unsigned long long)a->n_row_tiles * a->n_head_blocks * B;
     if (!grid_ok(blocks_a) || !grid_ok(blocks_b)) return 1;
-    snprintf(name_dq, 64, nw_dq == 8 ? "zt_bwd_dq8_d%d_k%d" : "zt_bwd_dq_d%d_k%d", dp, bk);
+    const bool qpf = bk == 32 && env_choice("ZT_ATTN_QPF", 1, {0, 1}) == 1;
+    if (qpf)
+        snprintf(name_dq, 64, nw_dq == 8 ? "zt_bwd_dq8p_d%d_k32" : "zt_bwd_dqp_d%d_k32", dp);
+    else
+        snprintf(name_dq, 64, nw_dq == 8 ? "zt_bwd_dq8_d%d_k%d" : "zt_bwd_dq_d%d_k%d", dp, bk);
     *threads_dq = 64u * nw_dq;
+    const bool pf = env_choice("ZT_ATTN_PF", 1, {0, 1}) == 1;
     if (wide)
-        snprintf(name_dkdv, 64, "zt_bwd_dkdv8_d%d_hs2", dp);
+        snprintf(name_dkdv, 64, pf ? "zt_bwd_dkdv8p_d%d_hs2" : "zt_bwd_dkdv8_d%d_hs2", dp);
     else
         snprintf(name_dkdv, 64, dma ? "zt_bwd_dkdv_dma_d%d_hs%d" : "zt_bwd_dkdv_d%d_hs%d", dp, hs);
     *threads_dkdv = wide ? 512 : kThreads;
@@ -605,9 +624,10 @@ int zt_attn_decode_step(const float *q, const float *k_new, const float *v_new, 
         ap.b_base = b0;
         ap.nb = B - b0 < ZT_DEC_MAXB ? B - b0 : ZT_DEC_MAXB;
         for (int i = 0; i < ap.nb; ++i) ap.pos[i] = pos[b0 + i];
-        const long long work = (long long)ap.nb * (n_heads + 2 * n_kv_heads) * dim;
-        long long blocks = (work + kThreads - 1) / kThreads;
-        if (blocks > 65536) blocks = 65536;
+        // One block per 256 tasks of a sequence: (H + Hkv) * dim/2 rotations + Hkv * dim copies.
+        const long long tasks = (long long)(n_heads + n_kv_heads) * (dim / 2) + (long long)n_kv_heads * dim;
+        const long long blocks = (long long)ap.nb * ((tasks + kThreads - 1) / kThreads);
+        if (!grid_ok((unsigned long long)blocks)) return 1;
         if (launch(st, "zt_rope_append", (unsigned)blocks, ap, stream)) return 1;
     }
     for (int b = 0; b < B; ++b) n_keys[b] = pos[b] + 1;
@@ -647,20 +667,26 @@ int zt_rmsnorm_forward(const float *x, const float *w, float *y, int rows, int c
     return launch(st, name, (unsigned)rows, a, stream);
 }
 
-static int rope_impl(const char *name, const float *x, float *y, int rows, int cols, int pos, double theta,
-                     int head_dim, hipStream_t stream) {
+// rows = B * T rows of tensor 1 (heads1 heads) and, when x2 is given, of
+// tensor 2 (heads2 heads); row r at position pos + r % T.
+static int rope_impl(const char *name, const float *x1, float *y1, const float *x2, float *y2, int B, int T,
+                     int heads1, int heads2, int pos, double theta, int head_dim, hipStream_t stream) {
     if (head_dim <= 0 || head_dim % 2 != 0) {
         fprintf(stderr, "zt_rope: head_dim %d is odd or not positive.\n", head_dim);
         return 1;
     }
-    if (rows < 0 || cols < 0 || cols % head_dim != 0 || pos < 0) {
-        fprintf(stderr, "zt_rope: %d rows of %d columns is not a whole number of %d-wide heads.\n", rows, cols,
-                head_dim);
+    if (B < 0 || T < 0 || heads1 < 0 || heads2 < 0 || pos < 0 || (long long)B * T > INT32_MAX) {
+        fprintf(stderr, "zt_rope: %d x %d rows of %d + %d heads at position %d is not launchable.\n", B, T, heads1,
+                heads2, pos);
         return 1;
     }
-    const long long work = (long long)rows * (cols / 2);
-    if (work == 0) return 0;
-    if (!x || !y) {
+    if (!(theta > 0.0)) {
+        fprintf(stderr, "zt_rope: theta %g is not usable.\n", theta);
+        return 1;
+    }
+    const long long work = (long long)B * T * (head_dim / 2);
+    if (work == 0 || heads1 + heads2 == 0) return 0;
+    if (!x1 || !y1 || (heads2 > 0 && (!x2 || !y2))) {
         fprintf(stderr, "zt_rope: a null tensor pointer is not launchable.\n");
         return 1;
     }
@@ -669,20 +695,46 @@ static int rope_impl(const char *name, const float *x, float *y, int rows, int c
         fprintf(stderr, "zt_rope: no usable gfx950 device or code object.\n");
         return 1;
     }
-    RopeArgs a{x, y, rows, cols, pos, head_dim, theta};
+    RopeArgs a{x1, heads2 > 0 ? x2 : nullptr, y1, heads2 > 0 ? y2 : nullptr, B * T, T, heads1, heads2, pos,
+               head_dim, theta};
     long long blocks = (work + kThreads - 1) / kThreads;
     if (blocks > 65536) blocks = 65536;
     return launch(st, name, (unsigned)blocks, a, stream);
 }
 
+static int rope_one(const char *name, const float *x, float *y, int rows, int cols, int pos, double theta,
+                    int head_dim, hipStream_t stream) {
+    if (head_dim <= 0 || head_dim % 2 != 0) {
+        fprintf(stderr, "zt_rope: head_dim %d is odd or not positive.\n", head_dim);
+        return 1;
+    }
+    if (rows < 0 || cols < 0 || cols % head_dim != 0) {  // src/rope.zig:30: DimensionMismatch
+        fprintf(stderr, "zt_rope: %d rows of %d columns is not a whole number of %d-wide heads.\n", rows, cols,
+                head_dim);
+        return 1;
+    }
+    return rope_impl(name, x, y, nullptr, nullptr, 1, rows, cols / head_dim, 0, pos, theta, head_dim, stream);
+}
+
 int zt_rope_forward(const float *x, float *y, int rows, int cols, int pos, double theta, int head_dim,
                     hipStream_t stream) {
-    return rope_impl("zt_rope", x, y, rows, cols, pos, theta, head_dim, stream);
+    return rope_one("zt_rope", x, y, rows, cols, pos, theta, head_dim, stream);
 }
 
 int zt_rope_backward(const float *dout, float *din, int rows, int cols, int pos, double theta, int head_dim,
                      hipStream_t stream) {
-    return rope_impl("zt_rope_bwd", dout, din, rows, cols, pos, theta, head_dim, stream);
+    return rope_one("zt_rope_bwd", dout, din, rows, cols, pos, theta, head_dim, stream);
+}
+
+int zt_rope_qk_forward(const float *q, const float *k, float *q_out, float *k_out, int B, int T, int n_heads,
+                       int n_kv_heads, int head_dim, int pos, double theta, hipStream_t stream) {
+    return rope_impl("zt_rope", q, q_out, k, k_out, B, T, n_heads, n_kv_heads, pos, theta, head_dim, stream);
+}
+
+int zt_rope_qk_backward(const float *dq, const float *dk, float *dq_out, float *dk_out, int B, int T,
+                        int n_heads, int n_kv_heads, int head_dim, int pos, double theta, hipStream_t stream) {
+    return rope_impl("zt_rope_bwd", dq, dq_out, dk, dk_out, B, T, n_heads, n_kv_heads, pos, theta, head_dim,
+                     stream);
 }
 
 static int fill_impl(const char *name, float *dst, size_t n, uint64_t seed, double p0, double p1,
@@ -721,8 +773,7 @@ int zt_attn_plan(int B, int T, int n_heads, int n_kv_heads, int dim, int max_til
     const int dp = pad32(dim);
     int bk = key_tile(Tiled::Forward, dp, max_tile);
     if (fwd_tile_bytes(dp, bk) > st->lds_limit) bk = 32;
-    snprintf(fwd, len, fwd_waves(heads_per_wg(n_heads / n_kv_heads)) == 8 ? "zt_fwd8_d%d_k%d" : "zt_fwd_d%d_k%d", dp,
-             bk);
+    fwd_kernel_name(fwd, len, dp, bk, fwd_waves(heads_per_wg(n_heads / n_kv_heads)));
     BwdArgs a;
     DeviceState *st2 = nullptr;
     unsigned ba = 0, bb = 0, ta = 0, tb = 0;

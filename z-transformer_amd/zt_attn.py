@@ -20,7 +20,8 @@ ABI_SYMBOLS = [
     "zt_attn_forward", "zt_attn_backward",
     "zt_attn_forward_batched", "zt_attn_backward_batched", "zt_attn_bwd_dq", "zt_attn_bwd_dkdv",
     "zt_attn_decode_workspace", "zt_attn_decode", "zt_attn_decode_step_workspace", "zt_attn_decode_step",
-    "zt_rmsnorm_forward", "zt_rope_forward", "zt_rope_backward", "zt_fill_normal", "zt_fill_uniform", "zt_attn_version",
+    "zt_rmsnorm_forward", "zt_rope_forward", "zt_rope_backward", "zt_rope_qk_forward",
+    "zt_rope_qk_backward", "zt_fill_normal", "zt_fill_uniform", "zt_attn_version",
     "zt_attn_lds_limit", "zt_attn_plan",
 ]
 HOLDER_SYMBOLS = [
@@ -67,6 +68,8 @@ def lib():
             "zt_rmsnorm_forward": (I, [P, P, P, I, I, D, P]),
             "zt_rope_forward": (I, [P, P, I, I, I, D, I, P]),
             "zt_rope_backward": (I, [P, P, I, I, I, D, I, P]),
+            "zt_rope_qk_forward": (I, [P, P, P, P, I, I, I, I, I, I, D, P]),
+            "zt_rope_qk_backward": (I, [P, P, P, P, I, I, I, I, I, I, D, P]),
             "zt_fill_normal": (I, [P, Z, U64, D, D, P]),
             "zt_fill_uniform": (I, [P, Z, U64, D, D, P]),
             "zt_attn_version": (ctypes.c_char_p, []),
@@ -208,6 +211,14 @@ def rope_backward(dout, din, rows, cols, pos, theta, head_dim, stream=None):
     _f32_cuda(dout, din)
     _check(lib().zt_rope_backward(_ptr(dout), _ptr(din), rows, cols, pos, theta, head_dim, _stream(stream)),
            "zt_rope_backward")
+
+
+def rope_qk(q, k, q_out, k_out, B, T, n_heads, n_kv_heads, head_dim, pos=0, theta=500000.0, backward=False,
+            stream=None):
+    _f32_cuda(q, k, q_out, k_out)
+    fn = lib().zt_rope_qk_backward if backward else lib().zt_rope_qk_forward
+    _check(fn(_ptr(q), _ptr(k), _ptr(q_out), _ptr(k_out), B, T, n_heads, n_kv_heads, head_dim, pos, theta,
+              _stream(stream)), "zt_rope_qk")
 
 
 def fill_normal(t, seed, mean=0.0, sigma=1.0, stream=None):
