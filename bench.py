@@ -1,12 +1,16 @@
 #!/usr/bin/env python3
 """Benchmark of the fused causal GQA attention path on one MI355X.
 
-A step is one forward (zt_attn_forward) plus one backward (zt_attn_backward)
-over BASELINE.json's C3 workload: B=1, T=4096, 32 query / 8 kv heads,
+A step is one attention forward plus backward of a training step
+(zt_attn_forward_train, which keeps each row's log-sum-exp, then
+zt_attn_backward_train) over BASELINE.json's C3 workload: B=1, T=4096, 32 query / 8 kv heads,
 head_dim 128, f32, RoPE (theta 500000) pre-applied to Q and K, all inputs
 seeded N(0,1) on the device and resident in HBM before timing.  The headline
 value is fwd+bwd TFLOP/s with the causal-pair FLOP count
-(fwd 2*B*H*d*T(T+1), bwd 5*B*H*d*T(T+1)).  The same line also carries the
+(fwd 2*B*H*d*T(T+1), bwd 5*B*H*d*T(T+1)).  The reference's own entry points
+(zt_attn_forward + zt_attn_backward, whose backward rebuilds the softmax
+statistics) are timed on the same inputs under "reference_abi".  The same
+line also carries the
 decode step (C4: B=64, 8192 cached keys, GB/s of K/V/q/out) and RMSNorm
 ([64,4096] and [4096,4096], GB/s over rotating buffers larger than the 256 MB
 MALL), per-kernel times from HIP events on the launch stream, the roofline of
@@ -95,65 +99,78 @@ def main():
     out, dq = torch.empty_like(q), torch.empty_like(q)
     dk, dv = torch.empty_like(k), torch.empty_like(v)
     rm, rl, rd = (torch.empty(B * T * H, device=dev) for _ in range(3))
-
-    def fwd():
-        zt.forward(q, k, v, out, T, H, Hkv, D)
-
-    def bwd():
-        zt.backward(q, k, v, do, dq, dk, dv, rm, rl, rd, T, H, Hkv, D)
-
-    def bwd_dq():
-        zt.bwd_dq(q, k, v, do, dq, rm, rl, rd, T, H, Hkv, D)
-
-    def bwd_dkdv():
-        zt.bwd_dkdv(q, k, v, do, dk, dv, rm, rl, rd, T, H, Hkv, D)
-
-    def step():
-        fwd()
-        bwd()
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t_wall = time.perf_counter()
-    s.record()
-    for _ in range(args.steps):
-        step()
-    e.record()
-    torch.cuda.synchronize()
-    wall_ms = (time.perf_counter() - t_wall) * 1e3 / args.steps
-    ms_step = s.elapsed_time(e) / args.steps
+    lse, delta = (torch.empty(B * T * H, device=dev) for _ in range(2))
     pairs = B * H * T * (T + 1) / 2          # causal (query, key) pairs over all heads
     unit = 2 * D * pairs                      # FLOPs of one T x T x d causal matmul
     fwd_flop, bwd_flop = 2 * unit, 5 * unit
-    value = (fwd_flop + bwd_flop) / (ms_step * 1e-3) / 1e12
-    log(f"C3 step: {ms_step:.3f} ms (wall {wall_ms:.3f} ms), {value:.2f} TFLOP/s fwd+bwd")
 
-    n_k = max(3, args.steps)
-    t_fwd = event_time(torch, fwd, n_k)
-    bwd_dq()
-    t_dq = event_time(torch, bwd_dq, n_k)
-    t_dkdv = event_time(torch, bwd_dkdv, n_k)
-    # Algorithmic FLOPs per launch: the forward's two matmuls; of the backward's
-    # five (S recompute, dP, dV, dK, dQ) the dk/dv kernel owns four and the dq
-    # kernel one -- the dq kernel's own recompute earns no credit.
-    n_fwd, n_dq, n_dkdv = zt.plan(B, T, H, Hkv, D)
-    kernels = [
-        {"kernel": n_fwd, "ms": t_fwd, "flop": fwd_flop},
-        {"kernel": n_dq, "ms": t_dq, "flop": unit},
-        {"kernel": n_dkdv, "ms": t_dkdv, "flop": 4 * unit},
-    ]
-    for kk in kernels:
-        kk["tflops"] = kk["flop"] / (kk["ms"] * 1e-3) / 1e12
-        kk["frac_mfma_f32"] = kk["tflops"] / PEAK_MFMA_F32
-        log(f"  {kk['kernel']}: {kk['ms']:.3f} ms, {kk['tflops']:.2f} TFLOP/s ({100 * kk['frac_mfma_f32']:.1f}% of "
-            f"FP32 MFMA peak)")
-    fwd_tflops = fwd_flop / (t_fwd * 1e-3) / 1e12
-    bwd_tflops = bwd_flop / ((t_dq + t_dkdv) * 1e-3) / 1e12
-    log(f"  forward {fwd_tflops:.2f} TFLOP/s ({100 * fwd_tflops / PEAK_MFMA_F32:.1f}%), backward "
-        f"{bwd_tflops:.2f} TFLOP/s ({100 * bwd_tflops / PEAK_MFMA_F32:.1f}%)")
+    # The timed step is a training step's attention: the forward keeps each
+    # row's log-sum-exp and the backward uses it (zt_attn_forward_train /
+    # zt_attn_backward_train).  The reference's own entry points, whose
+    # backward rebuilds the statistics, are timed beside it.
+    paths = {
+        "train": dict(
+            fwd=lambda: zt.forward_train(q, k, v, out, lse, T, H, Hkv, D),
+            dq=lambda: zt.bwd_dq_train(q, k, v, out, do, lse, dq, delta, T, H, Hkv, D),
+            dkdv=lambda: zt.bwd_dkdv_train(q, k, v, out, do, lse, delta, dk, dv, T, H, Hkv, D),
+            bwd=lambda: zt.backward_train(q, k, v, out, do, lse, dq, dk, dv, delta, T, H, Hkv, D),
+            names=zt.plan_train(B, T, H, Hkv, D)),
+        "reference_abi": dict(
+            fwd=lambda: zt.forward(q, k, v, out, T, H, Hkv, D),
+            dq=lambda: zt.bwd_dq(q, k, v, do, dq, rm, rl, rd, T, H, Hkv, D),
+            dkdv=lambda: zt.bwd_dkdv(q, k, v, do, dk, dv, rm, rl, rd, T, H, Hkv, D),
+            bwd=lambda: zt.backward(q, k, v, do, dq, dk, dv, rm, rl, rd, T, H, Hkv, D),
+            names=zt.plan(B, T, H, Hkv, D)),
+    }
+    res = {}
+    for pname, pth in paths.items():
+        def step():
+            pth["fwd"]()
+            pth["bwd"]()
+
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t_wall = time.perf_counter()
+        s.record()
+        for _ in range(args.steps):
+            step()
+        e.record()
+        torch.cuda.synchronize()
+        wall_ms = (time.perf_counter() - t_wall) * 1e3 / args.steps
+        ms_step = s.elapsed_time(e) / args.steps
+        val = (fwd_flop + bwd_flop) / (ms_step * 1e-3) / 1e12
+        log(f"C3 step ({pname}): {ms_step:.3f} ms (wall {wall_ms:.3f} ms), {val:.2f} TFLOP/s fwd+bwd")
+
+        n_k = max(3, args.steps)
+        t_fwd = event_time(torch, pth["fwd"], n_k)
+        pth["dq"]()
+        t_dq = event_time(torch, pth["dq"], n_k)
+        t_dkdv = event_time(torch, pth["dkdv"], n_k)
+        # Algorithmic FLOPs per launch: the forward's two matmuls; of the
+        # backward's five (S recompute, dP, dV, dK, dQ) the dk/dv kernel owns
+        # four and the dq kernel one -- the dq kernel's own recomputes earn no credit.
+        n_fwd, n_dq, n_dkdv = pth["names"]
+        kernels = [
+            {"kernel": n_fwd, "ms": t_fwd, "flop": fwd_flop},
+            {"kernel": n_dq, "ms": t_dq, "flop": unit},
+            {"kernel": n_dkdv, "ms": t_dkdv, "flop": 4 * unit},
+        ]
+        for kk in kernels:
+            kk["tflops"] = kk["flop"] / (kk["ms"] * 1e-3) / 1e12
+            kk["frac_mfma_f32"] = kk["tflops"] / PEAK_MFMA_F32
+            log(f"  {kk['kernel']}: {kk['ms']:.3f} ms, {kk['tflops']:.2f} TFLOP/s ({100 * kk['frac_mfma_f32']:.1f}% "
+                f"of FP32 MFMA peak)")
+        fwd_tflops = fwd_flop / (t_fwd * 1e-3) / 1e12
+        bwd_tflops = bwd_flop / ((t_dq + t_dkdv) * 1e-3) / 1e12
+        log(f"  forward {fwd_tflops:.2f} TFLOP/s ({100 * fwd_tflops / PEAK_MFMA_F32:.1f}%), backward "
+            f"{bwd_tflops:.2f} TFLOP/s ({100 * bwd_tflops / PEAK_MFMA_F32:.1f}%)")
+        res[pname] = dict(ms_step=ms_step, value=val, kernels=kernels, fwd_tflops=fwd_tflops,
+                          bwd_tflops=bwd_tflops)
+    ms_step, value = res["train"]["ms_step"], res["train"]["value"]
+    kernels, fwd_tflops, bwd_tflops = res["train"]["kernels"], res["train"]["fwd_tflops"], res["train"]["bwd_tflops"]
     dom = max(kernels, key=lambda x: x["ms"])
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic.json")
@@ -162,7 +179,7 @@ def main():
             traffic = json.load(f).get(dom["kernel"])
     roofline = {"bound": "mfma", "achieved": round(dom["tflops"], 3), "peak": PEAK_MFMA_F32, "unit": "TFLOP/s",
                 "frac": round(dom["tflops"] / PEAK_MFMA_F32, 4), "traffic": traffic, "kernel": dom["kernel"]}
-    del out, dq, dk, dv, do, q, k, v, rm, rl, rd
+    del out, dq, dk, dv, do, q, k, v, rm, rl, rd, lse, delta
 
     # ---------------- C4: decode step ----------------
     Bd, n_ctx = 64, 8192
@@ -270,6 +287,12 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "fwd_tflops": round(fwd_tflops, 3), "bwd_tflops": round(bwd_tflops, 3),
+        "step_path": "zt_attn_forward_train + zt_attn_backward_train (saved log-sum-exp)",
+        "reference_abi": {"step_path": "zt_attn_forward + zt_attn_backward",
+                          "ms_per_step": round(res["reference_abi"]["ms_step"], 4),
+                          "TFLOP/s": round(res["reference_abi"]["value"], 3),
+                          "kernels": [{k2: (round(v2, 4) if isinstance(v2, float) else v2) for k2, v2 in kk.items()}
+                                      for kk in res["reference_abi"]["kernels"]]},
         "kernels": [{k2: (round(v2, 4) if isinstance(v2, float) else v2) for k2, v2 in kk.items()} for kk in kernels],
         "decode": {"workload": "C4 B=64 n_keys=8192 Hq=32 Hkv=8 d=128 f32", "us": round(t_dec * 1e3, 2),
                    "GB/s": round(dec_gbs, 1), "bytes": dec_bytes, "frac_hbm": round(dec_gbs / PEAK_HBM, 4),

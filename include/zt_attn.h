@@ -146,6 +146,33 @@ int zt_rmsnorm_forward(const float *x, const float *w, float *y, int rows, int c
 int zt_rope_forward(const float *x, float *y, int rows, int cols, int pos, double theta,
                     int head_dim, hipStream_t stream);
 
+/* ---- Training path with saved statistics (no reference counterpart) ----
+ * The reference backward (zt_attn_backward above) rebuilds every row's softmax
+ * statistics itself, which costs its dq kernel a fourth matmul.  A training
+ * step that has just run the forward can keep them instead:
+ *   zt_attn_forward_train  = zt_attn_forward (causal, q_offset 0, n_keys T,
+ *       B sequences) that also writes lse[B, T, n_heads], each row's natural
+ *       log-sum-exp of its scaled scores;
+ *   zt_attn_backward_train = the same dq/dk/dv as zt_attn_backward from
+ *       (q, k, v, out, dout, lse); delta [B, T, n_heads] is caller scratch
+ *       (receives sum_d out * dout per row).  dq/dk/dv are assigned.
+ * Same refusals as the reference entry points; the two stages are also
+ * callable on their own (dq + delta first, then dk/dv on the same stream). */
+int zt_attn_forward_train(const float *q, const float *k, const float *v, float *out, float *lse, int B, int T,
+                          int n_heads, int n_kv_heads, int dim, hipStream_t stream);
+int zt_attn_backward_train(const float *q, const float *k, const float *v, const float *out, const float *dout,
+                           const float *lse, float *dq, float *dk, float *dv, float *delta, int B, int T,
+                           int n_heads, int n_kv_heads, int dim, hipStream_t stream);
+int zt_attn_bwd_dq_train(const float *q, const float *k, const float *v, const float *out, const float *dout,
+                         const float *lse, float *dq, float *delta, int B, int T, int n_heads, int n_kv_heads,
+                         int dim, hipStream_t stream);
+int zt_attn_bwd_dkdv_train(const float *q, const float *k, const float *v, const float *out, const float *dout,
+                           const float *lse, const float *delta, float *dk, float *dv, int B, int T, int n_heads,
+                           int n_kv_heads, int dim, hipStream_t stream);
+/* Kernel names the training path launches for a shape (as zt_attn_plan). */
+int zt_attn_plan_train(int B, int T, int n_heads, int n_kv_heads, int dim, char *fwd, char *dq, char *dkdv,
+                       size_t len);
+
 /* RoPE backward, src/autograd.zig:851-872 on the device: din = R^T dout at
  * position pos + r (the gradient through zt_rope_forward), so an attention
  * block's backward -- zt_attn_backward then this on dq and dk -- stays on the

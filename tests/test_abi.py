@@ -137,6 +137,20 @@ def test_decode_refusals(zt, capfd):
     assert L.zt_attn_decode_workspace(0, 8, 4, 2, 32) == 0
 
 
+def test_train_path_refusals(zt, capfd):
+    L = zt.lib()
+    p = 0x10000
+    assert L.zt_attn_forward_train(p, p, p, p, NULL, 1, 8, 4, 2, 32, NULL) == 1
+    assert "lse" in capfd.readouterr().err
+    assert L.zt_attn_forward_train(p, p, p, p, p, 1, 0, 4, 2, 32, NULL) == 1
+    assert "T 0" in capfd.readouterr().err
+    assert L.zt_attn_backward_train(p, p, p, p, p, p, p, p, p, NULL, 1, 8, 4, 2, 32, NULL) == 1
+    assert "delta" in capfd.readouterr().err
+    assert L.zt_attn_bwd_dkdv_train(p, p, p, p, p, NULL, p, p, p, 1, 8, 4, 2, 32, NULL) == 1
+    assert L.zt_attn_backward_train(p, p, p, p, p, p, p, p, p, p, 1, 8, 3, 2, 32, NULL) == 1
+    assert "not a group" in capfd.readouterr().err
+
+
 def test_decode_refuses_misaligned_rows(zt, capfd):
     # dim % 4 == 0 rows are read 16 bytes at a time; dim % 4 == 2 rows 8 at a time.
     L = zt.lib()

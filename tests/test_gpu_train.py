@@ -1,0 +1,113 @@
+"""The training path with saved statistics (zt_attn_forward_train +
+zt_attn_backward_train): the forward also writes each row's log-sum-exp and
+the backward uses it instead of rebuilding the softmax.  Gates as for the
+reference entry points: out max |diff| <= 1e-4; dq/dk/dv max|g - twin| /
+max|twin| <= 1e-3 against the CPU restatement of src/autograd.zig:636-842;
+lse and delta (= sum_d out * dO) against the twin's row statistics
+(autograd.zig:723-797)."""
+import numpy as np
+import pytest
+
+from gpuhelp import (BWD_REL, FWD_TOL, SEED_DO, SEED_K, SEED_Q, SEED_V, THETA, dev_normal, host, max_abs,
+                     rel_err)
+
+pytestmark = pytest.mark.gpu
+
+
+def _nan(torch, n):
+    return torch.full((n,), float("nan"), device="cuda", dtype=torch.float32)
+
+
+def _inputs(torch, zt, B, T, H, Hkv, D, sigma=1.0, rope=False):
+    q = dev_normal(torch, zt, B * T * H * D, SEED_Q, sigma)
+    k = dev_normal(torch, zt, B * T * Hkv * D, SEED_K, sigma)
+    v = dev_normal(torch, zt, B * T * Hkv * D, SEED_V, sigma)
+    do = dev_normal(torch, zt, B * T * H * D, SEED_DO, 1.0)
+    if rope:
+        zt.rope_qk(q, k, q, k, B, T, H, Hkv, D, 0, THETA)
+    return q, k, v, do
+
+
+def _train(torch, zt, q, k, v, do, B, T, H, Hkv, D, lse_shift=0.0):
+    out, lse = _nan(torch, q.numel()), _nan(torch, B * T * H)
+    zt.forward_train(q, k, v, out, lse, T, H, Hkv, D, B=B)
+    if lse_shift:
+        lse += lse_shift
+    dq, dk, dv, delta = _nan(torch, q.numel()), _nan(torch, k.numel()), _nan(torch, k.numel()), _nan(torch, B * T * H)
+    zt.backward_train(q, k, v, out, do, lse, dq, dk, dv, delta, T, H, Hkv, D, B=B)
+    torch.cuda.synchronize()
+    return [host(x) for x in (out, lse, dq, dk, dv, delta)]
+
+
+CASES = [
+    (1, 128, 4, 2, 32), (1, 1, 4, 2, 32), (1, 7, 2, 2, 34), (2, 50, 6, 3, 64), (1, 100, 8, 2, 80),
+    (1, 77, 4, 1, 128), (2, 33, 8, 8, 96), (1, 64, 4, 4, 192), (1, 90, 4, 2, 256), (1, 40, 16, 2, 160),
+]
+
+
+@pytest.mark.parametrize("B,T,H,Hkv,D", CASES)
+def test_train_path_matches_twin(gpu, zt, oracle, threads, B, T, H, Hkv, D):
+    q, k, v, do = _inputs(gpu, zt, B, T, H, Hkv, D)
+    out, lse, dq, dk, dv, delta = _train(gpu, zt, q, k, v, do, B, T, H, Hkv, D)
+    qh, kh, vh, dh = (host(x) for x in (q, k, v, do))
+    assert max_abs(out, oracle.attention_forward(qh, kh, vh, B, T, H, Hkv, D, threads=threads)) <= FWD_TOL
+    m, l, d = oracle.attention_row_stats(qh, kh, vh, dh, B, T, H, Hkv, D)
+    want_lse = m + np.log(l)
+    assert max_abs(lse, want_lse) <= 1e-5 * max(1.0, np.abs(want_lse).max())
+    assert max_abs(delta, d) <= 1e-4 * max(1.0, np.abs(d).max())
+    rq, rk, rv = oracle.attention_backward(qh, kh, vh, dh, B, T, H, Hkv, D, threads=threads)
+    assert rel_err(dq, rq) <= BWD_REL
+    assert rel_err(dk, rk) <= BWD_REL
+    assert rel_err(dv, rv) <= BWD_REL
+
+
+@pytest.mark.parametrize("cfg", ["c3", "c5"])
+def test_train_path_full_size(gpu, zt, oracle, threads, cfg):
+    if cfg == "c3":
+        B, T, H, Hkv, D, sigma, rope, W = 1, 4096, 32, 8, 128, 1.0, True, 64
+    else:
+        B, T, H, Hkv, D, sigma, rope, W = 2, 2048, 16, 4, 256, np.sqrt(2.0), False, 32
+    q, k, v, do = _inputs(gpu, zt, B, T, H, Hkv, D, sigma, rope)
+    out, lse, dq, dk, dv, delta = _train(gpu, zt, q, k, v, do, B, T, H, Hkv, D)
+    for g in (out, lse, dq, dk, dv, delta):
+        assert np.all(np.isfinite(g))
+    qh, kh, vh, dh = (host(x) for x in (q, k, v, do))
+    qs, ks = (B, T, H * D), (B, T, Hkv * D)
+    # Invariants over all rows: sum_s dk = 0 per (batch, kv head, d); sum_s dv = sum of dO over the group.
+    dk4 = dk.reshape(B, T, Hkv, D).astype(np.float64)
+    dv4 = dv.reshape(B, T, Hkv, D).astype(np.float64)
+    want = dh.reshape(B, T, Hkv, H // Hkv, D).astype(np.float64).sum(axis=(1, 3))
+    assert np.max(np.abs(dk4.sum(1))) <= 1e-3 * np.abs(dk4).sum(1).max()
+    assert np.max(np.abs(dv4.sum(1) - want)) <= 1e-3 * np.abs(want).max()
+    # Last W rows exact in the twin (dq rows, and dk/dv rows >= T - W); the forward's last rows too.
+    rq, rk, rv = oracle.attention_backward(qh, kh, vh, dh, B, T, H, Hkv, D, t_begin=T - W, threads=threads)
+    assert rel_err(dq.reshape(qs)[:, T - W:], rq.reshape(qs)[:, T - W:]) <= BWD_REL
+    assert rel_err(dk.reshape(ks)[:, T - W:], rk.reshape(ks)[:, T - W:]) <= BWD_REL
+    assert rel_err(dv.reshape(ks)[:, T - W:], rv.reshape(ks)[:, T - W:]) <= BWD_REL
+    ro = oracle.attention_forward(qh, kh, vh, B, T, H, Hkv, D, t_begin=T - W, threads=threads)
+    assert max_abs(out.reshape(qs)[:, T - W:], ro.reshape(qs)[:, T - W:]) <= FWD_TOL
+
+
+def test_train_stages_equal_the_whole_and_repeat_bit_for_bit(gpu, zt):
+    B, T, H, Hkv, D = 1, 300, 8, 2, 128
+    q, k, v, do = _inputs(gpu, zt, B, T, H, Hkv, D)
+    a = _train(gpu, zt, q, k, v, do, B, T, H, Hkv, D)
+    b = _train(gpu, zt, q, k, v, do, B, T, H, Hkv, D)
+    for x, y in zip(a, b):
+        assert np.array_equal(x.view(np.uint32), y.view(np.uint32))
+    out, lse = gpu.from_numpy(a[0]).cuda(), gpu.from_numpy(a[1]).cuda()
+    dq, dk, dv, delta = (_nan(gpu, n) for n in (q.numel(), k.numel(), k.numel(), B * T * H))
+    zt.bwd_dq_train(q, k, v, out, do, lse, dq, delta, T, H, Hkv, D, B=B)
+    zt.bwd_dkdv_train(q, k, v, out, do, lse, delta, dk, dv, T, H, Hkv, D, B=B)
+    gpu.cuda.synchronize()
+    for x, y in zip((dq, dk, dv, delta), a[2:]):
+        assert np.array_equal(host(x).view(np.uint32), y.view(np.uint32))
+
+
+def test_train_gate_sees_the_saved_statistics(gpu, zt, oracle):
+    # A log-sum-exp off by 0.01 scales every p by e^-0.01: the gate must fail.
+    B, T, H, Hkv, D = 1, 64, 4, 2, 64
+    q, k, v, do = _inputs(gpu, zt, B, T, H, Hkv, D)
+    _, _, dq, dk, dv, _ = _train(gpu, zt, q, k, v, do, B, T, H, Hkv, D, lse_shift=0.01)
+    rq, rk, rv = oracle.attention_backward(*(host(x) for x in (q, k, v, do)), B, T, H, Hkv, D)
+    assert max(rel_err(dq, rq), rel_err(dk, rk), rel_err(dv, rv)) > BWD_REL

@@ -8,6 +8,7 @@ struct FwdArgs {
     const float *k;    // [B, kv_rows, Hkv*dim]
     const float *v;    // [B, kv_rows, Hkv*dim]
     float *out;        // [B, T, H*dim]
+    float *lse;        // [B, T, H] log-sum-exp of each row's scaled scores, or null
     int B, T, H, Hkv, dim;
     int q_offset, n_keys, kv_rows;
     int HW;            // query heads per workgroup (1, 2 or 4; divides H/Hkv)
@@ -20,6 +21,10 @@ struct BwdArgs {
     const float *q, *k, *v, *dout;       // q/dout [B,T,H*dim]; k/v [B,T,Hkv*dim]
     float *dq, *dk, *dv;                 // assigned, never accumulated into
     float *row_max, *row_den, *row_del;  // [B,T,H]
+    // Saved-statistics mode (lse non-null): the forward's output o and
+    // log-sum-exp lse replace row_max / row_den; the dq kernel writes
+    // row_del = sum_d o * dO itself.
+    const float *o, *lse;
     int B, T, H, Hkv, dim;
     int HW, n_row_tiles, n_head_blocks;  // dq kernel decomposition (as the forward)
     int HS, n_key_tiles;                 // dk/dv kernel: head split, ceil(T / (16 * 4/HS))

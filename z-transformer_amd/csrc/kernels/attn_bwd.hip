@@ -212,6 +212,156 @@ __device__ __forceinline__ void bwd_dq_body(const BwdArgs &a) {
     }
 }
 
+// dq from saved statistics (training path: the forward wrote lse and o).
+// Per row: delta = sum_d o * dO (written to row_del for the dk/dv kernel);
+// per key tile: S^T = K Q^T, P = exp2(S - lse2) (no running max, no
+// rescaling), dP^T = V dO^T, dS = P (dP - delta), dq^T += K^T dS^T -- three
+// matmul units instead of the four the statistics-building kernel needs.
+// K/V tiles are register-prefetched as in bwd_dq_body.
+template <int DP, int BK, int NW>
+__device__ __forceinline__ void bwd_dq_lse_body(const BwdArgs &a) {
+    constexpr int LW = DP + 4, DQ = DP / 4, NT = DP / 16, NJ = BK / 16, NTH = 64 * NW, CPR = DP / 4;
+    __shared__ float Ks[BK * LW];
+    __shared__ float Vs[BK * LW];
+
+    const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, grp = lane >> 4, w = tid >> 6;
+    const int RB = NW / a.HW;
+    const int per_tile = a.n_head_blocks * a.B;
+    const int tile = a.n_row_tiles - 1 - (int)blockIdx.x / per_tile;
+    const int rem = (int)blockIdx.x % per_tile;
+    const int hb = rem % a.n_head_blocks, b = rem / a.n_head_blocks;
+    const int group = a.H / a.Hkv;
+    const int h = hb * a.HW + (w % a.HW);
+    const int kvh = h / group;
+    const int wg_row0 = tile * 16 * RB;
+    const int row0 = wg_row0 + 16 * (w / a.HW);
+    const bool vec4 = (a.dim & 3) == 0;
+    const size_t qld = (size_t)a.H * a.dim, kld = (size_t)a.Hkv * a.dim;
+    const size_t qoff = (size_t)b * a.T * qld + (size_t)h * a.dim;
+    const float *kb = a.k + (size_t)b * a.T * kld + (size_t)kvh * a.dim;
+    const float *vb = a.v + (size_t)b * a.T * kld + (size_t)kvh * a.dim;
+
+    const int my_row = row0 + l16;
+    const bool row_ok = my_row < a.T;
+    float qr[DQ], dor[DQ];
+    load_row_seg<DQ>(qr, a.q + qoff + (size_t)my_row * qld, grp * DQ, a.dim, vec4, row_ok, a.scale_log2e);
+    load_row_seg<DQ>(dor, a.dout + qoff + (size_t)my_row * qld, grp * DQ, a.dim, vec4, row_ok, 1.f);
+    float delta, lse2;
+    {
+        float orow[DQ];
+        load_row_seg<DQ>(orow, a.o + qoff + (size_t)my_row * qld, grp * DQ, a.dim, vec4, row_ok, 1.f);
+        float part = 0.f;
+#pragma unroll
+        for (int i = 0; i < DQ; ++i) part += orow[i] * dor[i];
+        delta = sum4grp(part);
+        const size_t so = ((size_t)b * a.T + my_row) * a.H + h;
+        lse2 = row_ok ? a.lse[so] * kLog2e : 0.f;
+        if (row_ok && grp == 0) a.row_del[so] = delta;
+    }
+
+    f4 acc[NT];
+#pragma unroll
+    for (int i = 0; i < NT; ++i) acc[i] = zero4();
+    const int kend_wg = min(a.T, wg_row0 + 16 * RB);
+    const int kend_w = row0 < a.T ? min(a.T, row0 + 16) : 0;
+
+    constexpr int NPF = 2 * BK * CPR / NTH;
+    static_assert((2 * BK * CPR) % NTH == 0, "prefetch split");
+    f4 pf[NPF];
+    auto fetch = [&](int k0) {
+#pragma unroll
+        for (int n = 0; n < NPF; ++n) {
+            const int e = tid + n * NTH;
+            const int arr = e / (BK * CPR), r = (e / CPR) % BK, c = (e % CPR) * 4;
+            const int key = k0 + r;
+            const float *src = (arr ? vb : kb) + (size_t)key * kld + c;
+            f4 x = zero4();
+            if (key < a.T && c < a.dim) {
+                if (vec4) {
+                    x = *reinterpret_cast<const f4 *>(src);
+                } else {
+                    const f2 lo = *reinterpret_cast<const f2 *>(src);
+                    x.x = lo.x; x.y = lo.y;
+                    if (c + 2 < a.dim) {
+                        const f2 hi = *reinterpret_cast<const f2 *>(src + 2);
+                        x.z = hi.x; x.w = hi.y;
+                    }
+                }
+            }
+            pf[n] = x;
+        }
+    };
+    fetch(0);
+
+    for (int k0 = 0; k0 < kend_wg; k0 += BK) {
+        __syncthreads();
+#pragma unroll
+        for (int n = 0; n < NPF; ++n) {
+            const int e = tid + n * NTH;
+            const int arr = e / (BK * CPR), r = (e / CPR) % BK, c = (e % CPR) * 4;
+            *reinterpret_cast<f4 *>((arr ? Vs : Ks) + r * LW + c) = pf[n];
+        }
+        __syncthreads();
+        if (k0 + BK < kend_wg) fetch(k0 + BK);
+        if (k0 >= kend_w) continue;
+
+        f4 s[NJ], dp[NJ];
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) { s[j] = zero4(); dp[j] = zero4(); }
+        const float *krow = Ks + l16 * LW + grp * DQ;
+        const float *vrow = Vs + l16 * LW + grp * DQ;
+        auto score_step = [&](int j, int kk) {
+            const f4 kx = *reinterpret_cast<const f4 *>(krow + 16 * j * LW + kk);
+            const f4 vx = *reinterpret_cast<const f4 *>(vrow + 16 * j * LW + kk);
+            s[j] = mfma16(kx.x, qr[kk + 0], s[j]);
+            dp[j] = mfma16(vx.x, dor[kk + 0], dp[j]);
+            s[j] = mfma16(kx.y, qr[kk + 1], s[j]);
+            dp[j] = mfma16(vx.y, dor[kk + 1], dp[j]);
+            s[j] = mfma16(kx.z, qr[kk + 2], s[j]);
+            dp[j] = mfma16(vx.z, dor[kk + 2], dp[j]);
+            s[j] = mfma16(kx.w, qr[kk + 3], s[j]);
+            dp[j] = mfma16(vx.w, dor[kk + 3], dp[j]);
+        };
+        if constexpr (DP <= 192) {
+#pragma unroll
+            for (int kk = 0; kk < DQ; kk += 4)
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) score_step(j, kk);
+        } else {
+#pragma unroll
+            for (int j = 0; j < NJ; ++j)
+#pragma unroll
+                for (int kk = 0; kk < DQ; kk += 4) score_step(j, kk);
+        }
+        // dS^T[key][query] = P (dP - delta), P = exp2(S - lse2); zero where masked.
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int key = k0 + 16 * j + 4 * grp + r;
+                const float p = (key <= my_row) ? exp2f(s[j][r] - lse2) : 0.f;
+                s[j][r] = p * (dp[j][r] - delta);
+            }
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            if (k0 + 16 * j >= kend_w) continue;
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+                float kx[NT];  // K^T rows, row-owner layout
+                lds_run<NT>(kx, Ks + (16 * j + 4 * grp + kk) * LW + l16 * NT);
+#pragma unroll
+                for (int i = 0; i < NT; ++i) acc[i] = mfma16(kx[i], s[j][kk], acc[i]);
+            }
+        }
+    }
+
+    if (row_ok) {
+        float *dqrow = a.dq + qoff + (size_t)my_row * qld;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) store_run<NT>(dqrow, (4 * grp + r) * NT, a.dim, vec4, acc, r, a.scale);
+    }
+}
+
 template <int DP, int HS, int KW, bool PF = false>
 __device__ __forceinline__ void bwd_dkdv_body(const BwdArgs &a) {
     constexpr int LW = DP + 4, DQ = DP / 4, NT = DP / 16, NTH = 64 * KW * HS;
@@ -298,8 +448,8 @@ __device__ __forceinline__ void bwd_dkdv_body(const BwdArgs &a) {
             pm2 = 0.f; pil = 0.f; pde = 0.f;
             if (t < a.T) {
                 const size_t o = ((size_t)b * a.T + t) * a.H + hh;
-                pm2 = a.row_max[o] * kLog2e;
-                pil = 1.f / a.row_den[o];
+                pm2 = (a.lse ? a.lse[o] : a.row_max[o]) * kLog2e;
+                pil = a.lse ? 1.f : 1.f / a.row_den[o];
                 pde = a.row_del[o];
             }
         }
@@ -342,8 +492,8 @@ __device__ __forceinline__ void bwd_dkdv_body(const BwdArgs &a) {
                 float m2 = 0.f, il = 0.f, de = 0.f;
                 if (t < a.T) {
                     const size_t o = ((size_t)b * a.T + t) * a.H + hh;
-                    m2 = a.row_max[o] * kLog2e;
-                    il = 1.f / a.row_den[o];
+                    m2 = (a.lse ? a.lse[o] : a.row_max[o]) * kLog2e;
+                    il = a.lse ? 1.f : 1.f / a.row_den[o];
                     de = a.row_del[o];
                 }
                 St[(part * BQ + r) * 4 + 0] = m2;
@@ -480,8 +630,8 @@ __device__ __forceinline__ void bwd_dkdv_dma_body(const BwdArgs &a) {
             sm2 = 0.f; sil = 0.f; sde = 0.f;
             if (t < a.T) {
                 const size_t o = ((size_t)b * a.T + t) * a.H + hh;
-                sm2 = a.row_max[o] * kLog2e;
-                sil = 1.f / a.row_den[o];
+                sm2 = (a.lse ? a.lse[o] : a.row_max[o]) * kLog2e;
+                sil = a.lse ? 1.f : 1.f / a.row_den[o];
                 sde = a.row_del[o];
             }
         }
@@ -596,6 +746,12 @@ __device__ __forceinline__ void bwd_dkdv_dma_body(const BwdArgs &a) {
     extern "C" __global__ void __launch_bounds__(512) zt_bwd_dq8_d##DP##_k##BK(BwdArgs a) {      \
         bwd_dq_body<DP, BK, 8>(a);                                                                 \
     }
+// dq from saved statistics (32-key tiles, register prefetch), four waves.
+#define ZT_BWD_DQ_LSE(DP)                                                                          \
+    extern "C" __global__ void __launch_bounds__(256, (DP) <= 192 ? 2 : 1)                        \
+        zt_bwd_dql_d##DP##_k32(BwdArgs a) {                                                        \
+        bwd_dq_lse_body<DP, 32, 4>(a);                                                             \
+    }
 // Register-prefetched dq (32-key tiles), four and eight waves.
 #define ZT_BWD_DQ_PF(DP)                                                                           \
     extern "C" __global__ void __launch_bounds__(256, (DP) <= 192 ? 2 : 1)                        \
@@ -622,7 +778,7 @@ __device__ __forceinline__ void bwd_dkdv_dma_body(const BwdArgs &a) {
         bwd_dkdv_dma_body<DP, HS>(a);                                                              \
     }
 #define ZT_BWD_ALL(DP)                                                                             \
-    ZT_BWD_DQ(DP, 32) ZT_BWD_DQ(DP, 64) ZT_BWD_DQ_PF(DP) ZT_BWD_DKDV(DP, 1) ZT_BWD_DKDV(DP, 2) ZT_BWD_DKDV8(DP)    \
+    ZT_BWD_DQ(DP, 32) ZT_BWD_DQ(DP, 64) ZT_BWD_DQ_PF(DP) ZT_BWD_DQ_LSE(DP) ZT_BWD_DKDV(DP, 1) ZT_BWD_DKDV(DP, 2) ZT_BWD_DKDV8(DP)    \
     ZT_BWD_DKDV_DMA(DP, 1) ZT_BWD_DKDV_DMA(DP, 2)
 
 ZT_BWD_ALL(32)

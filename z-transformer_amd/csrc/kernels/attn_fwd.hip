@@ -172,7 +172,10 @@ __device__ __forceinline__ void attn_fwd_body(const FwdArgs &a) {
         }
     }
 
-    const float inv = 1.f / sum4grp(lsum);
+    const float l = sum4grp(lsum);
+    const float inv = 1.f / l;
+    if (a.lse && grp == 0 && my_row < a.T)  // natural log: (m + log2 l) ln 2
+        a.lse[((size_t)b * a.T + my_row) * a.H + h] = (m + log2f(l)) * 0.69314718055994531f;
     if (my_row < a.T) {
         float *orow = a.out + (size_t)b * a.T * qld + (size_t)my_row * qld + (size_t)h * a.dim;
 #pragma unroll

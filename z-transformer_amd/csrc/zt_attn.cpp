@@ -248,7 +248,7 @@ static bool rows_aligned(int dim, std::initializer_list<const void *> ptrs) {
 
 int forward_impl(const float *q, const float *k, const float *v, float *out, int B, int T, int n_heads,
                  int n_kv_heads, int dim, int group_q, int max_tile, int q_offset, int n_keys, int kv_rows,
-                 hipStream_t stream) {
+                 hipStream_t stream, float *lse = nullptr) {
     if (T < 1) return refuse_T(T);
     if (!zt_attn_dim_ok(dim)) return refuse_dim(dim);
     if (check_group(n_heads, n_kv_heads)) return 1;
@@ -283,7 +283,7 @@ int forward_impl(const float *q, const float *k, const float *v, float *out, int
     }
     if (!rows_aligned(dim, {q, k, v, out})) return 1;
     FwdArgs a{};
-    a.q = q; a.k = k; a.v = v; a.out = out;
+    a.q = q; a.k = k; a.v = v; a.out = out; a.lse = lse;
     a.B = B; a.T = T; a.H = n_heads; a.Hkv = n_kv_heads; a.dim = dim;
     a.q_offset = q_offset; a.n_keys = n_keys; a.kv_rows = kv_rows;
     a.HW = heads_per_wg(n_heads / n_kv_heads);
@@ -305,7 +305,8 @@ int backward_prepare(const float *q, const float *k, const float *v, const float
                      float *dv, float *row_max, float *row_den, float *row_del, int B, int T, int n_heads,
                      int n_kv_heads, int dim, int max_tile, BwdArgs *a, DeviceState **st_out, char *name_dq,
                      char *name_dkdv, unsigned *blocks_dq, unsigned *blocks_dkdv, unsigned *threads_dq,
-                     unsigned *threads_dkdv) {
+                     unsigned *threads_dkdv, const float *o = nullptr, const float *lse = nullptr) {
+    const bool saved = lse != nullptr;  // statistics from the forward: 32-key, four-wave dq kernel
     if (T < 1) return refuse_T(T);
     if (!zt_attn_dim_ok(dim)) return refuse_dim(dim);
     if (check_group(n_heads, n_kv_heads)) return 1;
@@ -317,7 +318,7 @@ int backward_prepare(const float *q, const float *k, const float *v, const float
     DeviceState *st = require_device();
     if (!st) return 1;
     const int dp = pad32(dim);
-    int bk = key_tile(Tiled::Dq, dp, max_tile);
+    int bk = saved ? 32 : key_tile(Tiled::Dq, dp, max_tile);
     if (kv_tile_bytes(dp, bk) > st->lds_limit) bk = 32;
     const int group = n_heads / n_kv_heads;
     // dk/dv head split: two parts where the group allows (measured best at
@@ -336,14 +337,19 @@ int backward_prepare(const float *q, const float *k, const float *v, const float
         fprintf(stderr, "zt_attn: a null tensor pointer is not launchable.\n");
         return 1;
     }
-    if (!rows_aligned(dim, {q, k, v, dout, dq, dk, dv})) return 1;
+    if (saved && !o) {
+        fprintf(stderr, "zt_attn: the saved-statistics backward needs the forward output.\n");
+        return 1;
+    }
+    if (!rows_aligned(dim, {q, k, v, dout, dq, dk, dv, o})) return 1;
     *a = BwdArgs{};
+    a->o = o; a->lse = lse;
     a->q = q; a->k = k; a->v = v; a->dout = dout;
     a->dq = dq; a->dk = dk; a->dv = dv;
     a->row_max = row_max; a->row_den = row_den; a->row_del = row_del;
     a->B = B; a->T = T; a->H = n_heads; a->Hkv = n_kv_heads; a->dim = dim;
     a->HW = heads_per_wg(group);
-    const int nw_dq = dq_waves(dp);
+    const int nw_dq = saved ? 4 : dq_waves(dp);
     const int rows_per_wg = 16 * (nw_dq / a->HW);
     a->n_row_tiles = (T + rows_per_wg - 1) / rows_per_wg;
     a->n_head_blocks = n_heads / a->HW;
@@ -370,7 +376,9 @@ int backward_prepare(const float *q, const float *k, const float *v, const float
     const unsigned long long blocks_a = (unsigned long long)a->n_row_tiles * a->n_head_blocks * B;
     if (!grid_ok(blocks_a) || !grid_ok(blocks_b)) return 1;
     const bool qpf = bk == 32 && env_choice("ZT_ATTN_QPF", 1, {0, 1}) == 1;
-    if (qpf)
+    if (saved)
+        snprintf(name_dq, 64, "zt_bwd_dql_d%d_k32", dp);
+    else if (qpf)
         snprintf(name_dq, 64, nw_dq == 8 ? "zt_bwd_dq8p_d%d_k32" : "zt_bwd_dqp_d%d_k32", dp);
     else
         snprintf(name_dq, 64, nw_dq == 8 ? "zt_bwd_dq8_d%d_k%d" : "zt_bwd_dq_d%d_k%d", dp, bk);
@@ -390,13 +398,14 @@ int backward_prepare(const float *q, const float *k, const float *v, const float
 // stage: 1 = dq + row statistics, 2 = dk/dv (reads the statistics), 3 = both.
 int backward_impl(const float *q, const float *k, const float *v, const float *dout, float *dq, float *dk,
                   float *dv, float *row_max, float *row_den, float *row_del, int B, int T, int n_heads,
-                  int n_kv_heads, int dim, int max_tile, int stage, hipStream_t stream) {
+                  int n_kv_heads, int dim, int max_tile, int stage, hipStream_t stream, const float *o = nullptr,
+                  const float *lse = nullptr) {
     BwdArgs a;
     DeviceState *st = nullptr;
     char name_a[64], name_b[64];
     unsigned blocks_a = 0, blocks_b = 0, threads_a = kThreads, threads_b = kThreads;
     if (backward_prepare(q, k, v, dout, dq, dk, dv, row_max, row_den, row_del, B, T, n_heads, n_kv_heads, dim,
-                         max_tile, &a, &st, name_a, name_b, &blocks_a, &blocks_b, &threads_a, &threads_b))
+                         max_tile, &a, &st, name_a, name_b, &blocks_a, &blocks_b, &threads_a, &threads_b, o, lse))
         return 1;
     if ((stage & 1) && !dq) {
         fprintf(stderr, "zt_attn: a null dq is not launchable.\n");
@@ -491,6 +500,50 @@ int zt_attn_backward_batched(const float *q, const float *k, const float *v, con
                              int n_heads, int n_kv_heads, int dim, int max_tile, hipStream_t stream) {
     return backward_impl(q, k, v, dout, dq, dk, dv, row_max, row_den, row_del, B, T, n_heads, n_kv_heads, dim,
                          max_tile, 3, stream);
+}
+
+int zt_attn_forward_train(const float *q, const float *k, const float *v, float *out, float *lse, int B, int T,
+                          int n_heads, int n_kv_heads, int dim, hipStream_t stream) {
+    if (!lse && T >= 1 && zt_attn_dim_ok(dim)) {
+        fprintf(stderr, "zt_attn: forward_train needs an lse buffer.\n");
+        return 1;
+    }
+    return forward_impl(q, k, v, out, B, T, n_heads, n_kv_heads, dim, 1, 64, 0, T, T, stream, lse);
+}
+
+static int train_stats_ok(const float *lse, const float *delta) {
+    if (!lse || !delta) {
+        fprintf(stderr, "zt_attn: the saved-statistics backward needs lse and a delta buffer.\n");
+        return 0;
+    }
+    return 1;
+}
+
+int zt_attn_backward_train(const float *q, const float *k, const float *v, const float *out, const float *dout,
+                           const float *lse, float *dq, float *dk, float *dv, float *delta, int B, int T,
+                           int n_heads, int n_kv_heads, int dim, hipStream_t stream) {
+    if (!train_stats_ok(lse, delta)) return 1;
+    float *l = const_cast<float *>(lse);  // read only in this mode
+    return backward_impl(q, k, v, dout, dq, dk, dv, l, l, delta, B, T, n_heads, n_kv_heads, dim, 64, 3, stream, out,
+                         lse);
+}
+
+int zt_attn_bwd_dq_train(const float *q, const float *k, const float *v, const float *out, const float *dout,
+                         const float *lse, float *dq, float *delta, int B, int T, int n_heads, int n_kv_heads,
+                         int dim, hipStream_t stream) {
+    if (!train_stats_ok(lse, delta)) return 1;
+    float *l = const_cast<float *>(lse);
+    return backward_impl(q, k, v, dout, dq, nullptr, nullptr, l, l, delta, B, T, n_heads, n_kv_heads, dim, 64, 1,
+                         stream, out, lse);
+}
+
+int zt_attn_bwd_dkdv_train(const float *q, const float *k, const float *v, const float *out, const float *dout,
+                           const float *lse, const float *delta, float *dk, float *dv, int B, int T, int n_heads,
+                           int n_kv_heads, int dim, hipStream_t stream) {
+    if (!train_stats_ok(lse, delta)) return 1;
+    float *l = const_cast<float *>(lse);
+    return backward_impl(q, k, v, dout, nullptr, dk, dv, l, l, const_cast<float *>(delta), B, T, n_heads, n_kv_heads,
+                         dim, 64, 2, stream, out, lse);
 }
 
 int zt_attn_bwd_dq(const float *q, const float *k, const float *v, const float *dout, float *dq, float *row_max,
@@ -786,6 +839,13 @@ int zt_attn_plan(int B, int T, int n_heads, int n_kv_heads, int dim, int max_til
         return 1;
     snprintf(dq, len, "%s", na);
     snprintf(dkdv, len, "%s", nb);
+    return 0;
+}
+
+int zt_attn_plan_train(int B, int T, int n_heads, int n_kv_heads, int dim, char *fwd, char *dq, char *dkdv,
+                       size_t len) {
+    if (zt_attn_plan(B, T, n_heads, n_kv_heads, dim, 64, fwd, dq, dkdv, len)) return 1;
+    snprintf(dq, len, "zt_bwd_dql_d%d_k32", pad32(dim));
     return 0;
 }
 

@@ -22,7 +22,8 @@ ABI_SYMBOLS = [
     "zt_attn_decode_workspace", "zt_attn_decode", "zt_attn_decode_step_workspace", "zt_attn_decode_step",
     "zt_rmsnorm_forward", "zt_rope_forward", "zt_rope_backward", "zt_rope_qk_forward",
     "zt_rope_qk_backward", "zt_fill_normal", "zt_fill_uniform", "zt_attn_version",
-    "zt_attn_lds_limit", "zt_attn_plan",
+    "zt_attn_lds_limit", "zt_attn_plan", "zt_attn_forward_train", "zt_attn_backward_train",
+    "zt_attn_bwd_dq_train", "zt_attn_bwd_dkdv_train", "zt_attn_plan_train",
 ]
 HOLDER_SYMBOLS = [
     "zt_bytes_for", "zt_to_cint", "zt_forward_bounds", "zt_holder_init", "zt_holder_deinit",
@@ -66,6 +67,11 @@ def lib():
             "zt_attn_decode_step_workspace": (Z, [I, I, I, I, I]),
             "zt_attn_decode_step": (I, [P] * 7 + [I] * 5 + [D, P, Z, P]),
             "zt_rmsnorm_forward": (I, [P, P, P, I, I, D, P]),
+            "zt_attn_forward_train": (I, [P] * 5 + [I] * 5 + [P]),
+            "zt_attn_backward_train": (I, [P] * 10 + [I] * 5 + [P]),
+            "zt_attn_bwd_dq_train": (I, [P] * 8 + [I] * 5 + [P]),
+            "zt_attn_bwd_dkdv_train": (I, [P] * 9 + [I] * 5 + [P]),
+            "zt_attn_plan_train": (I, [I] * 5 + [P, P, P, Z]),
             "zt_rope_forward": (I, [P, P, I, I, I, D, I, P]),
             "zt_rope_backward": (I, [P, P, I, I, I, D, I, P]),
             "zt_rope_qk_forward": (I, [P, P, P, P, I, I, I, I, I, I, D, P]),
@@ -157,6 +163,39 @@ def bwd_dkdv(q, k, v, dout, dk, dv, row_max, row_den, row_del, T, n_heads, n_kv_
     _f32_cuda(q, k, v, dout, dk, dv, row_max, row_den, row_del)
     _check(lib().zt_attn_bwd_dkdv(*map(_ptr, (q, k, v, dout, dk, dv, row_max, row_den, row_del)), B, T, n_heads,
                                   n_kv_heads, dim, _stream(stream)), "zt_attn_bwd_dkdv")
+
+
+def forward_train(q, k, v, out, lse, T, n_heads, n_kv_heads, dim, B=1, stream=None):
+    _f32_cuda(q, k, v, out, lse)
+    _check(lib().zt_attn_forward_train(_ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(lse), B, T, n_heads, n_kv_heads,
+                                       dim, _stream(stream)), "zt_attn_forward_train")
+
+
+def backward_train(q, k, v, out, dout, lse, dq, dk, dv, delta, T, n_heads, n_kv_heads, dim, B=1, stream=None):
+    _f32_cuda(q, k, v, out, dout, lse, dq, dk, dv, delta)
+    _check(lib().zt_attn_backward_train(_ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(dout), _ptr(lse), _ptr(dq),
+                                        _ptr(dk), _ptr(dv), _ptr(delta), B, T, n_heads, n_kv_heads, dim,
+                                        _stream(stream)), "zt_attn_backward_train")
+
+
+def bwd_dq_train(q, k, v, out, dout, lse, dq, delta, T, n_heads, n_kv_heads, dim, B=1, stream=None):
+    _f32_cuda(q, k, v, out, dout, lse, dq, delta)
+    _check(lib().zt_attn_bwd_dq_train(_ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(dout), _ptr(lse), _ptr(dq),
+                                      _ptr(delta), B, T, n_heads, n_kv_heads, dim, _stream(stream)),
+           "zt_attn_bwd_dq_train")
+
+
+def bwd_dkdv_train(q, k, v, out, dout, lse, delta, dk, dv, T, n_heads, n_kv_heads, dim, B=1, stream=None):
+    _f32_cuda(q, k, v, out, dout, lse, delta, dk, dv)
+    _check(lib().zt_attn_bwd_dkdv_train(_ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(dout), _ptr(lse), _ptr(delta),
+                                        _ptr(dk), _ptr(dv), B, T, n_heads, n_kv_heads, dim, _stream(stream)),
+           "zt_attn_bwd_dkdv_train")
+
+
+def plan_train(B, T, n_heads, n_kv_heads, dim):
+    bufs = [ctypes.create_string_buffer(64) for _ in range(3)]
+    _check(lib().zt_attn_plan_train(B, T, n_heads, n_kv_heads, dim, *bufs, 64), "zt_attn_plan_train")
+    return tuple(b.value.decode() for b in bufs)
 
 
 def decode_workspace_bytes(B, n_ctx, n_heads, n_kv_heads, dim):
