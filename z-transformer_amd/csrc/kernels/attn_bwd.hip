@@ -159,14 +159,14 @@ __device__ __forceinline__ void bwd_dq_body(const BwdArgs &a) {
             mt = fmaxf(mt, fmaxf(fmaxf(s[j][0], s[j][1]), fmaxf(s[j][2], s[j][3])));
         mt = max4grp(mt);
         const float mnew = fmaxf(m, mt);
-        const float corr = exp2f(m - mnew);
+        const float corr = fast_exp2(m - mnew);
         m = mnew;
         float ps = 0.f, pds = 0.f;
 #pragma unroll
         for (int j = 0; j < NJ; ++j)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const float p = exp2f(s[j][r] - mnew);
+                const float p = fast_exp2(s[j][r] - mnew);
                 s[j][r] = p;
                 dp[j][r] *= p;  // p~ dp
                 ps += p;
@@ -184,7 +184,7 @@ __device__ __forceinline__ void bwd_dq_body(const BwdArgs &a) {
             for (int kk = 0; kk < 4; ++kk) {
                 const float pv = s[j][kk], pd = dp[j][kk];
                 float kx[NT];  // K^T rows, row-owner layout: K[key][l16 * NT + i]
-                lds_run<NT>(kx, Ks + (16 * j + 4 * grp + kk) * LW + l16 * NT);
+                lds_run<NT>(kx, Ks + (16 * j + 4 * grp + kk) * LW, l16);
 #pragma unroll
                 for (int i = 0; i < NT; ++i) {
                     a0[i] = mfma16(kx[i], pv, a0[i]);
@@ -202,7 +202,7 @@ __device__ __forceinline__ void bwd_dq_body(const BwdArgs &a) {
 #pragma unroll
         for (int i = 0; i < NT; ++i) a1[i] = a1[i] - delta * a0[i];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) store_run<NT>(dqrow, (4 * grp + r) * NT, a.dim, vec4, a1, r, f);
+        for (int r = 0; r < 4; ++r) store_run<NT>(dqrow, 4 * grp + r, a.dim, vec4, a1, r, f);
         if (grp == 0) {
             const size_t o = ((size_t)b * a.T + my_row) * a.H + h;
             a.row_max[o] = m * 0.69314718055994531f;  // back to natural units
@@ -339,7 +339,8 @@ __device__ __forceinline__ void bwd_dq_lse_body(const BwdArgs &a) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int key = k0 + 16 * j + 4 * grp + r;
-                const float p = (key <= my_row) ? exp2f(s[j][r] - lse2) : 0.f;
+                const float e = fast_exp2(s[j][r] - lse2);
+                const float p = (key <= my_row) ? e : 0.f;
                 s[j][r] = p * (dp[j][r] - delta);
             }
 #pragma unroll
@@ -348,7 +349,7 @@ __device__ __forceinline__ void bwd_dq_lse_body(const BwdArgs &a) {
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk) {
                 float kx[NT];  // K^T rows, row-owner layout
-                lds_run<NT>(kx, Ks + (16 * j + 4 * grp + kk) * LW + l16 * NT);
+                lds_run<NT>(kx, Ks + (16 * j + 4 * grp + kk) * LW, l16);
 #pragma unroll
                 for (int i = 0; i < NT; ++i) acc[i] = mfma16(kx[i], s[j][kk], acc[i]);
             }
@@ -358,7 +359,7 @@ __device__ __forceinline__ void bwd_dq_lse_body(const BwdArgs &a) {
     if (row_ok) {
         float *dqrow = a.dq + qoff + (size_t)my_row * qld;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) store_run<NT>(dqrow, (4 * grp + r) * NT, a.dim, vec4, acc, r, a.scale);
+        for (int r = 0; r < 4; ++r) store_run<NT>(dqrow, 4 * grp + r, a.dim, vec4, acc, r, a.scale);
     }
 }
 
@@ -504,6 +505,10 @@ __device__ __forceinline__ void bwd_dkdv_body(const BwdArgs &a) {
         }
         if (t0 + 15 < s0 || s0 >= a.T) continue;  // wave-uniform: no visible pair
 
+            // This lane's four query rows' statistics, read ahead of the MFMAs.
+            f4 stv[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) stv[r] = *reinterpret_cast<const f4 *>(st + (4 * grp + r) * 4);
             f4 s = zero4(), dp = zero4();
             {
                 const float *qrow = qs + l16 * LW + grp * DQ;
@@ -526,18 +531,17 @@ __device__ __forceinline__ void bwd_dkdv_body(const BwdArgs &a) {
             f4 p, dsv;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int tr = 4 * grp + r, t = t0 + tr;
-                const float m2 = st[tr * 4 + 0], il = st[tr * 4 + 1], de = st[tr * 4 + 2];
+                const int t = t0 + 4 * grp + r;
                 const bool vis = (t < a.T) && (t >= my_key);
-                const float pr = vis ? exp2f(s[r] - m2) * il : 0.f;
-                p[r] = pr;
-                dsv[r] = pr * (dp[r] - de);
+                const float e = fast_exp2(s[r] - stv[r].x) * stv[r].y;
+                p[r] = vis ? e : 0.f;
+                dsv[r] = p[r] * (dp[r] - stv[r].z);
             }
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk) {
                 float dx[NT], qx[NT];  // dO^T, Q^T rows in the row-owner layout
-                lds_run<NT>(dx, ds + (4 * grp + kk) * LW + l16 * NT);
-                lds_run<NT>(qx, qs + (4 * grp + kk) * LW + l16 * NT);
+                lds_run<NT>(dx, ds + (4 * grp + kk) * LW, l16);
+                lds_run<NT>(qx, qs + (4 * grp + kk) * LW, l16);
                 const float pv = p[kk], dv = dsv[kk];
 #pragma unroll
                 for (int i = 0; i < NT; ++i) {
@@ -570,8 +574,8 @@ __device__ __forceinline__ void bwd_dkdv_body(const BwdArgs &a) {
         float *dvrow = a.dv + kvoff + (size_t)my_key * kld;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            store_run<NT>(dkrow, (4 * grp + r) * NT, a.dim, vec4, dka, r, a.scale);
-            store_run<NT>(dvrow, (4 * grp + r) * NT, a.dim, vec4, dva, r, 1.f);
+            store_run<NT>(dkrow, 4 * grp + r, a.dim, vec4, dka, r, a.scale);
+            store_run<NT>(dvrow, 4 * grp + r, a.dim, vec4, dva, r, 1.f);
         }
     }
 }
@@ -664,6 +668,9 @@ __device__ __forceinline__ void bwd_dkdv_dma_body(const BwdArgs &a) {
             const float *qs = smem + buf * STAGE + (hs * 2 + 0) * TILE;
             const float *ds = smem + buf * STAGE + (hs * 2 + 1) * TILE;
             const float *sp = stats + buf * HS * BQ * 4 + hs * BQ * 4;
+            f4 stv[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) stv[r] = *reinterpret_cast<const f4 *>(sp + (4 * grp + r) * 4);
             f4 s = zero4(), dp = zero4();
 #pragma unroll
             for (int kk = 0; kk < DQ; kk += 4) {
@@ -682,20 +689,19 @@ __device__ __forceinline__ void bwd_dkdv_dma_body(const BwdArgs &a) {
             f4 p, dsv;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int tr = 4 * grp + r, t = t0 + tr;
-                const float m2 = sp[tr * 4 + 0], il = sp[tr * 4 + 1], de = sp[tr * 4 + 2];
+                const int t = t0 + 4 * grp + r;
                 const bool vis = (t < a.T) && (t >= my_key);
-                const float pr = vis ? exp2f(s[r] - m2) * il : 0.f;
-                p[r] = pr;
-                dsv[r] = pr * (dp[r] - de);
+                const float e = fast_exp2(s[r] - stv[r].x) * stv[r].y;
+                p[r] = vis ? e : 0.f;
+                dsv[r] = p[r] * (dp[r] - stv[r].z);
             }
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk) {
                 const int tr = 4 * grp + kk;
                 const float pv = p[kk], dv = dsv[kk];
                 float dx[NT], qx[NT];  // dO^T, Q^T rows in the row-owner layout
-                lds_run_swz<NT, CPR>(dx, ds, tr, l16 * NT);
-                lds_run_swz<NT, CPR>(qx, qs, tr, l16 * NT);
+                lds_run_swz<NT, CPR>(dx, ds, tr, l16);
+                lds_run_swz<NT, CPR>(qx, qs, tr, l16);
 #pragma unroll
                 for (int i = 0; i < NT; ++i) {
                     dva[i] = mfma16(dx[i], pv, dva[i]);
@@ -729,8 +735,8 @@ __device__ __forceinline__ void bwd_dkdv_dma_body(const BwdArgs &a) {
         float *dvrow = a.dv + kvoff + (size_t)my_key * kld;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            store_run<NT>(dkrow, (4 * grp + r) * NT, DP, true, dka, r, a.scale);
-            store_run<NT>(dvrow, (4 * grp + r) * NT, DP, true, dva, r, 1.f);
+            store_run<NT>(dkrow, 4 * grp + r, DP, true, dka, r, a.scale);
+            store_run<NT>(dvrow, 4 * grp + r, DP, true, dva, r, 1.f);
         }
     }
 }

@@ -170,7 +170,7 @@ __device__ __forceinline__ void decode_body(const DecArgs &a) {
                 if (jidx[cc] % G == gi) lm = fmaxf(lm, sc[cc]);
             const float mnew = fmaxf(m[gi], wave_max(lm));
             msafe[gi] = mnew == -INFINITY ? 0.f : mnew;
-            corr[gi] = exp2f(m[gi] - msafe[gi]);
+            corr[gi] = fast_exp2(m[gi] - msafe[gi]);
             m[gi] = mnew;
             ls[gi] *= corr[gi];
             acc[gi] *= corr[gi];
@@ -182,7 +182,7 @@ __device__ __forceinline__ void decode_body(const DecArgs &a) {
             float ms = msafe[0];
 #pragma unroll
             for (int g2 = 1; g2 < G; ++g2) ms = (gi == g2) ? msafe[g2] : ms;
-            const float p = exp2f(sc[cc] - ms);
+            const float p = fast_exp2(sc[cc] - ms);
             if (counted) {
 #pragma unroll
                 for (int g2 = 0; g2 < G; ++g2) ls[g2] += (gi == g2) ? p : 0.f;
@@ -221,7 +221,7 @@ __device__ __forceinline__ void decode_body(const DecArgs &a) {
         float L = 0.f;
         f4 A = zero4();
         for (int ww = 0; ww < 4; ++ww) {
-            const float f = Wm[ww][gi] == -INFINITY ? 0.f : exp2f(Wm[ww][gi] - M);
+            const float f = Wm[ww][gi] == -INFINITY ? 0.f : fast_exp2(Wm[ww][gi] - M);
             L += Wl[ww][gi] * f;
             A += Wacc[ww][gi][sb] * f;
         }
@@ -248,11 +248,11 @@ extern "C" __global__ void __launch_bounds__(256) zt_dec_combine(DecArgs a) {
     float M = -INFINITY;
     for (int c = 0; c < nch; ++c) M = fmaxf(M, a.part_ml[(slot0 + c) * 2]);
     float L = 0.f;
-    for (int c = 0; c < nch; ++c) L += a.part_ml[(slot0 + c) * 2 + 1] * exp2f(a.part_ml[(slot0 + c) * 2] - M);
+    for (int c = 0; c < nch; ++c) L += a.part_ml[(slot0 + c) * 2 + 1] * fast_exp2(a.part_ml[(slot0 + c) * 2] - M);
     const float inv = 1.f / L;
     for (int n = threadIdx.x; n < a.dim; n += blockDim.x) {
         float o = 0.f;
-        for (int c = 0; c < nch; ++c) o += a.part_acc[(slot0 + c) * a.dim + n] * exp2f(a.part_ml[(slot0 + c) * 2] - M);
+        for (int c = 0; c < nch; ++c) o += a.part_acc[(slot0 + c) * a.dim + n] * fast_exp2(a.part_ml[(slot0 + c) * 2] - M);
         a.out[(size_t)b * a.H * a.dim + (size_t)h * a.dim + n] = o * inv;
     }
 }

@@ -144,14 +144,14 @@ __device__ __forceinline__ void attn_fwd_body(const FwdArgs &a) {
             mt = fmaxf(mt, fmaxf(fmaxf(s[j][0], s[j][1]), fmaxf(s[j][2], s[j][3])));
         mt = max4grp(mt);
         const float mnew = fmaxf(m, mt);  // finite: key 0 is visible to every row
-        const float corr = exp2f(m - mnew);
+        const float corr = fast_exp2(m - mnew);
         m = mnew;
         float ps = 0.f;
 #pragma unroll
         for (int j = 0; j < NJ; ++j)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                s[j][r] = exp2f(s[j][r] - mnew);
+                s[j][r] = fast_exp2(s[j][r] - mnew);
                 ps += s[j][r];
             }
         lsum = lsum * corr + ps;
@@ -165,7 +165,7 @@ __device__ __forceinline__ void attn_fwd_body(const FwdArgs &a) {
             for (int kk = 0; kk < 4; ++kk) {
                 // A operand V^T in the row-owner layout: V[key 16 j + 4 grp + kk][l16 * NT + i].
                 float vx[NT];
-                lds_run<NT>(vx, Vs + (16 * j + 4 * grp + kk) * LW + l16 * NT);
+                lds_run<NT>(vx, Vs + (16 * j + 4 * grp + kk) * LW, l16);
 #pragma unroll
                 for (int i = 0; i < NT; ++i) o[i] = mfma16(vx[i], s[j][kk], o[i]);
             }
@@ -179,7 +179,7 @@ __device__ __forceinline__ void attn_fwd_body(const FwdArgs &a) {
     if (my_row < a.T) {
         float *orow = a.out + (size_t)b * a.T * qld + (size_t)my_row * qld + (size_t)h * a.dim;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) store_run<NT>(orow, (4 * grp + r) * NT, a.dim, vec4, o, r, inv);
+        for (int r = 0; r < 4; ++r) store_run<NT>(orow, 4 * grp + r, a.dim, vec4, o, r, inv);
     }
 }
 

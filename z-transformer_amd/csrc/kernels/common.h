@@ -12,11 +12,14 @@
 //     sum is order-free across k-steps, so each lane then reads DP/4
 //     contiguous floats of a row (128-bit loads) instead of a strided column.
 //   * Products whose output rows run over the head dimension (O^T, dq^T, dK^T,
-//     dV^T) use the "row-owner" layout: output row i (0..15) of column tile it
-//     (0..NT-1, NT = DP/16) is d = i * NT + it.  The A operand a lane needs for
-//     one k-step -- row i = l16 of every tile -- is then NT consecutive floats
-//     of one row-major LDS row (128- or 64-bit reads, lds_run), and accumulator
-//     row 4*grp + r holds NT consecutive d of one output row (store_run).
+//     dV^T) use the "row-owner" layout: with C = 4 floats when NT = DP/16 is a
+//     multiple of 4 (else C = 2), output row i (0..15) of column tile it
+//     (0..NT-1) is d = (it / C) * 16C + C i + it % C.  Row i thus owns the C-float
+//     chunk i of every 16C-wide column block, so the A operand a lane needs for
+//     one k-step -- row i = l16 of every tile -- is NT/C chunks of one row-major
+//     LDS row (128- or 64-bit reads, lds_run) with consecutive lanes on
+//     consecutive chunks (no bank conflicts), and accumulator row 4*grp + r
+//     holds whole C-float chunks of one output row (store_run).
 //   * Scores are kept transposed (keys on the M axis, queries on the N axis):
 //     the C layout of S^T (lane = query column, 4 key rows per register group)
 //     is then exactly the B-operand layout the P.V product needs, with key
@@ -37,6 +40,11 @@ DEVI f4 mfma16(float a, float b, f4 c) {
 }
 
 DEVI int lane_id() { return threadIdx.x & 63; }
+
+// 2^x on the hardware's v_exp_f32, without the library's rescaling of
+// results below 2^-126: softmax weights that small are negligible next to a
+// row sum of at least 1.  2^-inf = 0.
+DEVI float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 DEVI float wave_xor(float v, int mask) { return __shfl_xor(v, mask, 64); }
 
@@ -86,41 +94,49 @@ DEVI void store4(float *row, int c0, int dim, bool vec4, f4 x) {
     }
 }
 
-// Reads the NT floats p[0..NT) (the row-owner A operand): 128-bit reads when
-// NT % 4 == 0 (p then 16-byte aligned), else 64-bit reads.
+// Row-owner chunk width (floats) for NT column tiles.
 template <int NT>
-DEVI void lds_run(float (&x)[NT], const float *p) {
-    if constexpr (NT % 4 == 0) {
+constexpr int ro_chunk() { return NT % 4 == 0 ? 4 : 2; }
+
+// Reads the row-owner A operand of row rho from one LDS row: x[it] = row[d(rho, it)].
+// Rows must be 4C-byte aligned.
+template <int NT>
+DEVI void lds_run(float (&x)[NT], const float *row, int rho) {
+    constexpr int C = ro_chunk<NT>();
 #pragma unroll
-        for (int i = 0; i < NT; i += 4) {
-            const f4 v = *reinterpret_cast<const f4 *>(p + i);
-            x[i] = v.x; x[i + 1] = v.y; x[i + 2] = v.z; x[i + 3] = v.w;
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < NT; i += 2) {
-            const f2 v = *reinterpret_cast<const f2 *>(p + i);
-            x[i] = v.x; x[i + 1] = v.y;
+    for (int c = 0; c < NT / C; ++c) {
+        const float *p = row + 16 * C * c + C * rho;
+        if constexpr (C == 4) {
+            const f4 v = *reinterpret_cast<const f4 *>(p);
+            x[4 * c] = v.x; x[4 * c + 1] = v.y; x[4 * c + 2] = v.z; x[4 * c + 3] = v.w;
+        } else {
+            const f2 v = *reinterpret_cast<const f2 *>(p);
+            x[2 * c] = v.x; x[2 * c + 1] = v.y;
         }
     }
 }
 
-// Stores row r of row-owner accumulators, acc[it][r] * mul for it = 0..NT-1,
-// to row[c0 .. c0 + NT), c0 = (4 grp + r) * NT; columns >= dim are dropped.
-// 128-bit stores when rows are 16-byte aligned (vec4) and NT % 4 == 0, else
-// 64-bit stores (dim and c0 are even, so a pair never straddles dim).
+// Stores accumulator row r (output row rho = 4 grp + r) of row-owner
+// accumulators, acc[it][r] * mul, to its columns of `row`; columns >= dim are
+// dropped.  128-bit stores for 4-float chunks on 16-byte aligned rows (vec4),
+// else 64-bit stores (dim and chunk starts are even, so a pair never straddles dim).
 template <int NT>
-DEVI void store_run(float *row, int c0, int dim, bool vec4, const f4 (&acc)[NT], int r, float mul) {
-    if (NT % 4 == 0 && vec4) {
+DEVI void store_run(float *row, int rho, int dim, bool vec4, const f4 (&acc)[NT], int r, float mul) {
+    constexpr int C = ro_chunk<NT>();
 #pragma unroll
-        for (int i = 0; i < NT; i += 4)
-            if (c0 + i < dim)
-                *reinterpret_cast<f4 *>(row + c0 + i) =
-                    f4{acc[i][r], acc[i + 1][r], acc[i + 2][r], acc[i + 3][r]} * mul;
-    } else {
-#pragma unroll
-        for (int i = 0; i < NT; i += 2)
-            if (c0 + i < dim) *reinterpret_cast<f2 *>(row + c0 + i) = f2{acc[i][r], acc[i + 1][r]} * mul;
+    for (int c = 0; c < NT / C; ++c) {
+        const int col = 16 * C * c + C * rho;
+        if constexpr (C == 4) {
+            const f4 v = f4{acc[4 * c][r], acc[4 * c + 1][r], acc[4 * c + 2][r], acc[4 * c + 3][r]} * mul;
+            if (vec4) {
+                if (col < dim) *reinterpret_cast<f4 *>(row + col) = v;
+            } else {
+                if (col < dim) *reinterpret_cast<f2 *>(row + col) = f2{v.x, v.y};
+                if (col + 2 < dim) *reinterpret_cast<f2 *>(row + col + 2) = f2{v.z, v.w};
+            }
+        } else {
+            if (col < dim) *reinterpret_cast<f2 *>(row + col) = f2{acc[2 * c][r], acc[2 * c + 1][r]} * mul;
+        }
     }
 }
 
@@ -167,83 +183,21 @@ DEVI void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 template <int CPR>
 DEVI int swz(int chunk, int row) { return chunk ^ (row & (CPR % 16 == 0 ? 15 : 7)); }
 
-// Same from a swizzled unpadded tile (see swz): columns [c0, c0 + NT) of row r.
+// The row-owner A operand of row rho from row r of a swizzled unpadded tile (see swz).
 template <int NT, int CPR>
-DEVI void lds_run_swz(float (&x)[NT], const float *tile, int r, int c0) {
+DEVI void lds_run_swz(float (&x)[NT], const float *tile, int r, int rho) {
+    constexpr int C = ro_chunk<NT>();
     const float *rowp = tile + r * CPR * 4;
-    if constexpr (NT % 4 == 0) {
 #pragma unroll
-        for (int i = 0; i < NT; i += 4) {
-            const f4 v = *reinterpret_cast<const f4 *>(rowp + 4 * swz<CPR>((c0 + i) >> 2, r));
-            x[i] = v.x; x[i + 1] = v.y; x[i + 2] = v.z; x[i + 3] = v.w;
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < NT; i += 2) {
-            const int c = c0 + i;  // even: a 64-bit read never leaves its 16-byte chunk
-            const f2 v = *reinterpret_cast<const f2 *>(rowp + 4 * swz<CPR>(c >> 2, r) + (c & 3));
-            x[i] = v.x; x[i + 1] = v.y;
-        }
-    }
-}
-
-// Cooperative copy of `rows` rows x DP columns into LDS TRANSPOSED: element
-// (r, c) lands at lds[c * LT + r] (LT = rows + 4).  Consecutive lanes take
-// consecutive rows of one column chunk, so each scattered store of a wave hits
-// consecutive banks; a later 128-bit read of lds[n * LT + 4g .. 4g+3] then
-// yields four consecutive rows of column n, the A operand of four successive
-// k-steps.  Rows >= nvalid and columns >= dim are written as zero.
-template <int DP, int LT, int NT>
-DEVI void stage_rows_t(float *lds, const float *g, size_t ld, int rows, int nvalid, int dim, bool vec4,
-                       int tid) {
-    if (vec4) {
-        for (int e = tid; e < rows * (DP / 4); e += NT) {
-            const int r = e % rows, c = (e / rows) * 4;
-            f4 x = zero4();
-            if (r < nvalid && c < dim) x = *reinterpret_cast<const f4 *>(g + (size_t)r * ld + c);
-            lds[(c + 0) * LT + r] = x.x;
-            lds[(c + 1) * LT + r] = x.y;
-            lds[(c + 2) * LT + r] = x.z;
-            lds[(c + 3) * LT + r] = x.w;
-        }
-    } else {
-        for (int e = tid; e < rows * (DP / 2); e += NT) {
-            const int r = e % rows, c = (e / rows) * 2;
-            f2 x = f2{0.f, 0.f};
-            if (r < nvalid && c < dim) x = *reinterpret_cast<const f2 *>(g + (size_t)r * ld + c);
-            lds[(c + 0) * LT + r] = x.x;
-            lds[(c + 1) * LT + r] = x.y;
-        }
-    }
-}
-
-// One global read, two LDS layouts: element (r, c) of a rows x DP block goes to
-// rm[r * LW + c] (row-major, LW = DP + 4) and to tr[c * LT + r] (transposed,
-// LT = rows + 4).  Consecutive lanes take consecutive rows of one column chunk:
-// the row-major 128-bit stores then walk 4-bank steps (LW = DP + 4) and the
-// transposed scalar stores consecutive banks.  Zero beyond nvalid rows / dim.
-template <int DP, int LW, int LT, int NT>
-DEVI void stage_rows_both(float *rm, float *tr, const float *g, size_t ld, int rows, int nvalid, int dim,
-                          bool vec4, int tid) {
-    if (vec4) {
-        for (int e = tid; e < rows * (DP / 4); e += NT) {
-            const int r = e % rows, c = (e / rows) * 4;
-            f4 x = zero4();
-            if (r < nvalid && c < dim) x = *reinterpret_cast<const f4 *>(g + (size_t)r * ld + c);
-            *reinterpret_cast<f4 *>(rm + r * LW + c) = x;
-            tr[(c + 0) * LT + r] = x.x;
-            tr[(c + 1) * LT + r] = x.y;
-            tr[(c + 2) * LT + r] = x.z;
-            tr[(c + 3) * LT + r] = x.w;
-        }
-    } else {
-        for (int e = tid; e < rows * (DP / 2); e += NT) {
-            const int r = e % rows, c = (e / rows) * 2;
-            f2 x = f2{0.f, 0.f};
-            if (r < nvalid && c < dim) x = *reinterpret_cast<const f2 *>(g + (size_t)r * ld + c);
-            *reinterpret_cast<f2 *>(rm + r * LW + c) = x;
-            tr[(c + 0) * LT + r] = x.x;
-            tr[(c + 1) * LT + r] = x.y;
+    for (int c = 0; c < NT / C; ++c) {
+        const int col = 16 * C * c + C * rho;  // a C-float chunk never leaves its 16-byte chunk
+        const float *p = rowp + 4 * swz<CPR>(col >> 2, r) + (col & 3);
+        if constexpr (C == 4) {
+            const f4 v = *reinterpret_cast<const f4 *>(p);
+            x[4 * c] = v.x; x[4 * c + 1] = v.y; x[4 * c + 2] = v.z; x[4 * c + 3] = v.w;
+        } else {
+            const f2 v = *reinterpret_cast<const f2 *>(p);
+            x[2 * c] = v.x; x[2 * c + 1] = v.y;
         }
     }
 }
