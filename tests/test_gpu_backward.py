@@ -69,7 +69,7 @@ def test_backward_any_tile_cap(gpu, zt, oracle, max_tile):
 
 
 @pytest.mark.parametrize("env", [
-    {"ZT_ATTN_W8": "1"}, {"ZT_ATTN_W8": "1", "ZT_ATTN_PF": "1"},
+    {"ZT_ATTN_W8": "1", "ZT_ATTN_PF": "0"}, {"ZT_ATTN_W8": "1", "ZT_ATTN_PF": "1"},
     {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "0"}, {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "1"},
     {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "0", "ZT_ATTN_HS": "4"}, {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "1", "ZT_ATTN_HS": "4"},
     {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "0", "ZT_ATTN_HS": "1"}, {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "1", "ZT_ATTN_HS": "1"},

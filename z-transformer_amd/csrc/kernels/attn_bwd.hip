@@ -363,10 +363,10 @@ __device__ __forceinline__ void bwd_dq_lse_body(const BwdArgs &a) {
     }
 }
 
-template <int DP, int HS, int KW, bool PF = false>
+template <int DP, int HS, int KW, bool PF = false, int NU = 1>
 __device__ __forceinline__ void bwd_dkdv_body(const BwdArgs &a) {
     constexpr int LW = DP + 4, DQ = DP / 4, NT = DP / 16, NTH = 64 * KW * HS;
-    constexpr int BQ = 16;
+    constexpr int BQ = 16 * NU;  // query rows per stage: NU sub-tiles of 16
     // Per head-split part: Q rows, dO rows, and (m2, 1/l, delta) per row.
     // One buffer: the staging tiles, reused at the end for the head-split sum
     // ((HS-1) parts x KW blocks x 64 lanes x 2*NT float4).
@@ -503,52 +503,62 @@ __device__ __forceinline__ void bwd_dkdv_body(const BwdArgs &a) {
             }
             __syncthreads();
         }
-        if (t0 + 15 < s0 || s0 >= a.T) continue;  // wave-uniform: no visible pair
+        if (t0 + BQ - 1 < s0 || s0 >= a.T) continue;  // wave-uniform: no visible pair
 
-            // This lane's four query rows' statistics, read ahead of the MFMAs.
-            f4 stv[4];
+        // Sub-tile u holds query rows t0 + 16 u + [0, 16).  This lane's four
+        // rows' statistics per sub-tile are read ahead of the MFMAs.
+        f4 stv[NU][4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) stv[r] = *reinterpret_cast<const f4 *>(st + (4 * grp + r) * 4);
-            f4 s = zero4(), dp = zero4();
-            {
-                const float *qrow = qs + l16 * LW + grp * DQ;
-                const float *drow = ds + l16 * LW + grp * DQ;
+        for (int u = 0; u < NU; ++u)
 #pragma unroll
-                for (int kk = 0; kk < DQ; kk += 4) {
-                    const f4 qx = *reinterpret_cast<const f4 *>(qrow + kk);
-                    const f4 dx = *reinterpret_cast<const f4 *>(drow + kk);
-                    s = mfma16(qx.x, kr[kk + 0], s);
-                    dp = mfma16(dx.x, vr[kk + 0], dp);
-                    s = mfma16(qx.y, kr[kk + 1], s);
-                    dp = mfma16(dx.y, vr[kk + 1], dp);
-                    s = mfma16(qx.z, kr[kk + 2], s);
-                    dp = mfma16(dx.z, vr[kk + 2], dp);
-                    s = mfma16(qx.w, kr[kk + 3], s);
-                    dp = mfma16(dx.w, vr[kk + 3], dp);
-                }
+            for (int r = 0; r < 4; ++r) stv[u][r] = *reinterpret_cast<const f4 *>(st + (16 * u + 4 * grp + r) * 4);
+        f4 s[NU], dp[NU];
+#pragma unroll
+        for (int u = 0; u < NU; ++u) { s[u] = zero4(); dp[u] = zero4(); }
+#pragma unroll
+        for (int kk = 0; kk < DQ; kk += 4) {
+#pragma unroll
+            for (int u = 0; u < NU; ++u) {
+                const f4 qx = *reinterpret_cast<const f4 *>(qs + (16 * u + l16) * LW + grp * DQ + kk);
+                const f4 dx = *reinterpret_cast<const f4 *>(ds + (16 * u + l16) * LW + grp * DQ + kk);
+                s[u] = mfma16(qx.x, kr[kk + 0], s[u]);
+                dp[u] = mfma16(dx.x, vr[kk + 0], dp[u]);
+                s[u] = mfma16(qx.y, kr[kk + 1], s[u]);
+                dp[u] = mfma16(dx.y, vr[kk + 1], dp[u]);
+                s[u] = mfma16(qx.z, kr[kk + 2], s[u]);
+                dp[u] = mfma16(dx.z, vr[kk + 2], dp[u]);
+                s[u] = mfma16(qx.w, kr[kk + 3], s[u]);
+                dp[u] = mfma16(dx.w, vr[kk + 3], dp[u]);
             }
-            // s[r] = S[t = t0 + 4 grp + r][key = s0 + l16]
-            f4 p, dsv;
+        }
+        // s[u][r] = S[t = t0 + 16 u + 4 grp + r][key = s0 + l16]
+        f4 p[NU], dsv[NU];
+#pragma unroll
+        for (int u = 0; u < NU; ++u)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int t = t0 + 4 * grp + r;
+                const int t = t0 + 16 * u + 4 * grp + r;
                 const bool vis = (t < a.T) && (t >= my_key);
-                const float e = fast_exp2(s[r] - stv[r].x) * stv[r].y;
-                p[r] = vis ? e : 0.f;
-                dsv[r] = p[r] * (dp[r] - stv[r].z);
+                const float e = fast_exp2(s[u][r] - stv[u][r].x) * stv[u][r].y;
+                p[u][r] = vis ? e : 0.f;
+                dsv[u][r] = p[u][r] * (dp[u][r] - stv[u][r].z);
             }
+#pragma unroll
+        for (int u = 0; u < NU; ++u) {
+            if (t0 + 16 * u + 15 < s0) continue;  // wave-uniform: this sub-tile is wholly masked
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk) {
                 float dx[NT], qx[NT];  // dO^T, Q^T rows in the row-owner layout
-                lds_run<NT>(dx, ds + (4 * grp + kk) * LW, l16);
-                lds_run<NT>(qx, qs + (4 * grp + kk) * LW, l16);
-                const float pv = p[kk], dv = dsv[kk];
+                lds_run<NT>(dx, ds + (16 * u + 4 * grp + kk) * LW, l16);
+                lds_run<NT>(qx, qs + (16 * u + 4 * grp + kk) * LW, l16);
+                const float pv = p[u][kk], dv = dsv[u][kk];
 #pragma unroll
                 for (int i = 0; i < NT; ++i) {
                     dva[i] = mfma16(dx[i], pv, dva[i]);
                     dka[i] = mfma16(qx[i], dv, dka[i]);
                 }
             }
+        }
     }
 
     // Sum the head-split partials in a fixed order (part 0 + 1 + ...).
