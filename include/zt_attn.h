@@ -193,6 +193,15 @@ int zt_rope_qk_forward(const float *q, const float *k, float *q_out, float *k_ou
 int zt_rope_qk_backward(const float *dq, const float *dk, float *dq_out, float *dk_out, int B, int T,
                         int n_heads, int n_kv_heads, int head_dim, int pos, double theta, hipStream_t stream);
 
+/* Roofline calibration (no reference counterpart): the FP32 MFMA rate this
+ * device sustains (two interleaved v_mfma_f32_16x16x4_f32 chains per wave,
+ * four waves per SIMD) and the HBM rate of a streaming 16-byte-load read of
+ * `src` (the decode kernel's access pattern), each the minimum time of three
+ * runs after a warm-up.  scratch: one float per probe thread (>= 2048 * 256 * 4
+ * bytes).  Synchronises the stream. */
+int zt_calibrate(const float *src, size_t src_bytes, float *scratch, size_t scratch_bytes, double *mfma_tflops,
+                 double *read_gbs, hipStream_t stream);
+
 /* Seeded synthetic inputs (splitmix64 counter stream + Box-Muller): element i
  * depends only on (seed, i).  normal: mean + sigma*z; uniform: [lo, hi). */
 int zt_fill_normal(float *dst, size_t n, uint64_t seed, double mean, double sigma, hipStream_t stream);

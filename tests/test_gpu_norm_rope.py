@@ -125,3 +125,15 @@ def test_device_fill_matches_host_generator(gpu, zt, oracle):
     assert max_abs(host(t), ref) <= 1e-6
     u = dev_uniform(gpu, zt, 10_000, SEED_W, 0.5, 1.5)
     assert max_abs(host(u), oracle.fill_uniform(10_000, SEED_W, 0.5, 1.5)) <= 1e-7
+
+
+def test_calibration_probes_report_plausible_rates(gpu, zt):
+    # Sustained FP32 MFMA below the 157.3 TFLOP/s datasheet peak but near it;
+    # a streaming read below the 8 TB/s HBM peak.
+    src = gpu.empty(1 << 28, device="cuda")
+    scratch = gpu.empty(2048 * 256, device="cuda")
+    tf, gbs = zt.calibrate(src, scratch)
+    assert 100.0 < tf < 160.0, tf
+    assert 2000.0 < gbs < 8200.0, gbs
+    with pytest.raises(zt.ZtRefused):
+        zt.calibrate(src, gpu.empty(16, device="cuda"))

@@ -84,3 +84,12 @@ struct AppendArgs {
     int b_base, nb, n_ctx, H, Hkv, dim;
     double theta;
 };
+
+// Calibration probes (calibrate.hip).
+struct CalArgs {
+    const float *src;   // streaming-read source (16-byte aligned)
+    unsigned long long n4;  // float4 elements to read
+    float *out;         // one float per thread
+    int iters;          // MFMA iterations per chain
+};
+

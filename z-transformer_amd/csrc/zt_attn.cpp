@@ -31,6 +31,7 @@ extern const unsigned char zt_co_fwd[], zt_co_fwd_end[];
 extern const unsigned char zt_co_bwd[], zt_co_bwd_end[];
 extern const unsigned char zt_co_dec[], zt_co_dec_end[];
 extern const unsigned char zt_co_misc[], zt_co_misc_end[];
+extern const unsigned char zt_co_cal[], zt_co_cal_end[];
 }
 
 namespace {
@@ -44,7 +45,7 @@ struct DeviceState {
     bool ok = false;
     size_t lds_limit = 0;
     int cus = 0;
-    hipModule_t mods[4] = {};
+    hipModule_t mods[5] = {};
     std::mutex mu;
     std::unordered_map<std::string, hipFunction_t> fns;
 };
@@ -54,8 +55,8 @@ void load_device(DeviceState &st, int dev) {
     int lds = 0;
     if (hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || lds <= 0)
         return;
-    const unsigned char *images[4] = {zt_co_fwd, zt_co_bwd, zt_co_dec, zt_co_misc};
-    for (int i = 0; i < 4; ++i) {
+    const unsigned char *images[5] = {zt_co_fwd, zt_co_bwd, zt_co_dec, zt_co_misc, zt_co_cal};
+    for (int i = 0; i < 5; ++i) {
         if (hipModuleLoadData(&st.mods[i], images[i]) != hipSuccess) {
             fprintf(stderr, "zt_attn: the gfx950 code object %d would not load on device %d.\n", i, dev);
             return;
@@ -88,6 +89,7 @@ int module_of(const char *name) {
     if (strncmp(name, "zt_fwd", 6) == 0) return 0;
     if (strncmp(name, "zt_bwd", 6) == 0) return 1;
     if (strncmp(name, "zt_dec", 6) == 0) return 2;
+    if (strncmp(name, "zt_cal", 6) == 0) return 4;
     return 3;
 }
 
@@ -846,6 +848,53 @@ int zt_attn_plan_train(int B, int T, int n_heads, int n_kv_heads, int dim, char 
                        size_t len) {
     if (zt_attn_plan(B, T, n_heads, n_kv_heads, dim, 64, fwd, dq, dkdv, len)) return 1;
     snprintf(dq, len, "zt_bwd_dql_d%d_k32", pad32(dim));
+    return 0;
+}
+
+int zt_calibrate(const float *src, size_t src_bytes, float *scratch, size_t scratch_bytes, double *mfma_tflops,
+                 double *read_gbs, hipStream_t stream) {
+    DeviceState *st = require_device();
+    if (!st) return 1;
+    const unsigned mfma_blocks = (unsigned)st->cus * 4u;  // 4 waves per SIMD
+    const unsigned read_blocks = 2048u;
+    const size_t need = (size_t)(mfma_blocks > read_blocks ? mfma_blocks : read_blocks) * kThreads * sizeof(float);
+    if (!src || !scratch || !mfma_tflops || !read_gbs || scratch_bytes < need || src_bytes < (1u << 20) ||
+        (uintptr_t)src % 16 != 0) {
+        fprintf(stderr, "zt_calibrate: needs a 16-byte aligned source of at least 1 MiB and %zu bytes of scratch.\n",
+                need);
+        return 1;
+    }
+    hipEvent_t e0, e1;
+    if (hipEventCreate(&e0) != hipSuccess) return 1;
+    if (hipEventCreate(&e1) != hipSuccess) {
+        (void)hipEventDestroy(e0);
+        return 1;
+    }
+    CalArgs a{src, (unsigned long long)(src_bytes / 16), scratch, 20000};
+    int rc = 0;
+    float best_mfma = 1e30f, best_read = 1e30f;
+    for (int rep = 0; rep < 4 && rc == 0; ++rep) {  // the first of each pair warms up; min over the rest
+        float ms = 0.f;
+        rc |= hipEventRecord(e0, stream) != hipSuccess;
+        rc |= launch(st, "zt_cal_mfma", mfma_blocks, a, stream);
+        rc |= hipEventRecord(e1, stream) != hipSuccess;
+        rc |= hipEventSynchronize(e1) != hipSuccess;
+        rc |= hipEventElapsedTime(&ms, e0, e1) != hipSuccess;
+        if (rep > 0 && ms < best_mfma) best_mfma = ms;
+        rc |= hipEventRecord(e0, stream) != hipSuccess;
+        rc |= launch(st, "zt_cal_read", read_blocks, a, stream);
+        rc |= hipEventRecord(e1, stream) != hipSuccess;
+        rc |= hipEventSynchronize(e1) != hipSuccess;
+        rc |= hipEventElapsedTime(&ms, e0, e1) != hipSuccess;
+        if (rep > 0 && ms < best_read) best_read = ms;
+    }
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    if (rc) return 1;
+    // 2 chains x iters MFMAs of 16 x 16 x 4 x 2 FLOPs per wave, 4 waves per workgroup.
+    const double flop = 2.0 * a.iters * 2048.0 * 4.0 * mfma_blocks;
+    *mfma_tflops = flop / (best_mfma * 1e-3) / 1e12;
+    *read_gbs = (double)a.n4 * 16.0 / (best_read * 1e-3) / 1e9;
     return 0;
 }
 

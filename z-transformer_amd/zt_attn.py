@@ -23,7 +23,7 @@ ABI_SYMBOLS = [
     "zt_rmsnorm_forward", "zt_rope_forward", "zt_rope_backward", "zt_rope_qk_forward",
     "zt_rope_qk_backward", "zt_fill_normal", "zt_fill_uniform", "zt_attn_version",
     "zt_attn_lds_limit", "zt_attn_plan", "zt_attn_forward_train", "zt_attn_backward_train",
-    "zt_attn_bwd_dq_train", "zt_attn_bwd_dkdv_train", "zt_attn_plan_train",
+    "zt_attn_bwd_dq_train", "zt_attn_bwd_dkdv_train", "zt_attn_plan_train", "zt_calibrate",
 ]
 HOLDER_SYMBOLS = [
     "zt_bytes_for", "zt_to_cint", "zt_forward_bounds", "zt_holder_init", "zt_holder_deinit",
@@ -72,6 +72,7 @@ def lib():
             "zt_attn_bwd_dq_train": (I, [P] * 8 + [I] * 5 + [P]),
             "zt_attn_bwd_dkdv_train": (I, [P] * 9 + [I] * 5 + [P]),
             "zt_attn_plan_train": (I, [I] * 5 + [P, P, P, Z]),
+            "zt_calibrate": (I, [P, Z, P, Z, P, P, P]),
             "zt_rope_forward": (I, [P, P, I, I, I, D, I, P]),
             "zt_rope_backward": (I, [P, P, I, I, I, D, I, P]),
             "zt_rope_qk_forward": (I, [P, P, P, P, I, I, I, I, I, I, D, P]),
@@ -258,6 +259,15 @@ def rope_qk(q, k, q_out, k_out, B, T, n_heads, n_kv_heads, head_dim, pos=0, thet
     fn = lib().zt_rope_qk_backward if backward else lib().zt_rope_qk_forward
     _check(fn(_ptr(q), _ptr(k), _ptr(q_out), _ptr(k_out), B, T, n_heads, n_kv_heads, head_dim, pos, theta,
               _stream(stream)), "zt_rope_qk")
+
+
+def calibrate(src, scratch, stream=None):
+    """(sustained FP32 MFMA TFLOP/s, streaming-read GB/s) measured on this device."""
+    _f32_cuda(src, scratch)
+    tf, gb = ctypes.c_double(0.0), ctypes.c_double(0.0)
+    _check(lib().zt_calibrate(_ptr(src), src.numel() * 4, _ptr(scratch), scratch.numel() * 4, ctypes.addressof(tf),
+                              ctypes.addressof(gb), _stream(stream)), "zt_calibrate")
+    return tf.value, gb.value
 
 
 def fill_normal(t, seed, mean=0.0, sigma=1.0, stream=None):
