@@ -228,6 +228,18 @@ def main():
     log(f"C4 decode_step (rope + append + attention): {t_step * 1e3:.1f} us, {step_gbs:.0f} GB/s")
     del kc, vc, qd, od, ws, kn, vn, ws2
 
+    # ---------------- dense products (tensor.matmul and its gradients) ----------------
+    mm = {}
+    for tag, (M, K, N) in (("4096^3", (4096, 4096, 4096)), ("w_down 256x512x128", (256, 512, 128)),
+                           ("w_up 256x128x512", (256, 128, 512)), ("head 256x128x456", (256, 128, 456))):
+        a, b = normal(M * K, SEEDS["x"]), normal(K * N, SEEDS["w"])
+        c = torch.empty(M * N, device=dev)
+        t_mm = event_time(torch, lambda: zt.matmul(a, b, c, M, K, N), 10)
+        tf = 2.0 * M * K * N / (t_mm * 1e-3) / 1e12
+        mm[tag] = {"us": round(t_mm * 1e3, 2), "TFLOP/s": round(tf, 2), "frac_mfma_f32": round(tf / PEAK_MFMA_F32, 4)}
+        log(f"matmul {tag}: {t_mm * 1e3:.1f} us, {tf:.2f} TFLOP/s")
+        del a, b, c
+
     # ---------------- RMSNorm over rotating buffers ----------------
     norm = {}
     for rows, cols, sets in ((64, 4096, 256), (4096, 4096, 4)):
@@ -310,6 +322,7 @@ def main():
                    "GB/s": round(dec_gbs, 1), "bytes": dec_bytes, "frac_hbm": round(dec_gbs / PEAK_HBM, 4),
                    "step_us": round(t_step * 1e3, 2), "step_GB/s": round(step_gbs, 1)},
         "rmsnorm": norm,
+        "matmul": mm,
         "calibration": {"mfma_f32_tflops": round(cal_tflops, 1), "read_GB/s": round(cal_gbs, 1),
                         "dominant_frac_of_sustained": round(dom["tflops"] / cal_tflops, 4),
                         "decode_frac_of_streaming_read": round(dec_gbs / cal_gbs, 4)},

@@ -193,6 +193,18 @@ int zt_rope_qk_forward(const float *q, const float *k, float *q_out, float *k_ou
 int zt_rope_qk_backward(const float *dq, const float *dk, float *dq_out, float *dk_out, int B, int T,
                         int n_heads, int n_kv_heads, int head_dim, int pos, double theta, hipStream_t stream);
 
+/* ---- Dense products of the model step (no reference C entry point) ----
+ * src/tensor.zig:78-106 (tensor.matmul) on the device: out[M,N] = a[M,K] b[K,N],
+ * row-major f32, FP32 MFMA with f32 accumulation (the reference reduces in f32
+ * too, src/tensor_test.zig:185-273; only the rounding order differs).  K = 0
+ * writes zeros; M = 0 or N = 0 writes nothing.  The reference's
+ * DimensionMismatch is the caller's shape check (sizes are explicit here). */
+int zt_matmul(const float *a, const float *b, float *out, int M, int K, int N, hipStream_t stream);
+/* src/autograd.zig:958-972 (weightGrad): w[I,J] += input[T,I]^T dout[T,J]. */
+int zt_weight_grad(float *w, const float *input, const float *dout, int T, int I, int J, hipStream_t stream);
+/* src/autograd.zig:999-1022 (inputGrad): din[T,I] += dout[T,J] w[I,J]^T. */
+int zt_input_grad(float *din, const float *dout, const float *w, int T, int J, int I, hipStream_t stream);
+
 /* Roofline calibration (no reference counterpart): the FP32 MFMA rate this
  * device sustains (two interleaved v_mfma_f32_16x16x4_f32 chains per wave,
  * four waves per SIMD) and the HBM rate of a streaming 16-byte-load read of

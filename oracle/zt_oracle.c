@@ -13,10 +13,15 @@
  *   zto_attn_step              src/decode.zig:326-392
  *   zto_rmsnorm                src/norm.zig:14-47
  *   zto_rope                   src/rope.zig:21-55
+ *   zto_rope_backward          src/autograd.zig:851-872
+ *   zto_decode_step            src/decode.zig:244-270, src/kv_cache.zig:88-95
+ *   zto_matmul                 src/tensor.zig:78-106
+ *   zto_weight_grad            src/autograd.zig:958-972
+ *   zto_input_grad             src/autograd.zig:999-1022
  * The generators are this build's own (splitmix64, Steele/Lea/Flood 2014, and
  * the Box-Muller transform); the reference used an LCG (src/cuda/attn_twin.zig:283-289).
  *
- * How each function is pinned is recorded in tests/test_oracle_*.py: the
+ * How each function is pinned is recorded in tests/test_oracle.py: the
  * reference's own known-answer tests (as fixtures in tests/golden/), closed
  * forms, brute force and finite differences.
  */
@@ -402,6 +407,49 @@ int zto_decode_step(const float *q, const float *k_new, const float *v_new, floa
     }
     free(q_pos);
     return rc;
+}
+
+/* out[i][j] = sum_k a[i][k] b[k][j]: one f32 accumulator per output element,
+ * k ascending, each product rounded to f32 and then added (Zig's strict float
+ * mode contracts nothing); the 8-lane unrolling of tensor.zig:84-93 does not
+ * change any element's sequence. */
+void zto_matmul(const float *a, const float *b, float *out, int M, int K, int N) {
+    for (int i = 0; i < M; ++i)
+        for (int j = 0; j < N; ++j) {
+            float acc = 0.f;
+            for (int k = 0; k < K; ++k) {
+                const float prod = a[(size_t)i * K + k] * b[(size_t)k * N + j];
+                acc += prod;
+            }
+            out[(size_t)i * N + j] = acc;
+        }
+}
+
+/* w[i][j] += input[t][i] * dout[t][j], as an f32 read-modify-write per term,
+ * i outer, t ascending, j inner (autograd.zig:960-969). */
+void zto_weight_grad(float *w, const float *input, const float *dout, int T, int I, int J) {
+    for (int i = 0; i < I; ++i)
+        for (int t = 0; t < T; ++t) {
+            const float scale = input[(size_t)t * I + i];
+            for (int j = 0; j < J; ++j) {
+                const float prod = scale * dout[(size_t)t * J + j];
+                w[(size_t)i * J + j] += prod;
+            }
+        }
+}
+
+/* out[t][i] += sum_j dout[t][j] * w[i][j]: the sum in one f32 accumulator over
+ * j ascending, added to out once (autograd.zig:1001-1020). */
+void zto_input_grad(float *out, const float *dout, const float *w, int T, int J, int I) {
+    for (int t = 0; t < T; ++t)
+        for (int i = 0; i < I; ++i) {
+            float acc = 0.f;
+            for (int j = 0; j < J; ++j) {
+                const float prod = dout[(size_t)t * J + j] * w[(size_t)i * J + j];
+                acc += prod;
+            }
+            out[(size_t)t * I + i] += acc;
+        }
 }
 
 uint64_t zto_splitmix64(uint64_t seed, uint64_t counter) {

@@ -97,6 +97,16 @@ int zto_rope_backward(const float *dout, float *din, int rows, int cols, int pos
 int zto_decode_step(const float *q, const float *k_new, const float *v_new, float *k_cache, float *v_cache,
                     float *out, const int *pos, int B, int n_ctx, int H, int Hkv, int D, double theta);
 
+/* src/tensor.zig:78-106 (matmul): out[M,N] = a[M,K] b[K,N], f32 accumulator,
+ * k ascending, products rounded before the add. */
+void zto_matmul(const float *a, const float *b, float *out, int M, int K, int N);
+/* src/autograd.zig:958-972 (weightGrad): w[I,J] += input[T,I]^T dout[T,J], an
+ * f32 read-modify-write per term, i -> t -> j. */
+void zto_weight_grad(float *w, const float *input, const float *dout, int T, int I, int J);
+/* src/autograd.zig:999-1022 (inputGrad): out[T,I] += dout[T,J] w[I,J]^T, one
+ * f32 accumulator per element over j ascending, added once. */
+void zto_input_grad(float *out, const float *dout, const float *w, int T, int J, int I);
+
 /* Seeded inputs: splitmix64 counter stream -> Box-Muller.  Element i uses
  * the 64-bit outputs at counters 2i and 2i+1, so any element can be made on
  * its own.  out[i] = (float)(mean + sigma * z_i). */

@@ -34,6 +34,9 @@ def lib():
             "zto_rope": (I, [P, P, I, I, I, D, I]),
             "zto_rope_backward": (I, [P, P, I, I, I, D, I]),
             "zto_decode_step": (I, [P] * 7 + [I] * 5 + [D]),
+            "zto_matmul": (None, [P, P, P, I, I, I]),
+            "zto_weight_grad": (None, [P, P, P, I, I, I]),
+            "zto_input_grad": (None, [P, P, P, I, I, I]),
             "zto_fill_normal": (None, [P, Z, U, D, D]),
             "zto_fill_uniform": (None, [P, Z, U, D, D]),
             "zto_splitmix64": (U, [U, U]),
@@ -155,6 +158,30 @@ def decode_step(q, k_new, v_new, k_cache, v_cache, pos, B, n_ctx, H, Hkv, D, the
     if rc:
         raise OracleRefused(rc)
     return out, kc, vc
+
+
+def matmul(a, b, M, K, N):
+    """src/tensor.zig:78-106."""
+    a, b = _f32(a), _f32(b)
+    out = np.zeros(M * N, np.float32)
+    lib().zto_matmul(_p(a), _p(b), _p(out), M, K, N)
+    return out
+
+
+def weight_grad(w, inp, dout, T, I, J):
+    """src/autograd.zig:958-972; returns w + input^T dout (w is not modified)."""
+    w = np.array(w, dtype=np.float32, copy=True).ravel()
+    inp, dout = _f32(inp), _f32(dout)
+    lib().zto_weight_grad(_p(w), _p(inp), _p(dout), T, I, J)
+    return w
+
+
+def input_grad(out, dout, w, T, J, I):
+    """src/autograd.zig:999-1022; returns out + dout w^T (out is not modified)."""
+    out = np.array(out, dtype=np.float32, copy=True).ravel()
+    dout, w = _f32(dout), _f32(w)
+    lib().zto_input_grad(_p(out), _p(dout), _p(w), T, J, I)
+    return out
 
 
 def fill_normal(n, seed, mean=0.0, sigma=1.0):

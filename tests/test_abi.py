@@ -151,6 +151,16 @@ def test_train_path_refusals(zt, capfd):
     assert "not a group" in capfd.readouterr().err
 
 
+def test_dense_product_refusals(zt, capfd):
+    L = zt.lib()
+    assert L.zt_matmul(NULL, NULL, NULL, -1, 2, 2, NULL) == 1 and "not launchable" in capfd.readouterr().err
+    assert L.zt_matmul(NULL, NULL, NULL, 0, 5, 7, NULL) == 0   # no rows: nothing to write
+    assert L.zt_matmul(NULL, NULL, NULL, 3, 5, 0, NULL) == 0
+    assert L.zt_matmul(NULL, NULL, NULL, 3, 5, 2, NULL) == 1 and "null" in capfd.readouterr().err
+    assert L.zt_weight_grad(NULL, NULL, NULL, 4, -2, 3, NULL) == 1
+    assert L.zt_input_grad(NULL, NULL, NULL, 4, 3, 0, NULL) == 0
+
+
 def test_decode_refuses_misaligned_rows(zt, capfd):
     # dim % 4 == 0 rows are read 16 bytes at a time; dim % 4 == 2 rows 8 at a time.
     L = zt.lib()

@@ -371,3 +371,57 @@ def test_generators_are_seeded_and_well_formed(oracle):
     assert u.min() >= 0.5 and u.max() < 1.5 and abs(u.mean() - 1.0) < 0.01
     # splitmix64 known value (seed 0, first output), Vigna's reference generator.
     assert oracle.splitmix64(0, 0) == 0xE220A8397B1DCDAF
+
+
+# ------------------------------------------------------------------ matmul --
+
+def test_matmul_reference_known_answers(oracle, golden):
+    for c in golden["matmul"]:
+        got = oracle.matmul(c["a"], c["b"], c["M"], c["K"], c["N"])
+        assert np.array_equal(got, np.float32(c["out"])), c["src"]
+
+
+def _f32_gate(got, a, b, M, K, N):
+    """The reference's accumulator-width statistic (src/tensor_test.zig:185-273):
+    worst |got - f32(exact)| / sum|products|."""
+    a64, b64 = a.reshape(M, K).astype(np.float64), b.reshape(K, N).astype(np.float64)
+    exact = a64 @ b64
+    abs_sum = np.abs(a64) @ np.abs(b64)
+    wide = exact.astype(np.float32).astype(np.float64)
+    return float(np.max(np.abs(got.reshape(M, N).astype(np.float64) - wide) / abs_sum))
+
+
+def test_matmul_reduces_in_f32_not_f64(oracle, golden):
+    c = golden["matmul_f32_gate"]
+    M, K, N = c["M"], c["K"], c["N"]
+    rng = np.random.default_rng(7)
+    a = rng.uniform(c["lo"], c["hi"], M * K).astype(np.float32)
+    b = rng.uniform(c["lo"], c["hi"], K * N).astype(np.float32)
+    worst = _f32_gate(oracle.matmul(a, b, M, K, N), a, b, M, K, N)
+    assert (K - 1) * np.finfo(np.float64).eps < worst < (K - 1) * np.finfo(np.float32).eps
+    # A reduction carried in f64 (then stored in f32) sits on the f64 side of the gate.
+    wide = (a.reshape(M, K).astype(np.float64) @ b.reshape(K, N)).astype(np.float32)
+    assert _f32_gate(wide.ravel(), a, b, M, K, N) <= (K - 1) * np.finfo(np.float64).eps
+
+
+@pytest.mark.parametrize("T,I,J", [(1, 1, 1), (7, 5, 9), (64, 24, 40), (300, 16, 8)])
+def test_weight_and_input_grads_are_the_transposed_products(oracle, T, I, J):
+    # weightGrad from zero is matmul(input^T, dout) and inputGrad from zero is
+    # matmul(dout, w^T): the same products summed in the same order, so equal
+    # bit for bit; a transposed operand or a swapped index fails.
+    rng = np.random.default_rng(T * 100 + I)
+    inp, dout = _rand(rng, T, I), _rand(rng, T, J)
+    w = _rand(rng, I, J)
+    wg = oracle.weight_grad(np.zeros(I * J), inp, dout, T, I, J)
+    assert np.array_equal(wg, oracle.matmul(np.ascontiguousarray(inp.T), dout, I, T, J))
+    ig = oracle.input_grad(np.zeros(T * I), dout, w, T, J, I)
+    assert np.array_equal(ig, oracle.matmul(dout, np.ascontiguousarray(w.T), T, J, I))
+    # Both accumulate onto what the buffer held (Tensor.init zeroes; blockBackward reuses).
+    w0 = _rand(rng, I, J)
+    wg2 = oracle.weight_grad(w0, inp, dout, T, I, J)
+    want = w0.astype(np.float64).ravel() + (inp.astype(np.float64).T @ dout).ravel()
+    assert np.max(np.abs(wg2 - want)) <= 1e-5 * max(1.0, np.abs(want).max())
+    o0 = _rand(rng, T, I)
+    ig2 = oracle.input_grad(o0, dout, w, T, J, I)
+    want = o0.astype(np.float64).ravel() + (dout.astype(np.float64) @ w.T).ravel()
+    assert np.max(np.abs(ig2 - want)) <= 1e-5 * max(1.0, np.abs(want).max())

@@ -93,3 +93,14 @@ struct CalArgs {
     int iters;          // MFMA iterations per chain
 };
 
+// Dense f32 product C (+)= op(A) op(B) (gemm.hip).
+struct GemmArgs {
+    const float *a, *b;
+    float *c;
+    int M, N, K;
+    int lda, ldb, ldc;     // row strides in floats of the matrices as stored
+    int accumulate;        // 0: C = product; 1: C += product
+    bool vec_a, vec_b;     // 16-byte loads allowed along the contiguous dimension
+    bool vec_c;            // 16-byte stores allowed along C's rows
+};
+

@@ -1,0 +1,173 @@
+// f32 GEMM on FP32 MFMA for the model's dense products (gfx950):
+//   zt_gemm_nn: C  = A B      src/tensor.zig:78-106 (tensor.matmul)
+//   zt_gemm_tn: C += A^T B    src/autograd.zig:958-972 (weightGrad: w += input^T dout)
+//   zt_gemm_nt: C += A B^T    src/autograd.zig:999-1022 (inputGrad: d input += dout w^T)
+// All matrices row-major f32.  op(A) is M x K, op(B) is K x N, C is M x N.
+//
+// A workgroup of 4 waves computes a 128 x 128 tile of C, each wave a 64 x 64
+// quarter as 4 x 4 tiles of 16 x 16: 16 independent accumulation chains of
+// v_mfma_f32_16x16x4_f32.  Each 32-deep k slab of both operands is copied to
+// LDS in the orientation it has in memory, with 16-byte loads and stores:
+//   * k-contiguous (A as stored, B^T as stored): LDS [index][k], stride 36.
+//     Lane group grp owns k in [8 grp, 8 grp + 8) of the slab (the contraction
+//     is order-free across k-steps), so one 128-bit read gives a lane's
+//     operand for four k-steps of one tile; tile t's local index l16 is
+//     16 t + l16 of the wave's 64.
+//   * index-contiguous (A^T or B as stored): LDS [k][index], stride 132.
+//     Here a lane's four tiles are the four consecutive indices 4 l16 + t, so
+//     one 128-bit read gives its operand for all four tiles at one k.
+// Either way a k-step group of 4 x 4 x 4 MFMAs needs four 128-bit reads per
+// operand, and no scattered (transposing) LDS writes are needed.  The next slab
+// is prefetched into registers while the current one computes.  Accumulation
+// is f32 inside the MFMA; the result differs from the reference's sequential
+// f32 sum only in rounding order.
+#include "common.h"
+#include "args.h"
+
+namespace {
+
+constexpr int BT = 128, BK = 32, NTHR = 256;
+constexpr int LKC = BK + 4;   // row stride of a k-contiguous slab
+constexpr int LIC = BT + 4;   // row stride of an index-contiguous slab
+constexpr int NCH = BT * BK / 4 / NTHR;  // 16-byte chunks per thread per operand (4)
+
+// The 4 floats p[0..3] of a row with `avail` valid elements from p: one
+// 16-byte load when vec and all 4 are valid, else guarded scalar loads.
+DEVI f4 load4(const float *p, int avail, bool vec) {
+    if (vec && avail >= 4) return *reinterpret_cast<const f4 *>(p);
+    f4 x = zero4();
+    if (avail > 0) x.x = p[0];
+    if (avail > 1) x.y = p[1];
+    if (avail > 2) x.z = p[2];
+    if (avail > 3) x.w = p[3];
+    return x;
+}
+
+// Slab fetch of one operand into registers.  KC: memory rows are the tile
+// index (r0..r0+127, < rmax), k contiguous (k0..k0+31, < kmax).  Otherwise
+// memory rows are k and the index is contiguous.
+template <bool KC>
+DEVI void fetch(f4 (&pf)[NCH], const float *base, int ld, int r0, int rmax, int k0, int kmax, bool vec, int tid) {
+#pragma unroll
+    for (int n = 0; n < NCH; ++n) {
+        const int e = tid + n * NTHR;
+        if constexpr (KC) {
+            const int r = r0 + e / (BK / 4), k = k0 + 4 * (e % (BK / 4));
+            pf[n] = r < rmax ? load4(base + (size_t)r * ld + k, kmax - k, vec) : zero4();
+        } else {
+            const int k = k0 + e / (BT / 4), r = r0 + 4 * (e % (BT / 4));
+            pf[n] = k < kmax ? load4(base + (size_t)k * ld + r, rmax - r, vec) : zero4();
+        }
+    }
+}
+
+template <bool KC>
+DEVI void put(float *lds, const f4 (&pf)[NCH], int tid) {
+#pragma unroll
+    for (int n = 0; n < NCH; ++n) {
+        const int e = tid + n * NTHR;
+        if constexpr (KC)
+            *reinterpret_cast<f4 *>(lds + (e / (BK / 4)) * LKC + 4 * (e % (BK / 4))) = pf[n];
+        else
+            *reinterpret_cast<f4 *>(lds + (e / (BT / 4)) * LIC + 4 * (e % (BT / 4))) = pf[n];
+    }
+}
+
+// A lane's operand block x[t][c] for tiles t = 0..3 and k-steps c = 0..3 of
+// half h of the slab, w0 = the wave's first index (0 or 64).
+template <bool KC>
+DEVI void operand(f4 (&x)[4], const float *lds, int w0, int l16, int grp, int h) {
+    if constexpr (KC) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) x[t] = *reinterpret_cast<const f4 *>(lds + (w0 + 16 * t + l16) * LKC + 8 * grp + 4 * h);
+    } else {
+        f4 y[4];  // y[c][t]
+#pragma unroll
+        for (int c = 0; c < 4; ++c) y[c] = *reinterpret_cast<const f4 *>(lds + (8 * grp + 4 * h + c) * LIC + w0 + 4 * l16);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) x[t] = f4{y[0][t], y[1][t], y[2][t], y[3][t]};
+    }
+}
+
+// Index within the wave's 64 of tile t's local row/column j.
+template <bool KC>
+DEVI int local_index(int t, int j) { return KC ? 16 * t + j : 4 * j + t; }
+
+// A_KC: A stored M x K (else K x M).  B_KC: B stored N x K (else K x N).
+template <bool A_KC, bool B_KC>
+DEVI void gemm_body(const GemmArgs &g) {
+    __shared__ __attribute__((aligned(16))) float As[A_KC ? BT * LKC : BK * LIC];
+    __shared__ __attribute__((aligned(16))) float Bs[B_KC ? BT * LKC : BK * LIC];
+    const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, grp = lane >> 4, w = tid >> 6;
+    const int wm = 64 * (w >> 1), wn = 64 * (w & 1);
+    const int tiles_n = (g.N + BT - 1) / BT;
+    const int m0 = (int)(blockIdx.x / tiles_n) * BT, n0 = (int)(blockIdx.x % tiles_n) * BT;
+
+    f4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = zero4();
+
+    f4 pa[NCH], pb[NCH];
+    fetch<A_KC>(pa, g.a, g.lda, m0, g.M, 0, g.K, g.vec_a, tid);
+    fetch<B_KC>(pb, g.b, g.ldb, n0, g.N, 0, g.K, g.vec_b, tid);
+    for (int k0 = 0; k0 < g.K; k0 += BK) {
+        __syncthreads();
+        put<A_KC>(As, pa, tid);
+        put<B_KC>(Bs, pb, tid);
+        __syncthreads();
+        if (k0 + BK < g.K) {
+            fetch<A_KC>(pa, g.a, g.lda, m0, g.M, k0 + BK, g.K, g.vec_a, tid);
+            fetch<B_KC>(pb, g.b, g.ldb, n0, g.N, k0 + BK, g.K, g.vec_b, tid);
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            f4 av[4], bv[4];
+            operand<A_KC>(av, As, wm, l16, grp, h);
+            operand<B_KC>(bv, Bs, wn, l16, grp, h);
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) acc[i][j] = mfma16(av[i][c], bv[j][c], acc[i][j]);
+        }
+    }
+
+    // acc[i][j][r] = C[m0 + wm + local_index<A_KC>(i, 4 grp + r)][n0 + wn + local_index<B_KC>(j, l16)]
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int m = m0 + wm + local_index<A_KC>(i, 4 * grp + r);
+            if (m >= g.M) continue;
+            float *crow = g.c + (size_t)m * g.ldc;
+            if constexpr (!B_KC) {  // the lane's four columns are consecutive
+                const int n = n0 + wn + 4 * l16;
+                f4 v = f4{acc[0][0][0], 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) v[j] = acc[i][j][r];
+                if (g.vec_c && n + 3 < g.N) {
+                    f4 *p = reinterpret_cast<f4 *>(crow + n);
+                    *p = g.accumulate ? *p + v : v;
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        if (n + j < g.N) crow[n + j] = g.accumulate ? crow[n + j] + v[j] : v[j];
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int n = n0 + wn + 16 * j + l16;
+                    if (n < g.N) crow[n] = g.accumulate ? crow[n] + acc[i][j][r] : acc[i][j][r];
+                }
+            }
+        }
+}
+
+}  // namespace
+
+extern "C" __global__ void __launch_bounds__(256) zt_gemm_nn(GemmArgs g) { gemm_body<true, false>(g); }
+extern "C" __global__ void __launch_bounds__(256) zt_gemm_tn(GemmArgs g) { gemm_body<false, false>(g); }
+extern "C" __global__ void __launch_bounds__(256) zt_gemm_nt(GemmArgs g) { gemm_body<true, true>(g); }

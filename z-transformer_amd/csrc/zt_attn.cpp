@@ -32,6 +32,7 @@ extern const unsigned char zt_co_bwd[], zt_co_bwd_end[];
 extern const unsigned char zt_co_dec[], zt_co_dec_end[];
 extern const unsigned char zt_co_misc[], zt_co_misc_end[];
 extern const unsigned char zt_co_cal[], zt_co_cal_end[];
+extern const unsigned char zt_co_gemm[], zt_co_gemm_end[];
 }
 
 namespace {
@@ -45,7 +46,7 @@ struct DeviceState {
     bool ok = false;
     size_t lds_limit = 0;
     int cus = 0;
-    hipModule_t mods[5] = {};
+    hipModule_t mods[6] = {};
     std::mutex mu;
     std::unordered_map<std::string, hipFunction_t> fns;
 };
@@ -55,8 +56,8 @@ void load_device(DeviceState &st, int dev) {
     int lds = 0;
     if (hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || lds <= 0)
         return;
-    const unsigned char *images[5] = {zt_co_fwd, zt_co_bwd, zt_co_dec, zt_co_misc, zt_co_cal};
-    for (int i = 0; i < 5; ++i) {
+    const unsigned char *images[6] = {zt_co_fwd, zt_co_bwd, zt_co_dec, zt_co_misc, zt_co_cal, zt_co_gemm};
+    for (int i = 0; i < 6; ++i) {
         if (hipModuleLoadData(&st.mods[i], images[i]) != hipSuccess) {
             fprintf(stderr, "zt_attn: the gfx950 code object %d would not load on device %d.\n", i, dev);
             return;
@@ -90,6 +91,7 @@ int module_of(const char *name) {
     if (strncmp(name, "zt_bwd", 6) == 0) return 1;
     if (strncmp(name, "zt_dec", 6) == 0) return 2;
     if (strncmp(name, "zt_cal", 6) == 0) return 4;
+    if (strncmp(name, "zt_gem", 6) == 0) return 5;
     return 3;
 }
 
@@ -896,6 +898,48 @@ int zt_calibrate(const float *src, size_t src_bytes, float *scratch, size_t scra
     *mfma_tflops = flop / (best_mfma * 1e-3) / 1e12;
     *read_gbs = (double)a.n4 * 16.0 / (best_read * 1e-3) / 1e9;
     return 0;
+}
+
+// C (+)= op(A) op(B) with the kernel variant `name` (see gemm.hip).
+static int gemm_impl(const char *name, const char *what, const float *a, int lda, const float *b, int ldb, float *c,
+                     int ldc, int M, int N, int K, int accumulate, hipStream_t stream) {
+    if (M < 0 || N < 0 || K < 0) {
+        fprintf(stderr, "%s: a %d x %d x %d product is not launchable.\n", what, M, N, K);
+        return 1;
+    }
+    if (M == 0 || N == 0) return 0;  // nothing to write (src/tensor_test.zig:172-183)
+    if (!c || (K > 0 && (!a || !b))) {
+        fprintf(stderr, "%s: a null tensor pointer is not launchable.\n", what);
+        return 1;
+    }
+    DeviceState *st = device_state();
+    if (!st) {
+        fprintf(stderr, "%s: no usable gfx950 device or code object.\n", what);
+        return 1;
+    }
+    const unsigned long long blocks = (unsigned long long)((M + 127) / 128) * (unsigned long long)((N + 127) / 128);
+    if (!grid_ok(blocks)) return 1;
+    GemmArgs g{};
+    g.a = a; g.b = b; g.c = c;
+    g.M = M; g.N = N; g.K = K;
+    g.lda = lda; g.ldb = ldb; g.ldc = ldc;
+    g.accumulate = accumulate;
+    g.vec_a = lda % 4 == 0 && (uintptr_t)a % 16 == 0;
+    g.vec_b = ldb % 4 == 0 && (uintptr_t)b % 16 == 0;
+    g.vec_c = ldc % 4 == 0 && (uintptr_t)c % 16 == 0;
+    return launch(st, name, (unsigned)blocks, g, stream);
+}
+
+int zt_matmul(const float *a, const float *b, float *out, int M, int K, int N, hipStream_t stream) {
+    return gemm_impl("zt_gemm_nn", "zt_matmul", a, K, b, N, out, N, M, N, K, 0, stream);
+}
+
+int zt_weight_grad(float *w, const float *input, const float *dout, int T, int I, int J, hipStream_t stream) {
+    return gemm_impl("zt_gemm_tn", "zt_weight_grad", input, I, dout, J, w, J, I, J, T, 1, stream);
+}
+
+int zt_input_grad(float *din, const float *dout, const float *w, int T, int J, int I, hipStream_t stream) {
+    return gemm_impl("zt_gemm_nt", "zt_input_grad", dout, J, w, J, din, I, T, I, J, 1, stream);
 }
 
 const char *zt_attn_version(void) { return "zt_attn gfx950 0.1"; }

@@ -24,6 +24,7 @@ ABI_SYMBOLS = [
     "zt_rope_qk_backward", "zt_fill_normal", "zt_fill_uniform", "zt_attn_version",
     "zt_attn_lds_limit", "zt_attn_plan", "zt_attn_forward_train", "zt_attn_backward_train",
     "zt_attn_bwd_dq_train", "zt_attn_bwd_dkdv_train", "zt_attn_plan_train", "zt_calibrate",
+    "zt_matmul", "zt_weight_grad", "zt_input_grad",
 ]
 HOLDER_SYMBOLS = [
     "zt_bytes_for", "zt_to_cint", "zt_forward_bounds", "zt_holder_init", "zt_holder_deinit",
@@ -72,6 +73,9 @@ def lib():
             "zt_attn_bwd_dq_train": (I, [P] * 8 + [I] * 5 + [P]),
             "zt_attn_bwd_dkdv_train": (I, [P] * 9 + [I] * 5 + [P]),
             "zt_attn_plan_train": (I, [I] * 5 + [P, P, P, Z]),
+            "zt_matmul": (I, [P, P, P, I, I, I, P]),
+            "zt_weight_grad": (I, [P, P, P, I, I, I, P]),
+            "zt_input_grad": (I, [P, P, P, I, I, I, P]),
             "zt_calibrate": (I, [P, Z, P, Z, P, P, P]),
             "zt_rope_forward": (I, [P, P, I, I, I, D, I, P]),
             "zt_rope_backward": (I, [P, P, I, I, I, D, I, P]),
@@ -259,6 +263,30 @@ def rope_qk(q, k, q_out, k_out, B, T, n_heads, n_kv_heads, head_dim, pos=0, thet
     fn = lib().zt_rope_qk_backward if backward else lib().zt_rope_qk_forward
     _check(fn(_ptr(q), _ptr(k), _ptr(q_out), _ptr(k_out), B, T, n_heads, n_kv_heads, head_dim, pos, theta,
               _stream(stream)), "zt_rope_qk")
+
+
+class DimensionMismatch(ValueError):
+    """src/tensor.zig:79: a.cols != b.rows."""
+
+
+def matmul(a, b, out, M, K, N, stream=None):
+    """out[M,N] = a[M,K] b[K,N] (src/tensor.zig:78-106)."""
+    _f32_cuda(a, b, out)
+    if a.numel() != M * K or b.numel() != K * N or out.numel() != M * N:
+        raise DimensionMismatch(f"{M}x{K} @ {K}x{N} into {out.numel()} elements")
+    _check(lib().zt_matmul(_ptr(a), _ptr(b), _ptr(out), M, K, N, _stream(stream)), "zt_matmul")
+
+
+def weight_grad(w, inp, dout, T, I, J, stream=None):
+    """w[I,J] += inp[T,I]^T dout[T,J] (src/autograd.zig:958-972)."""
+    _f32_cuda(w, inp, dout)
+    _check(lib().zt_weight_grad(_ptr(w), _ptr(inp), _ptr(dout), T, I, J, _stream(stream)), "zt_weight_grad")
+
+
+def input_grad(din, dout, w, T, J, I, stream=None):
+    """din[T,I] += dout[T,J] w[I,J]^T (src/autograd.zig:999-1022)."""
+    _f32_cuda(din, dout, w)
+    _check(lib().zt_input_grad(_ptr(din), _ptr(dout), _ptr(w), T, J, I, _stream(stream)), "zt_input_grad")
 
 
 def calibrate(src, scratch, stream=None):
