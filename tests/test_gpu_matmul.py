@@ -108,3 +108,27 @@ def test_matmul_refusals(gpu, zt):
     with pytest.raises(zt.DimensionMismatch):
         zt.matmul(a, b, out, 2, 3, 3)
     assert zt.lib().zt_matmul(None, None, None, -1, 2, 2, None) == 1
+
+
+@pytest.mark.parametrize("tile", ["128", "64", "32"])
+@pytest.mark.parametrize("M,K,N", [(200, 70, 150), (33, 129, 65), (128, 64, 256)])
+def test_every_tile_size_passes_the_gate(gpu, zt, monkeypatch, tile, M, K, N):
+    """Each workgroup tile (forced through ZT_GEMM_TILE), for all three
+    products, on ragged shapes."""
+    monkeypatch.setenv("ZT_GEMM_TILE", tile)
+    rng = np.random.default_rng(M * K + N)
+    a = rng.uniform(-1, 1, (M, K)).astype(np.float32)
+    b = rng.uniform(-1, 1, (K, N)).astype(np.float32)
+    a64, b64 = a.astype(np.float64), b.astype(np.float64)
+    out = gpu.full((M * N,), float("nan"), device="cuda")
+    zt.matmul(_dev(gpu, a), _dev(gpu, b), out, M, K, N)
+    c0 = rng.uniform(-1, 1, (M, N)).astype(np.float32)
+    wg = _dev(gpu, c0)   # w[M,N] += (a^T as stored K x M)^T b: weightGrad with T = K, I = M, J = N
+    zt.weight_grad(wg, _dev(gpu, np.ascontiguousarray(a.T)), _dev(gpu, b), K, M, N)
+    ig = _dev(gpu, c0)   # din[M,N] += a (b^T as stored N x K)^T: inputGrad with T = M, J = K, I = N
+    zt.input_grad(ig, _dev(gpu, a), _dev(gpu, np.ascontiguousarray(b.T)), M, K, N)
+    gpu.cuda.synchronize()
+    exact, abs_sum = a64 @ b64, np.abs(a64) @ np.abs(b64)
+    assert _divergence(host(out).reshape(M, N), exact, abs_sum) < (K - 1) * EPS32
+    for g in (wg, ig):
+        assert _divergence(host(g).reshape(M, N), c0.astype(np.float64) + exact, abs_sum, c0) < K * EPS32

@@ -4,19 +4,20 @@
 //   zt_gemm_nt: C += A B^T    src/autograd.zig:999-1022 (inputGrad: d input += dout w^T)
 // All matrices row-major f32.  op(A) is M x K, op(B) is K x N, C is M x N.
 //
-// A workgroup of 4 waves computes a 128 x 128 tile of C, each wave a 64 x 64
-// quarter as 4 x 4 tiles of 16 x 16: 16 independent accumulation chains of
-// v_mfma_f32_16x16x4_f32.  Each 32-deep k slab of both operands is copied to
+// A workgroup of 4 waves computes a BT x BT tile of C (BT = 128, or 64 / 32
+// when the product is too small to fill the device with 128-tiles), each wave
+// a quarter as TW x TW tiles of 16 x 16 (TW = BT / 32): up to 16 independent
+// accumulation chains of v_mfma_f32_16x16x4_f32.  Each 32-deep k slab of both operands is copied to
 // LDS in the orientation it has in memory, with 16-byte loads and stores:
 //   * k-contiguous (A as stored, B^T as stored): LDS [index][k], stride 36.
 //     Lane group grp owns k in [8 grp, 8 grp + 8) of the slab (the contraction
 //     is order-free across k-steps), so one 128-bit read gives a lane's
 //     operand for four k-steps of one tile; tile t's local index l16 is
 //     16 t + l16 of the wave's 64.
-//   * index-contiguous (A^T or B as stored): LDS [k][index], stride 132.
-//     Here a lane's four tiles are the four consecutive indices 4 l16 + t, so
-//     one 128-bit read gives its operand for all four tiles at one k.
-// Either way a k-step group of 4 x 4 x 4 MFMAs needs four 128-bit reads per
+//   * index-contiguous (A^T or B as stored): LDS [k][index], stride BT + 4.
+//     Here a lane's TW tiles are the TW consecutive indices TW l16 + t, so
+//     one TW-float read gives its operand for all its tiles at one k.
+// Either way a k-step group of 4 x TW x TW MFMAs needs four LDS reads per
 // operand, and no scattered (transposing) LDS writes are needed.  The next slab
 // is prefetched into registers while the current one computes.  Accumulation
 // is f32 inside the MFMA; the result differs from the reference's sequential
@@ -26,10 +27,8 @@
 
 namespace {
 
-constexpr int BT = 128, BK = 32, NTHR = 256;
-constexpr int LKC = BK + 4;   // row stride of a k-contiguous slab
-constexpr int LIC = BT + 4;   // row stride of an index-contiguous slab
-constexpr int NCH = BT * BK / 4 / NTHR;  // 16-byte chunks per thread per operand (4)
+constexpr int BK = 32, NTHR = 256;
+constexpr int LKC = BK + 4;  // row stride of a k-contiguous slab
 
 // The 4 floats p[0..3] of a row with `avail` valid elements from p: one
 // 16-byte load when vec and all 4 are valid, else guarded scalar loads.
@@ -43,13 +42,24 @@ DEVI f4 load4(const float *p, int avail, bool vec) {
     return x;
 }
 
+// Workgroup tile BT x BT (128, 64 or 32); each of the 4 waves owns a quarter,
+// TW x TW MFMA tiles of 16 x 16.
+template <int BT>
+struct Tile {
+    static constexpr int TW = BT / 32;             // MFMA tiles per wave per dimension
+    static constexpr int WT = BT / 2;              // wave tile width
+    static constexpr int LIC = BT + 4;             // row stride of an index-contiguous slab
+    static constexpr int NCH = BT * BK / 4 / NTHR; // 16-byte chunks per thread per operand
+};
+
 // Slab fetch of one operand into registers.  KC: memory rows are the tile
-// index (r0..r0+127, < rmax), k contiguous (k0..k0+31, < kmax).  Otherwise
-// memory rows are k and the index is contiguous.
-template <bool KC>
-DEVI void fetch(f4 (&pf)[NCH], const float *base, int ld, int r0, int rmax, int k0, int kmax, bool vec, int tid) {
+// index (r0.., < rmax), k contiguous (k0.., < kmax).  Otherwise memory rows
+// are k and the index is contiguous.
+template <int BT, bool KC>
+DEVI void fetch(f4 (&pf)[Tile<BT>::NCH], const float *base, int ld, int r0, int rmax, int k0, int kmax, bool vec,
+                int tid) {
 #pragma unroll
-    for (int n = 0; n < NCH; ++n) {
+    for (int n = 0; n < Tile<BT>::NCH; ++n) {
         const int e = tid + n * NTHR;
         if constexpr (KC) {
             const int r = r0 + e / (BK / 4), k = k0 + 4 * (e % (BK / 4));
@@ -61,91 +71,106 @@ DEVI void fetch(f4 (&pf)[NCH], const float *base, int ld, int r0, int rmax, int 
     }
 }
 
-template <bool KC>
-DEVI void put(float *lds, const f4 (&pf)[NCH], int tid) {
+template <int BT, bool KC>
+DEVI void put(float *lds, const f4 (&pf)[Tile<BT>::NCH], int tid) {
 #pragma unroll
-    for (int n = 0; n < NCH; ++n) {
+    for (int n = 0; n < Tile<BT>::NCH; ++n) {
         const int e = tid + n * NTHR;
         if constexpr (KC)
             *reinterpret_cast<f4 *>(lds + (e / (BK / 4)) * LKC + 4 * (e % (BK / 4))) = pf[n];
         else
-            *reinterpret_cast<f4 *>(lds + (e / (BT / 4)) * LIC + 4 * (e % (BT / 4))) = pf[n];
+            *reinterpret_cast<f4 *>(lds + (e / (BT / 4)) * Tile<BT>::LIC + 4 * (e % (BT / 4))) = pf[n];
     }
 }
 
-// A lane's operand block x[t][c] for tiles t = 0..3 and k-steps c = 0..3 of
-// half h of the slab, w0 = the wave's first index (0 or 64).
-template <bool KC>
-DEVI void operand(f4 (&x)[4], const float *lds, int w0, int l16, int grp, int h) {
+// A lane's operand block x[t][c] for its tiles t < TW and k-steps c = 0..3 of
+// half h of the slab; w0 = the wave's first index.  KC: one 128-bit read per
+// tile.  Otherwise the lane's tiles are the TW consecutive indices TW l16 + t:
+// one TW-float read per k-step.
+template <int BT, bool KC>
+DEVI void operand(f4 (&x)[Tile<BT>::TW], const float *lds, int w0, int l16, int grp, int h) {
+    constexpr int TW = Tile<BT>::TW;
     if constexpr (KC) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t) x[t] = *reinterpret_cast<const f4 *>(lds + (w0 + 16 * t + l16) * LKC + 8 * grp + 4 * h);
+        for (int t = 0; t < TW; ++t)
+            x[t] = *reinterpret_cast<const f4 *>(lds + (w0 + 16 * t + l16) * LKC + 8 * grp + 4 * h);
     } else {
-        f4 y[4];  // y[c][t]
 #pragma unroll
-        for (int c = 0; c < 4; ++c) y[c] = *reinterpret_cast<const f4 *>(lds + (8 * grp + 4 * h + c) * LIC + w0 + 4 * l16);
+        for (int c = 0; c < 4; ++c) {
+            const float *p = lds + (8 * grp + 4 * h + c) * Tile<BT>::LIC + w0 + TW * l16;
+            if constexpr (TW == 4) {
+                const f4 y = *reinterpret_cast<const f4 *>(p);
 #pragma unroll
-        for (int t = 0; t < 4; ++t) x[t] = f4{y[0][t], y[1][t], y[2][t], y[3][t]};
+                for (int t = 0; t < 4; ++t) x[t][c] = y[t];
+            } else if constexpr (TW == 2) {
+                const f2 y = *reinterpret_cast<const f2 *>(p);
+                x[0][c] = y.x; x[1][c] = y.y;
+            } else {
+                x[0][c] = *p;
+            }
+        }
     }
 }
 
-// Index within the wave's 64 of tile t's local row/column j.
-template <bool KC>
-DEVI int local_index(int t, int j) { return KC ? 16 * t + j : 4 * j + t; }
+// Index within the wave's tile of MFMA tile t's local row/column j.
+template <int TW, bool KC>
+DEVI int local_index(int t, int j) { return KC ? 16 * t + j : TW * j + t; }
 
 // A_KC: A stored M x K (else K x M).  B_KC: B stored N x K (else K x N).
-template <bool A_KC, bool B_KC>
+template <int BT, bool A_KC, bool B_KC>
 DEVI void gemm_body(const GemmArgs &g) {
-    __shared__ __attribute__((aligned(16))) float As[A_KC ? BT * LKC : BK * LIC];
-    __shared__ __attribute__((aligned(16))) float Bs[B_KC ? BT * LKC : BK * LIC];
+    using TL = Tile<BT>;
+    constexpr int TW = TL::TW, NCH = TL::NCH;
+    __shared__ __attribute__((aligned(16))) float As[A_KC ? BT * LKC : BK * TL::LIC];
+    __shared__ __attribute__((aligned(16))) float Bs[B_KC ? BT * LKC : BK * TL::LIC];
     const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, grp = lane >> 4, w = tid >> 6;
-    const int wm = 64 * (w >> 1), wn = 64 * (w & 1);
+    const int wm = TL::WT * (w >> 1), wn = TL::WT * (w & 1);
     const int tiles_n = (g.N + BT - 1) / BT;
     const int m0 = (int)(blockIdx.x / tiles_n) * BT, n0 = (int)(blockIdx.x % tiles_n) * BT;
 
-    f4 acc[4][4];
+    f4 acc[TW][TW];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < TW; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = zero4();
+        for (int j = 0; j < TW; ++j) acc[i][j] = zero4();
 
     f4 pa[NCH], pb[NCH];
-    fetch<A_KC>(pa, g.a, g.lda, m0, g.M, 0, g.K, g.vec_a, tid);
-    fetch<B_KC>(pb, g.b, g.ldb, n0, g.N, 0, g.K, g.vec_b, tid);
+    fetch<BT, A_KC>(pa, g.a, g.lda, m0, g.M, 0, g.K, g.vec_a, tid);
+    fetch<BT, B_KC>(pb, g.b, g.ldb, n0, g.N, 0, g.K, g.vec_b, tid);
     for (int k0 = 0; k0 < g.K; k0 += BK) {
         __syncthreads();
-        put<A_KC>(As, pa, tid);
-        put<B_KC>(Bs, pb, tid);
+        put<BT, A_KC>(As, pa, tid);
+        put<BT, B_KC>(Bs, pb, tid);
         __syncthreads();
         if (k0 + BK < g.K) {
-            fetch<A_KC>(pa, g.a, g.lda, m0, g.M, k0 + BK, g.K, g.vec_a, tid);
-            fetch<B_KC>(pb, g.b, g.ldb, n0, g.N, k0 + BK, g.K, g.vec_b, tid);
+            fetch<BT, A_KC>(pa, g.a, g.lda, m0, g.M, k0 + BK, g.K, g.vec_a, tid);
+            fetch<BT, B_KC>(pb, g.b, g.ldb, n0, g.N, k0 + BK, g.K, g.vec_b, tid);
         }
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            f4 av[4], bv[4];
-            operand<A_KC>(av, As, wm, l16, grp, h);
-            operand<B_KC>(bv, Bs, wn, l16, grp, h);
+            f4 av[TW], bv[TW];
+            operand<BT, A_KC>(av, As, wm, l16, grp, h);
+            operand<BT, B_KC>(bv, Bs, wn, l16, grp, h);
 #pragma unroll
             for (int c = 0; c < 4; ++c)
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
+                for (int i = 0; i < TW; ++i)
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) acc[i][j] = mfma16(av[i][c], bv[j][c], acc[i][j]);
+                    for (int j = 0; j < TW; ++j) acc[i][j] = mfma16(av[i][c], bv[j][c], acc[i][j]);
         }
     }
 
-    // acc[i][j][r] = C[m0 + wm + local_index<A_KC>(i, 4 grp + r)][n0 + wn + local_index<B_KC>(j, l16)]
+    // acc[i][j][r] = C[m0 + wm + local_index(i, 4 grp + r)][n0 + wn + local_index(j, l16)]
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < TW; ++i)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int m = m0 + wm + local_index<A_KC>(i, 4 * grp + r);
+            const int m = m0 + wm + local_index<TW, A_KC>(i, 4 * grp + r);
             if (m >= g.M) continue;
             float *crow = g.c + (size_t)m * g.ldc;
-            if constexpr (!B_KC) {  // the lane's four columns are consecutive
+            if constexpr (!B_KC && TW == 4) {  // the lane's four columns are consecutive
                 const int n = n0 + wn + 4 * l16;
-                f4 v = f4{acc[0][0][0], 0.f, 0.f, 0.f};
+                f4 v;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) v[j] = acc[i][j][r];
                 if (g.vec_c && n + 3 < g.N) {
@@ -158,8 +183,8 @@ DEVI void gemm_body(const GemmArgs &g) {
                 }
             } else {
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int n = n0 + wn + 16 * j + l16;
+                for (int j = 0; j < TW; ++j) {
+                    const int n = n0 + wn + local_index<TW, B_KC>(j, l16);
                     if (n < g.N) crow[n] = g.accumulate ? crow[n] + acc[i][j][r] : acc[i][j][r];
                 }
             }
@@ -168,6 +193,12 @@ DEVI void gemm_body(const GemmArgs &g) {
 
 }  // namespace
 
-extern "C" __global__ void __launch_bounds__(256) zt_gemm_nn(GemmArgs g) { gemm_body<true, false>(g); }
-extern "C" __global__ void __launch_bounds__(256) zt_gemm_tn(GemmArgs g) { gemm_body<false, false>(g); }
-extern "C" __global__ void __launch_bounds__(256) zt_gemm_nt(GemmArgs g) { gemm_body<true, true>(g); }
+// Kernel names: zt_gemm_<op>_<tile>.
+#define ZT_GEMM(BT)                                                                                \
+    extern "C" __global__ void __launch_bounds__(256) zt_gemm_nn_##BT(GemmArgs g) { gemm_body<BT, true, false>(g); } \
+    extern "C" __global__ void __launch_bounds__(256) zt_gemm_tn_##BT(GemmArgs g) { gemm_body<BT, false, false>(g); } \
+    extern "C" __global__ void __launch_bounds__(256) zt_gemm_nt_##BT(GemmArgs g) { gemm_body<BT, true, true>(g); }
+
+ZT_GEMM(128)
+ZT_GEMM(64)
+ZT_GEMM(32)

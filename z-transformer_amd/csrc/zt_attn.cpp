@@ -917,7 +917,14 @@ static int gemm_impl(const char *name, const char *what, const float *a, int lda
         fprintf(stderr, "%s: no usable gfx950 device or code object.\n", what);
         return 1;
     }
-    const unsigned long long blocks = (unsigned long long)((M + 127) / 128) * (unsigned long long)((N + 127) / 128);
+    // The largest workgroup tile whose grid still gives every CU a workgroup
+    // (the model's own products, 256 x 128 x 512 and the like, would leave
+    // most of the device idle with 128-tiles).
+    auto tiles = [&](int bt) { return (unsigned long long)((M + bt - 1) / bt) * (unsigned long long)((N + bt - 1) / bt); };
+    int bt = 128;
+    if (tiles(128) < (unsigned long long)st->cus) bt = tiles(64) >= (unsigned long long)st->cus / 2 ? 64 : 32;
+    bt = env_choice("ZT_GEMM_TILE", bt, {32, 64, 128});
+    const unsigned long long blocks = tiles(bt);
     if (!grid_ok(blocks)) return 1;
     GemmArgs g{};
     g.a = a; g.b = b; g.c = c;
@@ -927,7 +934,9 @@ static int gemm_impl(const char *name, const char *what, const float *a, int lda
     g.vec_a = lda % 4 == 0 && (uintptr_t)a % 16 == 0;
     g.vec_b = ldb % 4 == 0 && (uintptr_t)b % 16 == 0;
     g.vec_c = ldc % 4 == 0 && (uintptr_t)c % 16 == 0;
-    return launch(st, name, (unsigned)blocks, g, stream);
+    char kname[32];
+    snprintf(kname, sizeof kname, "%s_%d", name, bt);
+    return launch(st, kname, (unsigned)blocks, g, stream);
 }
 
 int zt_matmul(const float *a, const float *b, float *out, int M, int K, int N, hipStream_t stream) {
