@@ -6,8 +6,8 @@
 // back-to-back MFMAs); launched with four waves per SIMD it measures the
 // sustained FP32 matrix rate.
 // zt_cal_read: a grid-stride streaming read of a large buffer in 16-byte
-// loads, the access pattern of the decode kernel, reduced to one value per
-// thread so the loads cannot be dropped.
+// nontemporal loads, the access pattern of the decode kernel, reduced to one
+// value per thread so the loads cannot be dropped.
 #include "common.h"
 #include "args.h"
 
@@ -26,6 +26,6 @@ extern "C" __global__ void __launch_bounds__(256) zt_cal_read(CalArgs a) {
     const f4 *x = reinterpret_cast<const f4 *>(a.src);
     f4 acc = zero4();
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < a.n4; i += (size_t)gridDim.x * blockDim.x)
-        acc += x[i];
+        acc += __builtin_nontemporal_load(x + i);
     a.out[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = acc.x + acc.y + acc.z + acc.w;
 }

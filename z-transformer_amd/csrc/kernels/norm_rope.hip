@@ -52,7 +52,9 @@ __device__ __forceinline__ void rms_vec(const NormArgs &a) {
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
         const int c = threadIdx.x + 256 * i;
-        xv[i] = c < n4 ? reinterpret_cast<const f4 *>(xr)[c] : zero4();
+        // x is read once and y written once: nontemporal, so neither displaces
+        // the gain row every workgroup rereads.
+        xv[i] = c < n4 ? __builtin_nontemporal_load(reinterpret_cast<const f4 *>(xr) + c) : zero4();
         ss += (double)xv[i].x * (double)xv[i].x;
         ss += (double)xv[i].y * (double)xv[i].y;
         ss += (double)xv[i].z * (double)xv[i].z;
@@ -70,7 +72,7 @@ __device__ __forceinline__ void rms_vec(const NormArgs &a) {
             yv.y = xv[i].y / rms * wv.y;
             yv.z = xv[i].z / rms * wv.z;
             yv.w = xv[i].w / rms * wv.w;
-            reinterpret_cast<f4 *>(yr)[c] = yv;
+            __builtin_nontemporal_store(yv, reinterpret_cast<f4 *>(yr) + c);
         }
     }
 }
