@@ -3,7 +3,8 @@
 
 A step is one attention forward plus backward of a training step
 (zt_attn_forward_train, which keeps each row's log-sum-exp, then
-zt_attn_backward_train) over BASELINE.json's C3 workload: B=1, T=4096, 32 query / 8 kv heads,
+zt_attn_backward_train_ws, whose dk/dv kernel also stores dS so that dq is
+one causal product) over BASELINE.json's C3 workload: B=1, T=4096, 32 query / 8 kv heads,
 head_dim 128, f32, RoPE (theta 500000) pre-applied to Q and K, all inputs
 seeded N(0,1) on the device and resident in HBM before timing.  The headline
 value is fwd+bwd TFLOP/s with the causal-pair FLOP count
@@ -113,6 +114,7 @@ def main():
     dk, dv = torch.empty_like(k), torch.empty_like(v)
     rm, rl, rd = (torch.empty(B * T * H, device=dev) for _ in range(3))
     lse, delta = (torch.empty(B * T * H, device=dev) for _ in range(2))
+    work = torch.empty(zt.backward_train_workspace_bytes(B, T, H, Hkv, D) // 4, device=dev)  # delta + dS tiles
     pairs = B * H * T * (T + 1) / 2          # causal (query, key) pairs over all heads
     unit = 2 * D * pairs                      # FLOPs of one T x T x d causal matmul
     fwd_flop, bwd_flop = 2 * unit, 5 * unit
@@ -124,10 +126,16 @@ def main():
     paths = {
         "train": dict(
             fwd=lambda: zt.forward_train(q, k, v, out, lse, T, H, Hkv, D),
+            dkdv=lambda: zt.backward_train_ws(q, k, v, out, do, lse, dq, dk, dv, work, T, H, Hkv, D, stage=1),
+            dq=lambda: zt.backward_train_ws(q, k, v, out, do, lse, dq, dk, dv, work, T, H, Hkv, D, stage=2),
+            bwd=lambda: zt.backward_train_ws(q, k, v, out, do, lse, dq, dk, dv, work, T, H, Hkv, D),
+            names=zt.plan_train(B, T, H, Hkv, D)),
+        "train_dq_kernel": dict(
+            fwd=lambda: zt.forward_train(q, k, v, out, lse, T, H, Hkv, D),
             dq=lambda: zt.bwd_dq_train(q, k, v, out, do, lse, dq, delta, T, H, Hkv, D),
             dkdv=lambda: zt.bwd_dkdv_train(q, k, v, out, do, lse, delta, dk, dv, T, H, Hkv, D),
             bwd=lambda: zt.backward_train(q, k, v, out, do, lse, dq, dk, dv, delta, T, H, Hkv, D),
-            names=zt.plan_train(B, T, H, Hkv, D)),
+            names=(zt.plan_train(B, T, H, Hkv, D)[0], "zt_bwd_dql_d%d_k32" % D, zt.plan_train(B, T, H, Hkv, D)[2])),
         "reference_abi": dict(
             fwd=lambda: zt.forward(q, k, v, out, T, H, Hkv, D),
             dq=lambda: zt.bwd_dq(q, k, v, do, dq, rm, rl, rd, T, H, Hkv, D),
@@ -159,9 +167,9 @@ def main():
 
         n_k = max(3, args.steps)
         t_fwd = event_time(torch, pth["fwd"], n_k)
-        pth["dq"]()
-        t_dq = event_time(torch, pth["dq"], n_k)
+        pth["dkdv"]()  # the dq stage reads what the dk/dv stage wrote (row statistics or dS)
         t_dkdv = event_time(torch, pth["dkdv"], n_k)
+        t_dq = event_time(torch, pth["dq"], n_k)
         # Algorithmic FLOPs per launch: the forward's two matmuls; of the
         # backward's five (S recompute, dP, dV, dK, dQ) the dk/dv kernel owns
         # four and the dq kernel one -- the dq kernel's own recomputes earn no credit.
@@ -192,7 +200,7 @@ def main():
             traffic = json.load(f).get(dom["kernel"])
     roofline = {"bound": "mfma", "achieved": round(dom["tflops"], 3), "peak": PEAK_MFMA_F32, "unit": "TFLOP/s",
                 "frac": round(dom["tflops"] / PEAK_MFMA_F32, 4), "traffic": traffic, "kernel": dom["kernel"]}
-    del out, dq, dk, dv, do, q, k, v, rm, rl, rd, lse, delta
+    del out, dq, dk, dv, do, q, k, v, rm, rl, rd, lse, delta, work
 
     # ---------------- C4: decode step ----------------
     Bd, n_ctx = 64, 8192
@@ -324,7 +332,11 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "fwd_tflops": round(fwd_tflops, 3), "bwd_tflops": round(bwd_tflops, 3),
-        "step_path": "zt_attn_forward_train + zt_attn_backward_train (saved log-sum-exp)",
+        "step_path": "zt_attn_forward_train + zt_attn_backward_train_ws (saved log-sum-exp; dq = dS k from the dS "
+                     "tiles the dk/dv kernel stores)",
+        "train_dq_kernel": {"step_path": "zt_attn_forward_train + zt_attn_backward_train",
+                            "ms_per_step": round(res["train_dq_kernel"]["ms_step"], 4),
+                            "TFLOP/s": round(res["train_dq_kernel"]["value"], 3)},
         "reference_abi": {"step_path": "zt_attn_forward + zt_attn_backward",
                           "ms_per_step": round(res["reference_abi"]["ms_step"], 4),
                           "TFLOP/s": round(res["reference_abi"]["value"], 3),

@@ -169,7 +169,20 @@ int zt_attn_bwd_dq_train(const float *q, const float *k, const float *v, const f
 int zt_attn_bwd_dkdv_train(const float *q, const float *k, const float *v, const float *out, const float *dout,
                            const float *lse, const float *delta, float *dk, float *dv, int B, int T, int n_heads,
                            int n_kv_heads, int dim, hipStream_t stream);
-/* Kernel names the training path launches for a shape (as zt_attn_plan). */
+/* The same backward with dq formed from a stored dS instead of a third
+ * kernel that rebuilds it: the dk/dv kernel writes dS[b, h, t, s] for every
+ * causal pair into the workspace, and dq = dS k / sqrt(d) is then one causal
+ * product per head.  Deterministic like the rest.  workspace: at least
+ * zt_attn_backward_train_workspace(...) bytes (delta, then B * H * ceil(T/16)^2
+ * 16 x 16 tiles of dS: 2 GiB at T = 4096 with 32 heads).  stage: 1 = delta + dk/dv
+ * (+ dS), 2 = dq from dS, 3 = both.  No reference counterpart. */
+size_t zt_attn_backward_train_workspace(int B, int T, int n_heads, int n_kv_heads, int dim);
+int zt_attn_backward_train_ws(const float *q, const float *k, const float *v, const float *out, const float *dout,
+                              const float *lse, float *dq, float *dk, float *dv, void *workspace,
+                              size_t workspace_bytes, int B, int T, int n_heads, int n_kv_heads, int dim, int stage,
+                              hipStream_t stream);
+/* Kernel names the training path (zt_attn_forward_train +
+ * zt_attn_backward_train_ws) launches for a shape, as zt_attn_plan. */
 int zt_attn_plan_train(int B, int T, int n_heads, int n_kv_heads, int dim, char *fwd, char *dq, char *dkdv,
                        size_t len);
 

@@ -28,13 +28,18 @@ def _inputs(torch, zt, B, T, H, Hkv, D, sigma=1.0, rope=False):
     return q, k, v, do
 
 
-def _train(torch, zt, q, k, v, do, B, T, H, Hkv, D, lse_shift=0.0):
+def _train(torch, zt, q, k, v, do, B, T, H, Hkv, D, lse_shift=0.0, ws=False):
     out, lse = _nan(torch, q.numel()), _nan(torch, B * T * H)
     zt.forward_train(q, k, v, out, lse, T, H, Hkv, D, B=B)
     if lse_shift:
         lse += lse_shift
     dq, dk, dv, delta = _nan(torch, q.numel()), _nan(torch, k.numel()), _nan(torch, k.numel()), _nan(torch, B * T * H)
-    zt.backward_train(q, k, v, out, do, lse, dq, dk, dv, delta, T, H, Hkv, D, B=B)
+    if ws:  # dq from the dS the dk/dv kernel stores; the workspace starts as NaN so an unwritten dS shows
+        work = _nan(torch, zt.backward_train_workspace_bytes(B, T, H, Hkv, D) // 4)
+        zt.backward_train_ws(q, k, v, out, do, lse, dq, dk, dv, work, T, H, Hkv, D, B=B)
+        delta = work[:B * T * H]
+    else:
+        zt.backward_train(q, k, v, out, do, lse, dq, dk, dv, delta, T, H, Hkv, D, B=B)
     torch.cuda.synchronize()
     return [host(x) for x in (out, lse, dq, dk, dv, delta)]
 
@@ -45,10 +50,11 @@ CASES = [
 ]
 
 
+@pytest.mark.parametrize("ws", [False, True], ids=["dq-kernel", "dq-from-ds"])
 @pytest.mark.parametrize("B,T,H,Hkv,D", CASES)
-def test_train_path_matches_twin(gpu, zt, oracle, threads, B, T, H, Hkv, D):
+def test_train_path_matches_twin(gpu, zt, oracle, threads, B, T, H, Hkv, D, ws):
     q, k, v, do = _inputs(gpu, zt, B, T, H, Hkv, D)
-    out, lse, dq, dk, dv, delta = _train(gpu, zt, q, k, v, do, B, T, H, Hkv, D)
+    out, lse, dq, dk, dv, delta = _train(gpu, zt, q, k, v, do, B, T, H, Hkv, D, ws=ws)
     qh, kh, vh, dh = (host(x) for x in (q, k, v, do))
     assert max_abs(out, oracle.attention_forward(qh, kh, vh, B, T, H, Hkv, D, threads=threads)) <= FWD_TOL
     m, l, d = oracle.attention_row_stats(qh, kh, vh, dh, B, T, H, Hkv, D)
@@ -61,14 +67,15 @@ def test_train_path_matches_twin(gpu, zt, oracle, threads, B, T, H, Hkv, D):
     assert rel_err(dv, rv) <= BWD_REL
 
 
+@pytest.mark.parametrize("ws", [False, True], ids=["dq-kernel", "dq-from-ds"])
 @pytest.mark.parametrize("cfg", ["c3", "c5"])
-def test_train_path_full_size(gpu, zt, oracle, threads, cfg):
+def test_train_path_full_size(gpu, zt, oracle, threads, cfg, ws):
     if cfg == "c3":
         B, T, H, Hkv, D, sigma, rope, W = 1, 4096, 32, 8, 128, 1.0, True, 64
     else:
         B, T, H, Hkv, D, sigma, rope, W = 2, 2048, 16, 4, 256, np.sqrt(2.0), False, 32
     q, k, v, do = _inputs(gpu, zt, B, T, H, Hkv, D, sigma, rope)
-    out, lse, dq, dk, dv, delta = _train(gpu, zt, q, k, v, do, B, T, H, Hkv, D)
+    out, lse, dq, dk, dv, delta = _train(gpu, zt, q, k, v, do, B, T, H, Hkv, D, ws=ws)
     for g in (out, lse, dq, dk, dv, delta):
         assert np.all(np.isfinite(g))
     qh, kh, vh, dh = (host(x) for x in (q, k, v, do))
@@ -111,3 +118,26 @@ def test_train_gate_sees_the_saved_statistics(gpu, zt, oracle):
     _, _, dq, dk, dv, _ = _train(gpu, zt, q, k, v, do, B, T, H, Hkv, D, lse_shift=0.01)
     rq, rk, rv = oracle.attention_backward(*(host(x) for x in (q, k, v, do)), B, T, H, Hkv, D)
     assert max(rel_err(dq, rq), rel_err(dk, rk), rel_err(dv, rv)) > BWD_REL
+
+
+def test_train_ws_stages_and_repeats(gpu, zt):
+    """The workspace path is bit-reproducible, its two stages equal the whole,
+    and it agrees with the dq-kernel path (dk/dv identically; dq to rounding)."""
+    B, T, H, Hkv, D = 2, 130, 8, 2, 64
+    q, k, v, do = _inputs(gpu, zt, B, T, H, Hkv, D)
+    a = _train(gpu, zt, q, k, v, do, B, T, H, Hkv, D, ws=True)
+    b = _train(gpu, zt, q, k, v, do, B, T, H, Hkv, D, ws=True)
+    for x, y in zip(a, b):
+        assert np.array_equal(x.view(np.uint32), y.view(np.uint32))
+    c = _train(gpu, zt, q, k, v, do, B, T, H, Hkv, D, ws=False)
+    assert rel_err(a[2], c[2]) <= 1e-5 and rel_err(a[3], c[3]) <= 1e-5 and rel_err(a[4], c[4]) <= 1e-5
+    out, lse = gpu.from_numpy(a[0]).cuda(), gpu.from_numpy(a[1]).cuda()
+    work = _nan(gpu, zt.backward_train_workspace_bytes(B, T, H, Hkv, D) // 4)
+    dq, dk, dv = (_nan(gpu, n) for n in (q.numel(), k.numel(), k.numel()))
+    zt.backward_train_ws(q, k, v, out, do, lse, dq, dk, dv, work, T, H, Hkv, D, B=B, stage=1)
+    zt.backward_train_ws(q, k, v, out, do, lse, dq, dk, dv, work, T, H, Hkv, D, B=B, stage=2)
+    gpu.cuda.synchronize()
+    for x, y in zip((dq, dk, dv), a[2:5]):
+        assert np.array_equal(host(x).view(np.uint32), y.view(np.uint32))
+    with pytest.raises(zt.ZtRefused):
+        zt.backward_train_ws(q, k, v, out, do, lse, dq, dk, dv, work[:16], T, H, Hkv, D, B=B)

@@ -25,6 +25,12 @@ struct BwdArgs {
     // log-sum-exp lse replace row_max / row_den; the dq kernel writes
     // row_del = sum_d o * dO itself.
     const float *o, *lse;
+    // If non-null, the dk/dv kernel writes dS here in 16 x 16 tiles: tile
+    // (b, h, t / 16, s / 16) at ((b*H + h) * nt + t/16) * nt + s/16 (nt = ceil(T/16)),
+    // 256 floats in lane order (lane l, element r) = (t = 16 tb + 4 (l >> 4) + r,
+    // s = 16 sb + (l & 15)); masked pairs are 0.  Tiles above the diagonal are
+    // never written.
+    float *ds_out;
     int B, T, H, Hkv, dim;
     int HW, n_row_tiles, n_head_blocks;  // dq kernel decomposition (as the forward)
     int HS, n_key_tiles;                 // dk/dv kernel: head split, ceil(T / (16 * 4/HS))
@@ -102,5 +108,16 @@ struct GemmArgs {
     int accumulate;        // 0: C = product; 1: C += product
     bool vec_a, vec_b;     // 16-byte loads allowed along the contiguous dimension
     bool vec_c;            // 16-byte stores allowed along C's rows
+};
+
+// dq from a stored dS (gemm.hip): dq[b, t, h, :] = scale * sum_{s <= t} dS[b, h, t, s] k[b, s, h / group, :].
+struct DqDsArgs {
+    const float *ds;   // dS in the tiled layout of BwdArgs::ds_out
+    const float *k;    // [B, T, Hkv * dim]
+    float *dq;         // [B, T, H * dim]
+    int B, T, H, Hkv, dim;
+    int tiles_m, tiles_n;
+    float scale;
+    bool vec;          // 16-byte loads and stores along k and dq rows
 };
 

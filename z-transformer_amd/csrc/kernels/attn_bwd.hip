@@ -543,6 +543,18 @@ __device__ __forceinline__ void bwd_dkdv_body(const BwdArgs &a) {
                 p[u][r] = vis ? e : 0.f;
                 dsv[u][r] = p[u][r] * (dp[u][r] - stv[u][r].z);
             }
+        // dS for a dq product outside this kernel, one 16 x 16 tile per (u) in lane
+        // order; nontemporal, so the 1 GB stream does not evict the Q/dO rows
+        // the other workgroups are about to reread.
+        if (a.ds_out) {
+            const int hh = kvh * group + hs * hpp + hi;
+            const int nt = (a.T + 15) >> 4;
+#pragma unroll
+            for (int u = 0; u < NU; ++u) {
+                const size_t tile = (((size_t)b * a.H + hh) * nt + ((t0 >> 4) + u)) * nt + (s0 >> 4);
+                __builtin_nontemporal_store(dsv[u], reinterpret_cast<f4 *>(a.ds_out + tile * 256) + lane);
+            }
+        }
 #pragma unroll
         for (int u = 0; u < NU; ++u) {
             if (t0 + 16 * u + 15 < s0) continue;  // wave-uniform: this sub-tile is wholly masked
@@ -705,6 +717,12 @@ __device__ __forceinline__ void bwd_dkdv_dma_body(const BwdArgs &a) {
                 p[r] = vis ? e : 0.f;
                 dsv[r] = p[r] * (dp[r] - stv[r].z);
             }
+            if (a.ds_out) {  // dS for a dq product outside this kernel: the 16 x 16 tile in lane order
+                const int hh = kvh * group + hs * hpp + st / n_t;
+                const int nt = (a.T + 15) >> 4;
+                const size_t tile = (((size_t)b * a.H + hh) * nt + (t0 >> 4)) * nt + (s0 >> 4);
+                __builtin_nontemporal_store(dsv, reinterpret_cast<f4 *>(a.ds_out + tile * 256) + lane);
+            }
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk) {
                 const int tr = 4 * grp + kk;
@@ -815,3 +833,27 @@ ZT_BWD_ALL(160)
 ZT_BWD_ALL(192)
 ZT_BWD_ALL(224)
 ZT_BWD_ALL(256)
+
+// delta[row] = sum_d o[row, d] * dout[row, d] over the B*T*H rows of dim
+// floats (the row statistic the dk/dv kernel needs, autograd.zig:774-797 as
+// dO . O).  16 lanes per row, 4 rows per wave, 16 rows per workgroup.
+extern "C" __global__ void __launch_bounds__(256) zt_bwd_delta(BwdArgs a) {
+    const int lane = threadIdx.x & 63, l16 = lane & 15;
+    const long long rows = (long long)a.B * a.T * a.H;
+    const long long row = (long long)blockIdx.x * 16 + (threadIdx.x >> 4);
+    const bool vec4 = (a.dim & 3) == 0;
+    float part = 0.f;
+    if (row < rows) {
+        const float *o = a.o + (size_t)row * a.dim, *d = a.dout + (size_t)row * a.dim;
+        for (int c = 4 * l16; c < a.dim; c += 64) {
+            float x[4], y[4];
+            load_row_seg<4>(x, o, c, a.dim, vec4, true, 1.f);
+            load_row_seg<4>(y, d, c, a.dim, vec4, true, 1.f);
+            part += (x[0] * y[0] + x[1] * y[1]) + (x[2] * y[2] + x[3] * y[3]);
+        }
+    }
+#pragma unroll
+    for (int m = 8; m >= 1; m >>= 1) part += wave_xor(part, m);
+    if (row < rows && l16 == 0) a.row_del[row] = part;
+}
+

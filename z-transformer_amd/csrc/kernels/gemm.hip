@@ -191,6 +191,107 @@ DEVI void gemm_body(const GemmArgs &g) {
         }
 }
 
+// dq from a stored dS (the training backward's workspace path):
+//   dq[b, t, h, :] = scale * sum_{s <= t} dS[b, h, t, s] k[b, s, h / group, :]
+// A GEMM per (sequence, head): A = dS, B = k rows (index-contiguous: the head
+// dimension), C = dq rows; the reduction stops at the row tile's last query.
+// dS arrives in 16 x 16 tiles in lane order (the dk/dv kernel's store): a
+// 16-byte chunk of a tile is 4 consecutive queries at one key, which is the
+// index-contiguous orientation of A, so slabs are staged with 16-byte loads and
+// stores; tiles above the diagonal (never written) and rows past T read as 0.
+// Grid: row tiles latest (heaviest) first, then (sequence, head), then column tiles.
+template <int BT>
+DEVI void dq_ds_body(const DqDsArgs &g) {
+    using TL = Tile<BT>;
+    constexpr int TW = TL::TW, NCH = TL::NCH;
+    __shared__ __attribute__((aligned(16))) float As[BK * TL::LIC];
+    __shared__ __attribute__((aligned(16))) float Bs[BK * TL::LIC];
+    const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, grp = lane >> 4, w = tid >> 6;
+    const int wm = TL::WT * (w >> 1), wn = TL::WT * (w & 1);
+    int rem = (int)blockIdx.x;
+    const int tn = rem % g.tiles_n;
+    rem /= g.tiles_n;
+    const int bh = rem % (g.B * g.H);
+    const int tm = g.tiles_m - 1 - rem / (g.B * g.H);
+    const int b = bh / g.H, h = bh % g.H, kvh = h / (g.H / g.Hkv);
+    const int m0 = tm * BT, n0 = tn * BT;
+    const size_t qld = (size_t)g.H * g.dim, kld = (size_t)g.Hkv * g.dim;
+    const int nt = (g.T + 15) >> 4;
+    const float *A = g.ds + (size_t)bh * nt * nt * 256;
+    const float *Bm = g.k + (size_t)b * g.T * kld + (size_t)kvh * g.dim;
+    float *C = g.dq + (size_t)b * g.T * qld + (size_t)h * g.dim;
+    const int kend = min(g.T, m0 + BT);
+
+    f4 acc[TW][TW];
+#pragma unroll
+    for (int i = 0; i < TW; ++i)
+#pragma unroll
+        for (int j = 0; j < TW; ++j) acc[i][j] = zero4();
+
+    // A slab: keys k0..k0+31 x queries m0..m0+BT-1 = (BT/16) x 2 tiles; chunk e
+    // is (tile, lane-chunk); put() stores it at [key][query .. query+3].
+    f4 pa[NCH], pb[NCH];
+    auto fetch_a = [&](int k0) {
+#pragma unroll
+        for (int n = 0; n < NCH; ++n) {
+            const int e = tid + n * NTHR;
+            const int tile = e >> 6, c = e & 63;         // 64 chunks per tile
+            const int tb = (m0 >> 4) + tile % (BT / 16), sb = (k0 >> 4) + tile / (BT / 16);
+            f4 x = zero4();
+            if (sb <= tb && tb < nt)  // read once: nontemporal
+                x = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(A + ((size_t)tb * nt + sb) * 256) + c);
+            pa[n] = x;
+        }
+    };
+    auto put_a = [&]() {
+#pragma unroll
+        for (int n = 0; n < NCH; ++n) {
+            const int e = tid + n * NTHR;
+            const int tile = e >> 6, c = e & 63;
+            const int tl = 16 * (tile % (BT / 16)) + 4 * (c >> 4), sl = 16 * (tile / (BT / 16)) + (c & 15);
+            *reinterpret_cast<f4 *>(As + sl * TL::LIC + tl) = pa[n];
+        }
+    };
+    fetch_a(0);
+    fetch<BT, false>(pb, Bm, (int)kld, n0, g.dim, 0, kend, g.vec, tid);
+    for (int k0 = 0; k0 < kend; k0 += BK) {
+        __syncthreads();
+        put_a();
+        put<BT, false>(Bs, pb, tid);
+        __syncthreads();
+        if (k0 + BK < kend) {
+            fetch_a(k0 + BK);
+            fetch<BT, false>(pb, Bm, (int)kld, n0, g.dim, k0 + BK, kend, g.vec, tid);
+        }
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            f4 av[TW], bv[TW];
+            operand<BT, false>(av, As, wm, l16, grp, hh);
+            operand<BT, false>(bv, Bs, wn, l16, grp, hh);
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+#pragma unroll
+                for (int i = 0; i < TW; ++i)
+#pragma unroll
+                    for (int j = 0; j < TW; ++j) acc[i][j] = mfma16(av[i][c], bv[j][c], acc[i][j]);
+        }
+    }
+
+#pragma unroll
+    for (int i = 0; i < TW; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int t = m0 + wm + local_index<TW, false>(i, 4 * grp + r);
+            if (t >= g.T) continue;
+            float *crow = C + (size_t)t * qld;
+#pragma unroll
+            for (int j = 0; j < TW; ++j) {
+                const int n = n0 + wn + local_index<TW, false>(j, l16);
+                if (n < g.dim) crow[n] = acc[i][j][r] * g.scale;
+            }
+        }
+}
+
 }  // namespace
 
 // Kernel names: zt_gemm_<op>_<tile>.
@@ -202,3 +303,6 @@ DEVI void gemm_body(const GemmArgs &g) {
 ZT_GEMM(128)
 ZT_GEMM(64)
 ZT_GEMM(32)
+
+extern "C" __global__ void __launch_bounds__(256) zt_gemm_dqds_128(DqDsArgs g) { dq_ds_body<128>(g); }
+extern "C" __global__ void __launch_bounds__(256) zt_gemm_dqds_64(DqDsArgs g) { dq_ds_body<64>(g); }

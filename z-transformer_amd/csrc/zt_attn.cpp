@@ -236,6 +236,8 @@ bool grid_ok(unsigned long long blocks) {
     return true;
 }
 
+static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
 // Rows are read with 16-byte vector loads when dim % 4 == 0 and with 8-byte
 // loads otherwise, so every tensor base (null ones aside) must be aligned to that.
 static bool rows_aligned(int dim, std::initializer_list<const void *> ptrs) {
@@ -550,6 +552,78 @@ int zt_attn_bwd_dkdv_train(const float *q, const float *k, const float *v, const
                          dim, 64, 2, stream, out, lse);
 }
 
+// Tile of the dq-from-dS product: 128 x 128 unless the head is 64 wide or less
+// or 128-tiles would leave CUs idle.
+static int dqds_tile(int B, int T, int n_heads, int dim, int cus) {
+    const unsigned long long tiles128 = (unsigned long long)((T + 127) / 128) * ((dim + 127) / 128) * B * n_heads;
+    return (dim > 64 && tiles128 >= (unsigned long long)cus) ? 128 : 64;
+}
+
+size_t zt_attn_backward_train_workspace(int B, int T, int n_heads, int n_kv_heads, int dim) {
+    if (B < 1 || T < 1 || !zt_attn_dim_ok(dim) || n_heads <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads != 0)
+        return 0;
+    const size_t nt = (size_t)(T + 15) / 16;  // dS in 16 x 16 tiles
+    return align256((size_t)B * T * n_heads * sizeof(float)) + (size_t)B * n_heads * nt * nt * 256 * sizeof(float);
+}
+
+int zt_attn_backward_train_ws(const float *q, const float *k, const float *v, const float *out, const float *dout,
+                              const float *lse, float *dq, float *dk, float *dv, void *workspace,
+                              size_t workspace_bytes, int B, int T, int n_heads, int n_kv_heads, int dim, int stage,
+                              hipStream_t stream) {
+    if (stage < 1 || stage > 3) {
+        fprintf(stderr, "zt_attn: backward_train_ws stage %d is not 1, 2 or 3.\n", stage);
+        return 1;
+    }
+    if (!lse || !out) {
+        fprintf(stderr, "zt_attn: the saved-statistics backward needs lse and the forward output.\n");
+        return 1;
+    }
+    const size_t need = zt_attn_backward_train_workspace(B, T, n_heads, n_kv_heads, dim);
+    if (need != 0 && (!workspace || workspace_bytes < need)) {
+        fprintf(stderr, "zt_attn: backward_train_ws workspace of %zu bytes is short of the %zu needed.\n",
+                workspace_bytes, need);
+        return 1;
+    }
+    float *delta = static_cast<float *>(workspace);
+    float *ds = need ? reinterpret_cast<float *>(static_cast<char *>(workspace) +
+                                                 align256((size_t)B * T * n_heads * sizeof(float)))
+                     : nullptr;
+    BwdArgs a;
+    DeviceState *st = nullptr;
+    char name_a[64], name_b[64];
+    unsigned blocks_a = 0, blocks_b = 0, threads_a = kThreads, threads_b = kThreads;
+    float *l = const_cast<float *>(lse);
+    if (backward_prepare(q, k, v, dout, dq, dk, dv, l, l, delta, B, T, n_heads, n_kv_heads, dim, 64, &a, &st, name_a,
+                         name_b, &blocks_a, &blocks_b, &threads_a, &threads_b, out, lse))
+        return 1;
+    if (((stage & 1) && (!dk || !dv)) || ((stage & 2) && !dq)) {
+        fprintf(stderr, "zt_attn: a null gradient pointer is not launchable.\n");
+        return 1;
+    }
+    a.ds_out = ds;
+    if (stage & 1) {
+        const unsigned long long rows = (unsigned long long)B * T * n_heads;
+        if (!grid_ok((rows + 15) / 16)) return 1;
+        if (launch(st, "zt_bwd_delta", (unsigned)((rows + 15) / 16), a, stream)) return 1;
+        // Same stream: dk/dv reads delta, then writes dS for the product below.
+        if (launch(st, name_b, blocks_b, a, stream, threads_b)) return 1;
+    }
+    if (stage & 2) {
+        DqDsArgs g{};
+        g.ds = ds; g.k = k; g.dq = dq;
+        g.B = B; g.T = T; g.H = n_heads; g.Hkv = n_kv_heads; g.dim = dim;
+        g.scale = a.scale;
+        g.vec = dim % 4 == 0 && (uintptr_t)k % 16 == 0;
+        const int bt = dqds_tile(B, T, n_heads, dim, st->cus);
+        g.tiles_m = (T + bt - 1) / bt;
+        g.tiles_n = (dim + bt - 1) / bt;
+        const unsigned long long blocks = (unsigned long long)g.tiles_m * g.tiles_n * B * n_heads;
+        if (!grid_ok(blocks)) return 1;
+        if (launch(st, bt == 128 ? "zt_gemm_dqds_128" : "zt_gemm_dqds_64", (unsigned)blocks, g, stream)) return 1;
+    }
+    return 0;
+}
+
 int zt_attn_bwd_dq(const float *q, const float *k, const float *v, const float *dout, float *dq, float *row_max,
                    float *row_den, float *row_del, int B, int T, int n_heads, int n_kv_heads, int dim, int max_tile,
                    hipStream_t stream) {
@@ -564,7 +638,6 @@ int zt_attn_bwd_dkdv(const float *q, const float *k, const float *v, const float
                          const_cast<float *>(row_del), B, T, n_heads, n_kv_heads, dim, 64, 2, stream);
 }
 
-static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
 size_t zt_attn_decode_workspace(int B, int n_ctx, int n_heads, int n_kv_heads, int dim) {
     if (B < 1 || n_ctx < 1 || !zt_attn_dim_ok(dim) || n_heads <= 0 || n_kv_heads <= 0 ||
@@ -849,7 +922,9 @@ int zt_attn_plan(int B, int T, int n_heads, int n_kv_heads, int dim, int max_til
 int zt_attn_plan_train(int B, int T, int n_heads, int n_kv_heads, int dim, char *fwd, char *dq, char *dkdv,
                        size_t len) {
     if (zt_attn_plan(B, T, n_heads, n_kv_heads, dim, 64, fwd, dq, dkdv, len)) return 1;
-    snprintf(dq, len, "zt_bwd_dql_d%d_k32", pad32(dim));
+    DeviceState *st = device_state();
+    if (!st) return 1;
+    snprintf(dq, len, "zt_gemm_dqds_%d", dqds_tile(B, T, n_heads, dim, st->cus));
     return 0;
 }
 

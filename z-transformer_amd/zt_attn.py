@@ -24,7 +24,8 @@ ABI_SYMBOLS = [
     "zt_rope_qk_backward", "zt_fill_normal", "zt_fill_uniform", "zt_attn_version",
     "zt_attn_lds_limit", "zt_attn_plan", "zt_attn_forward_train", "zt_attn_backward_train",
     "zt_attn_bwd_dq_train", "zt_attn_bwd_dkdv_train", "zt_attn_plan_train", "zt_calibrate",
-    "zt_matmul", "zt_weight_grad", "zt_input_grad",
+    "zt_matmul", "zt_weight_grad", "zt_input_grad", "zt_attn_backward_train_workspace",
+    "zt_attn_backward_train_ws",
 ]
 HOLDER_SYMBOLS = [
     "zt_bytes_for", "zt_to_cint", "zt_forward_bounds", "zt_holder_init", "zt_holder_deinit",
@@ -73,6 +74,8 @@ def lib():
             "zt_attn_bwd_dq_train": (I, [P] * 8 + [I] * 5 + [P]),
             "zt_attn_bwd_dkdv_train": (I, [P] * 9 + [I] * 5 + [P]),
             "zt_attn_plan_train": (I, [I] * 5 + [P, P, P, Z]),
+            "zt_attn_backward_train_workspace": (Z, [I] * 5),
+            "zt_attn_backward_train_ws": (I, [P] * 10 + [Z] + [I] * 6 + [P]),
             "zt_matmul": (I, [P, P, P, I, I, I, P]),
             "zt_weight_grad": (I, [P, P, P, I, I, I, P]),
             "zt_input_grad": (I, [P, P, P, I, I, I, P]),
@@ -195,6 +198,19 @@ def bwd_dkdv_train(q, k, v, out, dout, lse, delta, dk, dv, T, n_heads, n_kv_head
     _check(lib().zt_attn_bwd_dkdv_train(_ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(dout), _ptr(lse), _ptr(delta),
                                         _ptr(dk), _ptr(dv), B, T, n_heads, n_kv_heads, dim, _stream(stream)),
            "zt_attn_bwd_dkdv_train")
+
+
+def backward_train_workspace_bytes(B, T, n_heads, n_kv_heads, dim):
+    return lib().zt_attn_backward_train_workspace(B, T, n_heads, n_kv_heads, dim)
+
+
+def backward_train_ws(q, k, v, out, dout, lse, dq, dk, dv, workspace, T, n_heads, n_kv_heads, dim, B=1, stage=3,
+                      stream=None):
+    _f32_cuda(q, k, v, out, dout, lse, dq, dk, dv, workspace)
+    nbytes = workspace.numel() * workspace.element_size()
+    _check(lib().zt_attn_backward_train_ws(_ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(dout), _ptr(lse), _ptr(dq),
+                                           _ptr(dk), _ptr(dv), _ptr(workspace), nbytes, B, T, n_heads, n_kv_heads,
+                                           dim, stage, _stream(stream)), "zt_attn_backward_train_ws")
 
 
 def plan_train(B, T, n_heads, n_kv_heads, dim):
