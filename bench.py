@@ -2,9 +2,10 @@
 """Benchmark of the fused causal GQA attention path on one MI355X.
 
 A step is one attention forward plus backward of a training step
-(zt_attn_forward_train, which keeps each row's log-sum-exp, then
-zt_attn_backward_train_ws, whose dk/dv kernel also stores dS so that dq is
-one causal product) over BASELINE.json's C3 workload: B=1, T=4096, 32 query / 8 kv heads,
+(zt_attn_forward_train_ws, which keeps each row's log-sum-exp and its scaled
+scores, then zt_attn_backward_train_ws, whose dk/dv kernel reads those scores
+instead of forming Q K^T again and overwrites them with dS, so that dq is one
+causal product) over BASELINE.json's C3 workload: B=1, T=4096, 32 query / 8 kv heads,
 head_dim 128, f32, RoPE (theta 500000) pre-applied to Q and K, all inputs
 seeded N(0,1) on the device and resident in HBM before timing.  The headline
 value is fwd+bwd TFLOP/s with the causal-pair FLOP count
@@ -120,28 +121,43 @@ def main():
     fwd_flop, bwd_flop = 2 * unit, 5 * unit
 
     # The timed step is a training step's attention: the forward keeps each
-    # row's log-sum-exp and the backward uses it (zt_attn_forward_train /
-    # zt_attn_backward_train).  The reference's own entry points, whose
-    # backward rebuilds the statistics, are timed beside it.
+    # row's log-sum-exp and its scores, and the backward uses them
+    # (zt_attn_forward_train_ws / zt_attn_backward_train_ws).  The same pair
+    # without the scores, the pair without a workspace, and the reference's
+    # own entry points, whose backward rebuilds the statistics, are timed
+    # beside it.  dkdv_units: the matmuls the dk/dv kernel executes (the
+    # score-reading kernel: dP, dV, dK; the others also S = Q K^T).
+    scores = 3 | zt.ZT_WS_SCORES
     paths = {
         "train": dict(
+            fwd=lambda: zt.forward_train_ws(q, k, v, out, lse, work, T, H, Hkv, D),
+            # Repeated on its own, the dk/dv stage reads the dS its previous
+            # launch left in place of the scores; its work does not depend on the values.
+            dkdv=lambda: zt.backward_train_ws(q, k, v, out, do, lse, dq, dk, dv, work, T, H, Hkv, D,
+                                              stage=1 | zt.ZT_WS_SCORES),
+            dq=lambda: zt.backward_train_ws(q, k, v, out, do, lse, dq, dk, dv, work, T, H, Hkv, D, stage=2),
+            bwd=lambda: zt.backward_train_ws(q, k, v, out, do, lse, dq, dk, dv, work, T, H, Hkv, D, stage=scores),
+            names=zt.plan_train(B, T, H, Hkv, D), dkdv_units=3),
+        "train_recompute_scores": dict(
             fwd=lambda: zt.forward_train(q, k, v, out, lse, T, H, Hkv, D),
             dkdv=lambda: zt.backward_train_ws(q, k, v, out, do, lse, dq, dk, dv, work, T, H, Hkv, D, stage=1),
             dq=lambda: zt.backward_train_ws(q, k, v, out, do, lse, dq, dk, dv, work, T, H, Hkv, D, stage=2),
             bwd=lambda: zt.backward_train_ws(q, k, v, out, do, lse, dq, dk, dv, work, T, H, Hkv, D),
-            names=zt.plan_train(B, T, H, Hkv, D)),
+            names=(zt.plan(B, T, H, Hkv, D)[0], zt.plan_train(B, T, H, Hkv, D)[1], zt.plan(B, T, H, Hkv, D)[2]),
+            dkdv_units=4),
         "train_dq_kernel": dict(
             fwd=lambda: zt.forward_train(q, k, v, out, lse, T, H, Hkv, D),
             dq=lambda: zt.bwd_dq_train(q, k, v, out, do, lse, dq, delta, T, H, Hkv, D),
             dkdv=lambda: zt.bwd_dkdv_train(q, k, v, out, do, lse, delta, dk, dv, T, H, Hkv, D),
             bwd=lambda: zt.backward_train(q, k, v, out, do, lse, dq, dk, dv, delta, T, H, Hkv, D),
-            names=(zt.plan_train(B, T, H, Hkv, D)[0], "zt_bwd_dql_d%d_k32" % D, zt.plan_train(B, T, H, Hkv, D)[2])),
+            names=(zt.plan(B, T, H, Hkv, D)[0], "zt_bwd_dql_d%d_k32" % D, zt.plan(B, T, H, Hkv, D)[2]),
+            dkdv_units=4),
         "reference_abi": dict(
             fwd=lambda: zt.forward(q, k, v, out, T, H, Hkv, D),
             dq=lambda: zt.bwd_dq(q, k, v, do, dq, rm, rl, rd, T, H, Hkv, D),
             dkdv=lambda: zt.bwd_dkdv(q, k, v, do, dk, dv, rm, rl, rd, T, H, Hkv, D),
             bwd=lambda: zt.backward(q, k, v, do, dq, dk, dv, rm, rl, rd, T, H, Hkv, D),
-            names=zt.plan(B, T, H, Hkv, D)),
+            names=zt.plan(B, T, H, Hkv, D), dkdv_units=4),
     }
     res = {}
     for pname, pth in paths.items():
@@ -172,12 +188,13 @@ def main():
         t_dq = event_time(torch, pth["dq"], n_k)
         # Algorithmic FLOPs per launch: the forward's two matmuls; of the
         # backward's five (S recompute, dP, dV, dK, dQ) the dk/dv kernel owns
-        # four and the dq kernel one -- the dq kernel's own recomputes earn no credit.
+        # the ones it executes (three when it reads the forward's scores, else
+        # four) and the dq kernel one -- the dq kernel's own recomputes earn no credit.
         n_fwd, n_dq, n_dkdv = pth["names"]
         kernels = [
             {"kernel": n_fwd, "ms": t_fwd, "flop": fwd_flop},
             {"kernel": n_dq, "ms": t_dq, "flop": unit},
-            {"kernel": n_dkdv, "ms": t_dkdv, "flop": 4 * unit},
+            {"kernel": n_dkdv, "ms": t_dkdv, "flop": pth["dkdv_units"] * unit},
         ]
         for kk in kernels:
             kk["tflops"] = kk["flop"] / (kk["ms"] * 1e-3) / 1e12
@@ -192,6 +209,7 @@ def main():
                           bwd_tflops=bwd_tflops)
     ms_step, value = res["train"]["ms_step"], res["train"]["value"]
     kernels, fwd_tflops, bwd_tflops = res["train"]["kernels"], res["train"]["fwd_tflops"], res["train"]["bwd_tflops"]
+    exec_flop = sum(kk["flop"] for kk in kernels)   # the matmuls the step's kernels execute
     dom = max(kernels, key=lambda x: x["ms"])
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic.json")
@@ -332,8 +350,13 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "fwd_tflops": round(fwd_tflops, 3), "bwd_tflops": round(bwd_tflops, 3),
-        "step_path": "zt_attn_forward_train + zt_attn_backward_train_ws (saved log-sum-exp; dq = dS k from the dS "
-                     "tiles the dk/dv kernel stores)",
+        "step_path": "zt_attn_forward_train_ws + zt_attn_backward_train_ws with ZT_WS_SCORES (saved log-sum-exp "
+                     "and scores; the dk/dv kernel reads the scores and stores dS in their place; dq = dS k)",
+        "executed_tflops": round(exec_flop / (ms_step * 1e-3) / 1e12, 3),
+        "train_recompute_scores": {"step_path": "zt_attn_forward_train + zt_attn_backward_train_ws (the dk/dv "
+                                                "kernel forms Q K^T again)",
+                                   "ms_per_step": round(res["train_recompute_scores"]["ms_step"], 4),
+                                   "TFLOP/s": round(res["train_recompute_scores"]["value"], 3)},
         "train_dq_kernel": {"step_path": "zt_attn_forward_train + zt_attn_backward_train",
                             "ms_per_step": round(res["train_dq_kernel"]["ms_step"], 4),
                             "TFLOP/s": round(res["train_dq_kernel"]["value"], 3)},

@@ -175,14 +175,30 @@ int zt_attn_bwd_dkdv_train(const float *q, const float *k, const float *v, const
  * product per head.  Deterministic like the rest.  workspace: at least
  * zt_attn_backward_train_workspace(...) bytes (delta, then B * H * ceil(T/16)^2
  * 16 x 16 tiles of dS: 2 GiB at T = 4096 with 32 heads).  stage: 1 = delta + dk/dv
- * (+ dS), 2 = dq from dS, 3 = both.  No reference counterpart. */
+ * (+ dS), 2 = dq from dS, 3 = both; | ZT_WS_SCORES when the workspace holds
+ * the scores zt_attn_forward_train_ws wrote for these q, k (the dk/dv kernel
+ * then reads each score tile and overwrites it with dS instead of forming
+ * Q K^T again).  No reference counterpart. */
+#define ZT_WS_SCORES 4
 size_t zt_attn_backward_train_workspace(int B, int T, int n_heads, int n_kv_heads, int dim);
 int zt_attn_backward_train_ws(const float *q, const float *k, const float *v, const float *out, const float *dout,
                               const float *lse, float *dq, float *dk, float *dv, void *workspace,
                               size_t workspace_bytes, int B, int T, int n_heads, int n_kv_heads, int dim, int stage,
                               hipStream_t stream);
-/* Kernel names the training path (zt_attn_forward_train +
- * zt_attn_backward_train_ws) launches for a shape, as zt_attn_plan. */
+/* zt_attn_forward_train that also leaves the scaled scores q k log2(e)/sqrt(d)
+ * of every causal 16 x 16 tile in the workspace's dS tiles, for
+ * zt_attn_backward_train_ws(..., stage | ZT_WS_SCORES, ...).  Scores are kept
+ * for the shapes whose dk/dv kernel reads them (head_dim <= 128, an even
+ * number of query heads per kv head); for the others this is
+ * zt_attn_forward_train and ZT_WS_SCORES is ignored.  The workspace is the
+ * backward's (zt_attn_backward_train_workspace bytes).  No reference
+ * counterpart. */
+int zt_attn_forward_train_ws(const float *q, const float *k, const float *v, float *out, float *lse, void *workspace,
+                             size_t workspace_bytes, int B, int T, int n_heads, int n_kv_heads, int dim,
+                             hipStream_t stream);
+/* Kernel names the training path (zt_attn_forward_train_ws +
+ * zt_attn_backward_train_ws with ZT_WS_SCORES) launches for a shape, as
+ * zt_attn_plan. */
 int zt_attn_plan_train(int B, int T, int n_heads, int n_kv_heads, int dim, char *fwd, char *dq, char *dkdv,
                        size_t len);
 

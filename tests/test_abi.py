@@ -149,6 +149,14 @@ def test_train_path_refusals(zt, capfd):
     assert L.zt_attn_bwd_dkdv_train(p, p, p, p, p, NULL, p, p, p, 1, 8, 4, 2, 32, NULL) == 1
     assert L.zt_attn_backward_train(p, p, p, p, p, p, p, p, p, p, 1, 8, 3, 2, 32, NULL) == 1
     assert "not a group" in capfd.readouterr().err
+    need = L.zt_attn_backward_train_workspace(1, 8, 4, 2, 32)
+    assert need > 0
+    assert L.zt_attn_forward_train_ws(p, p, p, p, p, p, need - 1, 1, 8, 4, 2, 32, NULL) == 1
+    assert "workspace" in capfd.readouterr().err
+    assert L.zt_attn_forward_train_ws(p, p, p, p, NULL, p, need, 1, 8, 4, 2, 32, NULL) == 1
+    assert "lse" in capfd.readouterr().err
+    assert L.zt_attn_backward_train_ws(p, p, p, p, p, p, p, p, p, p, need, 1, 8, 4, 2, 32, 4, NULL) == 1
+    assert "stage" in capfd.readouterr().err   # ZT_WS_SCORES alone names no stage
 
 
 def test_dense_product_refusals(zt, capfd):

@@ -29,14 +29,21 @@ def _inputs(torch, zt, B, T, H, Hkv, D, sigma=1.0, rope=False):
 
 
 def _train(torch, zt, q, k, v, do, B, T, H, Hkv, D, lse_shift=0.0, ws=False):
+    """ws: False = the dq kernel; "ds" (or True) = dq from the stored dS;
+    "scores" = that, with the forward's scores read back by the dk/dv kernel."""
     out, lse = _nan(torch, q.numel()), _nan(torch, B * T * H)
-    zt.forward_train(q, k, v, out, lse, T, H, Hkv, D, B=B)
+    # The workspace starts as NaN so that an unwritten score or dS tile shows.
+    work = _nan(torch, zt.backward_train_workspace_bytes(B, T, H, Hkv, D) // 4) if ws else None
+    if ws == "scores":
+        zt.forward_train_ws(q, k, v, out, lse, work, T, H, Hkv, D, B=B)
+    else:
+        zt.forward_train(q, k, v, out, lse, T, H, Hkv, D, B=B)
     if lse_shift:
         lse += lse_shift
     dq, dk, dv, delta = _nan(torch, q.numel()), _nan(torch, k.numel()), _nan(torch, k.numel()), _nan(torch, B * T * H)
-    if ws:  # dq from the dS the dk/dv kernel stores; the workspace starts as NaN so an unwritten dS shows
-        work = _nan(torch, zt.backward_train_workspace_bytes(B, T, H, Hkv, D) // 4)
-        zt.backward_train_ws(q, k, v, out, do, lse, dq, dk, dv, work, T, H, Hkv, D, B=B)
+    if ws:
+        stage = 3 | (zt.ZT_WS_SCORES if ws == "scores" else 0)
+        zt.backward_train_ws(q, k, v, out, do, lse, dq, dk, dv, work, T, H, Hkv, D, B=B, stage=stage)
         delta = work[:B * T * H]
     else:
         zt.backward_train(q, k, v, out, do, lse, dq, dk, dv, delta, T, H, Hkv, D, B=B)
@@ -50,7 +57,11 @@ CASES = [
 ]
 
 
-@pytest.mark.parametrize("ws", [False, True], ids=["dq-kernel", "dq-from-ds"])
+MODES = [False, "ds", "scores"]
+MODE_IDS = ["dq-kernel", "dq-from-ds", "scores"]
+
+
+@pytest.mark.parametrize("ws", MODES, ids=MODE_IDS)
 @pytest.mark.parametrize("B,T,H,Hkv,D", CASES)
 def test_train_path_matches_twin(gpu, zt, oracle, threads, B, T, H, Hkv, D, ws):
     q, k, v, do = _inputs(gpu, zt, B, T, H, Hkv, D)
@@ -67,7 +78,7 @@ def test_train_path_matches_twin(gpu, zt, oracle, threads, B, T, H, Hkv, D, ws):
     assert rel_err(dv, rv) <= BWD_REL
 
 
-@pytest.mark.parametrize("ws", [False, True], ids=["dq-kernel", "dq-from-ds"])
+@pytest.mark.parametrize("ws", MODES, ids=MODE_IDS)
 @pytest.mark.parametrize("cfg", ["c3", "c5"])
 def test_train_path_full_size(gpu, zt, oracle, threads, cfg, ws):
     if cfg == "c3":
@@ -125,8 +136,8 @@ def test_train_ws_stages_and_repeats(gpu, zt):
     and it agrees with the dq-kernel path (dk/dv identically; dq to rounding)."""
     B, T, H, Hkv, D = 2, 130, 8, 2, 64
     q, k, v, do = _inputs(gpu, zt, B, T, H, Hkv, D)
-    a = _train(gpu, zt, q, k, v, do, B, T, H, Hkv, D, ws=True)
-    b = _train(gpu, zt, q, k, v, do, B, T, H, Hkv, D, ws=True)
+    a = _train(gpu, zt, q, k, v, do, B, T, H, Hkv, D, ws="ds")
+    b = _train(gpu, zt, q, k, v, do, B, T, H, Hkv, D, ws="ds")
     for x, y in zip(a, b):
         assert np.array_equal(x.view(np.uint32), y.view(np.uint32))
     c = _train(gpu, zt, q, k, v, do, B, T, H, Hkv, D, ws=False)
@@ -141,3 +152,36 @@ def test_train_ws_stages_and_repeats(gpu, zt):
         assert np.array_equal(host(x).view(np.uint32), y.view(np.uint32))
     with pytest.raises(zt.ZtRefused):
         zt.backward_train_ws(q, k, v, out, do, lse, dq, dk, dv, work[:16], T, H, Hkv, D, B=B)
+
+
+@pytest.mark.parametrize("B,T,H,Hkv,D", [(2, 130, 8, 2, 64), (1, 333, 8, 2, 128), (1, 45, 4, 2, 66)])
+def test_train_scores_stages_and_repeats(gpu, zt, B, T, H, Hkv, D):
+    """The forward that keeps its scores gives the same out and lse bit for bit;
+    the backward that reads them back repeats bit for bit, its stages equal the
+    whole, and it agrees with the backward that recomputes Q K^T to rounding."""
+    q, k, v, do = _inputs(gpu, zt, B, T, H, Hkv, D)
+    a = _train(gpu, zt, q, k, v, do, B, T, H, Hkv, D, ws="scores")
+    b = _train(gpu, zt, q, k, v, do, B, T, H, Hkv, D, ws="scores")
+    for x, y in zip(a, b):
+        assert np.array_equal(x.view(np.uint32), y.view(np.uint32))
+    c = _train(gpu, zt, q, k, v, do, B, T, H, Hkv, D, ws="ds")
+    assert np.array_equal(a[0].view(np.uint32), c[0].view(np.uint32))
+    assert np.array_equal(a[1].view(np.uint32), c[1].view(np.uint32))
+    assert rel_err(a[2], c[2]) <= 1e-5 and rel_err(a[3], c[3]) <= 1e-5 and rel_err(a[4], c[4]) <= 1e-5
+    work = _nan(gpu, zt.backward_train_workspace_bytes(B, T, H, Hkv, D) // 4)
+    out, lse = _nan(gpu, q.numel()), _nan(gpu, B * T * H)
+    zt.forward_train_ws(q, k, v, out, lse, work, T, H, Hkv, D, B=B)
+    dq, dk, dv = (_nan(gpu, n) for n in (q.numel(), k.numel(), k.numel()))
+    zt.backward_train_ws(q, k, v, out, do, lse, dq, dk, dv, work, T, H, Hkv, D, B=B, stage=1 | zt.ZT_WS_SCORES)
+    zt.backward_train_ws(q, k, v, out, do, lse, dq, dk, dv, work, T, H, Hkv, D, B=B, stage=2)
+    gpu.cuda.synchronize()
+    for x, y in zip((dq, dk, dv), a[2:5]):
+        assert np.array_equal(host(x).view(np.uint32), y.view(np.uint32))
+    with pytest.raises(zt.ZtRefused):
+        zt.forward_train_ws(q, k, v, out, lse, work[:16], T, H, Hkv, D, B=B)
+
+
+def test_train_scores_plan_names_the_score_reading_kernel(gpu, zt):
+    assert zt.plan_train(1, 4096, 32, 8, 128) == ("zt_fwd8ps_d128_k32", "zt_gemm_dqds_128", "zt_bwd_dkdv8s_d128_hs2")
+    assert "dkdv8s" not in zt.plan_train(1, 256, 8, 8, 128)[2]   # MHA: no score-reading kernel
+    assert "dkdv8s" not in zt.plan_train(1, 256, 8, 2, 256)[2]   # d = 256: no score-reading kernel

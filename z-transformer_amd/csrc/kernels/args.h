@@ -9,6 +9,10 @@ struct FwdArgs {
     const float *v;    // [B, kv_rows, Hkv*dim]
     float *out;        // [B, T, H*dim]
     float *lse;        // [B, T, H] log-sum-exp of each row's scaled scores, or null
+    // If non-null (T = n_keys, q_offset 0), the scaled scores s = q k log2(e)/sqrt(dim)
+    // of every 16 x 16 tile on or below the diagonal, unmasked, in the dS tile
+    // order of BwdArgs::ds_out, for a dk/dv kernel that reads them back.
+    float *s_out;
     int B, T, H, Hkv, dim;
     int q_offset, n_keys, kv_rows;
     int HW;            // query heads per workgroup (1, 2 or 4; divides H/Hkv)
@@ -31,6 +35,10 @@ struct BwdArgs {
     // s = 16 sb + (l & 15)); masked pairs are 0.  Tiles above the diagonal are
     // never written.
     float *ds_out;
+    // Scores mode (dk/dv kernels built for it): ds_out holds the forward's
+    // scaled scores (FwdArgs::s_out) on entry; each tile is read before its
+    // dS replaces it.
+    int scores_in;
     int B, T, H, Hkv, dim;
     int HW, n_row_tiles, n_head_blocks;  // dq kernel decomposition (as the forward)
     int HS, n_key_tiles;                 // dk/dv kernel: head split, ceil(T / (16 * 4/HS))

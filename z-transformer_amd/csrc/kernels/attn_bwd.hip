@@ -363,8 +363,9 @@ __device__ __forceinline__ void bwd_dq_lse_body(const BwdArgs &a) {
     }
 }
 
-template <int DP, int HS, int KW, bool PF = false, int NU = 1>
+template <int DP, int HS, int KW, bool PF = false, int NU = 1, bool SIN = false>
 __device__ __forceinline__ void bwd_dkdv_body(const BwdArgs &a) {
+    static_assert(!SIN || PF, "the scores are prefetched with the stage's rows");
     constexpr int LW = DP + 4, DQ = DP / 4, NT = DP / 16, NTH = 64 * KW * HS;
     constexpr int BQ = 16 * NU;  // query rows per stage: NU sub-tiles of 16
     // Per head-split part: Q rows, dO rows, and (m2, 1/l, delta) per row.
@@ -391,17 +392,15 @@ __device__ __forceinline__ void bwd_dkdv_body(const BwdArgs &a) {
 
     const int my_key = s0 + l16;
     const bool key_ok = my_key < a.T;
-    float kr[DQ], vr[DQ];
-    load_row_seg<DQ>(kr, a.k + kvoff + (size_t)my_key * kld, grp * DQ, a.dim, vec4, key_ok, a.scale_log2e);
+    float kr[SIN ? 1 : DQ], vr[DQ];  // with the forward's scores K is not needed
+    if constexpr (!SIN)
+        load_row_seg<DQ>(kr, a.k + kvoff + (size_t)my_key * kld, grp * DQ, a.dim, vec4, key_ok, a.scale_log2e);
     load_row_seg<DQ>(vr, a.v + kvoff + (size_t)my_key * kld, grp * DQ, a.dim, vec4, key_ok, 1.f);
 
     f4 dka[NT], dva[NT];
 #pragma unroll
     for (int i = 0; i < NT; ++i) { dka[i] = zero4(); dva[i] = zero4(); }
 
-    float *qs = Qs + hs * BQ * LW;
-    float *ds = Ds + hs * BQ * LW;
-    float *st = St + hs * BQ * 4;
     // Stages: (head of each part hi, 16-row tile t0 of the suffix t >= wg_s0),
     // the tiles walked from the last row down so that the workgroups resident
     // at one time -- which all reach the end of the sequence -- read the same
@@ -419,6 +418,7 @@ __device__ __forceinline__ void bwd_dkdv_body(const BwdArgs &a) {
     static_assert(!PF || (HS * 2 * BQ * CPR) % NTH == 0, "prefetch split");
     f4 pf[NPF];
     float pm2 = 0.f, pil = 0.f, pde = 0.f;
+    f4 sn[SIN ? NU : 1], sc[SIN ? NU : 1];  // scores of the next / this stage (SIN)
     auto fetch = [&](int stg) {
         const int hi = stg / n_t, t0 = tile_row(stg);
 #pragma unroll
@@ -454,6 +454,20 @@ __device__ __forceinline__ void bwd_dkdv_body(const BwdArgs &a) {
                 pde = a.row_del[o];
             }
         }
+        if constexpr (SIN) {
+            // This wave's score tiles of the stage (lane order, as dS is stored).
+            const int hh = kvh * group + hs * hpp + hi;
+            const int nt = (a.T + 15) >> 4;
+#pragma unroll
+            for (int u = 0; u < NU; ++u) {
+                sn[u] = zero4();
+                const int tu = t0 + 16 * u;
+                if (tu < a.T && tu + 15 >= s0 && s0 < a.T) {
+                    const size_t tile = (((size_t)b * a.H + hh) * nt + (tu >> 4)) * nt + (s0 >> 4);
+                    sn[u] = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(a.ds_out + tile * 256) + lane);
+                }
+            }
+        }
     };
     auto put = [&]() {
 #pragma unroll
@@ -471,39 +485,11 @@ __device__ __forceinline__ void bwd_dkdv_body(const BwdArgs &a) {
     };
     if constexpr (PF) fetch(0);
 
-    for (int stg = 0; stg < n_stage; ++stg) {
+    // One stage's products for this wave, from the staged rows.
+    const float *qs = Qs + hs * BQ * LW, *ds = Ds + hs * BQ * LW, *st = St + hs * BQ * 4;
+    auto work = [&](int stg) {
         const int hi = stg / n_t, t0 = tile_row(stg);
-        __syncthreads();
-        if constexpr (PF) {
-            put();
-            __syncthreads();
-            if (stg + 1 < n_stage) fetch(stg + 1);
-        } else {
-            // Stage Q, dO rows [t0, t0+16) for every part's head.
-            const int nvalid = min(BQ, a.T - t0);
-            for (int part = 0; part < HS; ++part) {
-                const int hh = kvh * group + part * hpp + hi;
-                const size_t off = (size_t)b * a.T * qld + (size_t)t0 * qld + (size_t)hh * a.dim;
-                stage_rows<DP, LW, NTH>(Qs + part * BQ * LW, a.q + off, qld, BQ, nvalid, a.dim, vec4, tid);
-                stage_rows<DP, LW, NTH>(Ds + part * BQ * LW, a.dout + off, qld, BQ, nvalid, a.dim, vec4, tid);
-            }
-            if (tid < HS * BQ) {
-                const int part = tid / BQ, r = tid % BQ, t = t0 + r;
-                const int hh = kvh * group + part * hpp + hi;
-                float m2 = 0.f, il = 0.f, de = 0.f;
-                if (t < a.T) {
-                    const size_t o = ((size_t)b * a.T + t) * a.H + hh;
-                    m2 = (a.lse ? a.lse[o] : a.row_max[o]) * kLog2e;
-                    il = a.lse ? 1.f : 1.f / a.row_den[o];
-                    de = a.row_del[o];
-                }
-                St[(part * BQ + r) * 4 + 0] = m2;
-                St[(part * BQ + r) * 4 + 1] = il;
-                St[(part * BQ + r) * 4 + 2] = de;
-            }
-            __syncthreads();
-        }
-        if (t0 + BQ - 1 < s0 || s0 >= a.T) continue;  // wave-uniform: no visible pair
+        if (t0 + BQ - 1 < s0 || s0 >= a.T) return;  // wave-uniform: no visible pair
 
         // Sub-tile u holds query rows t0 + 16 u + [0, 16).  This lane's four
         // rows' statistics per sub-tile are read ahead of the MFMAs.
@@ -515,20 +501,40 @@ __device__ __forceinline__ void bwd_dkdv_body(const BwdArgs &a) {
         f4 s[NU], dp[NU];
 #pragma unroll
         for (int u = 0; u < NU; ++u) { s[u] = zero4(); dp[u] = zero4(); }
+        if constexpr (SIN) {
+            // Scores from the forward; dP alone as two interleaved chains.
+            f4 dp2[NU];
 #pragma unroll
-        for (int kk = 0; kk < DQ; kk += 4) {
+            for (int u = 0; u < NU; ++u) { s[u] = sc[u]; dp2[u] = zero4(); }
 #pragma unroll
-            for (int u = 0; u < NU; ++u) {
-                const f4 qx = *reinterpret_cast<const f4 *>(qs + (16 * u + l16) * LW + grp * DQ + kk);
-                const f4 dx = *reinterpret_cast<const f4 *>(ds + (16 * u + l16) * LW + grp * DQ + kk);
-                s[u] = mfma16(qx.x, kr[kk + 0], s[u]);
-                dp[u] = mfma16(dx.x, vr[kk + 0], dp[u]);
-                s[u] = mfma16(qx.y, kr[kk + 1], s[u]);
-                dp[u] = mfma16(dx.y, vr[kk + 1], dp[u]);
-                s[u] = mfma16(qx.z, kr[kk + 2], s[u]);
-                dp[u] = mfma16(dx.z, vr[kk + 2], dp[u]);
-                s[u] = mfma16(qx.w, kr[kk + 3], s[u]);
-                dp[u] = mfma16(dx.w, vr[kk + 3], dp[u]);
+            for (int kk = 0; kk < DQ; kk += 4) {
+#pragma unroll
+                for (int u = 0; u < NU; ++u) {
+                    const f4 dx = *reinterpret_cast<const f4 *>(ds + (16 * u + l16) * LW + grp * DQ + kk);
+                    dp[u] = mfma16(dx.x, vr[kk + 0], dp[u]);
+                    dp2[u] = mfma16(dx.y, vr[kk + 1], dp2[u]);
+                    dp[u] = mfma16(dx.z, vr[kk + 2], dp[u]);
+                    dp2[u] = mfma16(dx.w, vr[kk + 3], dp2[u]);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < NU; ++u) dp[u] += dp2[u];
+        } else {
+#pragma unroll
+            for (int kk = 0; kk < DQ; kk += 4) {
+#pragma unroll
+                for (int u = 0; u < NU; ++u) {
+                    const f4 qx = *reinterpret_cast<const f4 *>(qs + (16 * u + l16) * LW + grp * DQ + kk);
+                    const f4 dx = *reinterpret_cast<const f4 *>(ds + (16 * u + l16) * LW + grp * DQ + kk);
+                    s[u] = mfma16(qx.x, kr[kk + 0], s[u]);
+                    dp[u] = mfma16(dx.x, vr[kk + 0], dp[u]);
+                    s[u] = mfma16(qx.y, kr[kk + 1], s[u]);
+                    dp[u] = mfma16(dx.y, vr[kk + 1], dp[u]);
+                    s[u] = mfma16(qx.z, kr[kk + 2], s[u]);
+                    dp[u] = mfma16(dx.z, vr[kk + 2], dp[u]);
+                    s[u] = mfma16(qx.w, kr[kk + 3], s[u]);
+                    dp[u] = mfma16(dx.w, vr[kk + 3], dp[u]);
+                }
             }
         }
         // s[u][r] = S[t = t0 + 16 u + 4 grp + r][key = s0 + l16]
@@ -571,6 +577,45 @@ __device__ __forceinline__ void bwd_dkdv_body(const BwdArgs &a) {
                 }
             }
         }
+    };
+
+    for (int stg = 0; stg < n_stage; ++stg) {
+        __syncthreads();
+        if constexpr (PF) {
+            put();
+            __syncthreads();
+            if constexpr (SIN) {
+#pragma unroll
+                for (int u = 0; u < NU; ++u) sc[u] = sn[u];
+            }
+            if (stg + 1 < n_stage) fetch(stg + 1);
+        } else {
+            const int hi = stg / n_t, t0 = tile_row(stg);
+            // Stage Q, dO rows [t0, t0+16) for every part's head.
+            const int nvalid = min(BQ, a.T - t0);
+            for (int part = 0; part < HS; ++part) {
+                const int hh = kvh * group + part * hpp + hi;
+                const size_t off = (size_t)b * a.T * qld + (size_t)t0 * qld + (size_t)hh * a.dim;
+                stage_rows<DP, LW, NTH>(Qs + part * BQ * LW, a.q + off, qld, BQ, nvalid, a.dim, vec4, tid);
+                stage_rows<DP, LW, NTH>(Ds + part * BQ * LW, a.dout + off, qld, BQ, nvalid, a.dim, vec4, tid);
+            }
+            if (tid < HS * BQ) {
+                const int part = tid / BQ, r = tid % BQ, t = t0 + r;
+                const int hh = kvh * group + part * hpp + hi;
+                float m2 = 0.f, il = 0.f, de = 0.f;
+                if (t < a.T) {
+                    const size_t o = ((size_t)b * a.T + t) * a.H + hh;
+                    m2 = (a.lse ? a.lse[o] : a.row_max[o]) * kLog2e;
+                    il = a.lse ? 1.f : 1.f / a.row_den[o];
+                    de = a.row_del[o];
+                }
+                St[(part * BQ + r) * 4 + 0] = m2;
+                St[(part * BQ + r) * 4 + 1] = il;
+                St[(part * BQ + r) * 4 + 2] = de;
+            }
+            __syncthreads();
+        }
+        work(stg);
     }
 
     // Sum the head-split partials in a fixed order (part 0 + 1 + ...).
@@ -807,6 +852,11 @@ __device__ __forceinline__ void bwd_dkdv_dma_body(const BwdArgs &a) {
     extern "C" __global__ void __launch_bounds__(512) zt_bwd_dkdv8p_d##DP##_hs2(BwdArgs a) {    \
         bwd_dkdv_body<DP, 2, 4, true>(a);                                                          \
     }
+// Eight-wave dk/dv that reads the forward's scores instead of recomputing Q K^T.
+#define ZT_BWD_DKDV8S(DP)                                                                          \
+    extern "C" __global__ void __launch_bounds__(512) zt_bwd_dkdv8s_d##DP##_hs2(BwdArgs a) {    \
+        bwd_dkdv_body<DP, 2, 4, true, 1, true>(a);                                                 \
+    }
 #define ZT_BWD_DKDV_DMA(DP, HS)                                                                    \
     extern "C" __global__ void __launch_bounds__(256) zt_bwd_dkdv_dma_d##DP##_hs##HS(BwdArgs a) { \
         bwd_dkdv_dma_body<DP, HS>(a);                                                              \
@@ -819,6 +869,7 @@ ZT_BWD_ALL(32)
 ZT_BWD_ALL(64)
 ZT_BWD_ALL(96)
 ZT_BWD_ALL(128)
+ZT_BWD_DKDV8S(32) ZT_BWD_DKDV8S(64) ZT_BWD_DKDV8S(96) ZT_BWD_DKDV8S(128)
 // The 4-way splits: the 160 KB LDS holds 4 parts' tiles (double-buffered for
 // the asynchronous variant) up to d = 128.
 ZT_BWD_DKDV(32, 4)

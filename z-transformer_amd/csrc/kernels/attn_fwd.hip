@@ -130,6 +130,21 @@ __device__ __forceinline__ void attn_fwd_body(const FwdArgs &a) {
                 s[j] = mfma16(kx.w, qr[kk + 3], s[j]);
             }
         }
+        if (a.s_out) {
+            // Element (t = row0 + l16, s = k0 + 16 j + 4 grp + r) goes to lane
+            // (s & 15) + 16 ((t & 15) >> 2), element t & 3 of its tile: four
+            // lanes write each 16-byte run.  (A quad transpose to one 16-byte
+            // store per lane measured no faster.)
+            const int nt = (a.T + 15) >> 4;
+            float *srow = a.s_out + ((((size_t)b * a.H + h) * nt + (row0 >> 4)) * nt + (k0 >> 4)) * 256 +
+                          (16 * (l16 >> 2)) * 4 + (l16 & 3);
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+                if (k0 + 16 * j >= kend_w) continue;  // wave-uniform: above the diagonal
+#pragma unroll
+                for (int r = 0; r < 4; ++r) srow[j * 256 + (4 * grp + r) * 4] = s[j][r];
+            }
+        }
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
 #pragma unroll
@@ -209,3 +224,10 @@ ZT_FWD(224, 32) ZT_FWD(224, 64)
 ZT_FWD(256, 32) ZT_FWD(256, 64)
 ZT_FWD_PF(32) ZT_FWD_PF(64) ZT_FWD_PF(96) ZT_FWD_PF(128)
 ZT_FWD_PF(160) ZT_FWD_PF(192) ZT_FWD_PF(224) ZT_FWD_PF(256)
+// The same eight-wave kernel under its own name for launches that keep the
+// scores (s_out set), so that a profile tells the two roles apart.
+#define ZT_FWD_PFS(DP)                                                                             \
+    extern "C" __global__ void __launch_bounds__(512, 4) zt_fwd8ps_d##DP##_k32(FwdArgs a) {      \
+        attn_fwd_body<DP, 32, 8, true>(a);                                                         \
+    }
+ZT_FWD_PFS(32) ZT_FWD_PFS(64) ZT_FWD_PFS(96) ZT_FWD_PFS(128)

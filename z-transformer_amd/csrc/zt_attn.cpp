@@ -254,7 +254,7 @@ static bool rows_aligned(int dim, std::initializer_list<const void *> ptrs) {
 
 int forward_impl(const float *q, const float *k, const float *v, float *out, int B, int T, int n_heads,
                  int n_kv_heads, int dim, int group_q, int max_tile, int q_offset, int n_keys, int kv_rows,
-                 hipStream_t stream, float *lse = nullptr) {
+                 hipStream_t stream, float *lse = nullptr, float *s_out = nullptr) {
     if (T < 1) return refuse_T(T);
     if (!zt_attn_dim_ok(dim)) return refuse_dim(dim);
     if (check_group(n_heads, n_kv_heads)) return 1;
@@ -289,7 +289,7 @@ int forward_impl(const float *q, const float *k, const float *v, float *out, int
     }
     if (!rows_aligned(dim, {q, k, v, out})) return 1;
     FwdArgs a{};
-    a.q = q; a.k = k; a.v = v; a.out = out; a.lse = lse;
+    a.q = q; a.k = k; a.v = v; a.out = out; a.lse = lse; a.s_out = s_out;
     a.B = B; a.T = T; a.H = n_heads; a.Hkv = n_kv_heads; a.dim = dim;
     a.q_offset = q_offset; a.n_keys = n_keys; a.kv_rows = kv_rows;
     a.HW = heads_per_wg(n_heads / n_kv_heads);
@@ -302,6 +302,8 @@ int forward_impl(const float *q, const float *k, const float *v, float *out, int
     if (!grid_ok(blocks)) return 1;
     char name[64];
     fwd_kernel_name(name, sizeof name, dp, bk, nw);
+    if (s_out && dp <= 128 && strncmp(name, "zt_fwd8p_d", 10) == 0)
+        snprintf(name, sizeof name, "zt_fwd8ps_d%d_k32", dp);  // same kernel, named for its role
     return launch(st, name, (unsigned)blocks, a, stream, 64u * nw);
 }
 
@@ -566,12 +568,45 @@ size_t zt_attn_backward_train_workspace(int B, int T, int n_heads, int n_kv_head
     return align256((size_t)B * T * n_heads * sizeof(float)) + (size_t)B * n_heads * nt * nt * 256 * sizeof(float);
 }
 
+// Shapes whose dk/dv kernel can take the forward's scores instead of
+// rebuilding them: the eight-wave, two-way head split kernel (d <= 128, an
+// even head group).  The forward writes scores only for these.
+static bool scores_path(int dim, int n_heads, int n_kv_heads, size_t lds_limit) {
+    const int dp = pad32(dim);
+    return n_kv_heads > 0 && (n_heads / n_kv_heads) % 2 == 0 && dp <= 128 && dkdv_bytes(dp, 2, 4) <= lds_limit;
+}
+
+static float *ws_tiles(void *workspace, int B, int T, int n_heads) {
+    return reinterpret_cast<float *>(static_cast<char *>(workspace) + align256((size_t)B * T * n_heads * sizeof(float)));
+}
+
+int zt_attn_forward_train_ws(const float *q, const float *k, const float *v, float *out, float *lse, void *workspace,
+                             size_t workspace_bytes, int B, int T, int n_heads, int n_kv_heads, int dim,
+                             hipStream_t stream) {
+    if (!lse && T >= 1 && zt_attn_dim_ok(dim)) {
+        fprintf(stderr, "zt_attn: forward_train needs an lse buffer.\n");
+        return 1;
+    }
+    const size_t need = zt_attn_backward_train_workspace(B, T, n_heads, n_kv_heads, dim);
+    if (need != 0 && (!workspace || workspace_bytes < need)) {
+        fprintf(stderr, "zt_attn: forward_train_ws workspace of %zu bytes is short of the %zu needed.\n",
+                workspace_bytes, need);
+        return 1;
+    }
+    DeviceState *st = need ? device_state() : nullptr;
+    float *s_out = (st && scores_path(dim, n_heads, n_kv_heads, st->lds_limit)) ? ws_tiles(workspace, B, T, n_heads)
+                                                                                : nullptr;
+    return forward_impl(q, k, v, out, B, T, n_heads, n_kv_heads, dim, 1, 64, 0, T, T, stream, lse, s_out);
+}
+
 int zt_attn_backward_train_ws(const float *q, const float *k, const float *v, const float *out, const float *dout,
                               const float *lse, float *dq, float *dk, float *dv, void *workspace,
                               size_t workspace_bytes, int B, int T, int n_heads, int n_kv_heads, int dim, int stage,
                               hipStream_t stream) {
-    if (stage < 1 || stage > 3) {
-        fprintf(stderr, "zt_attn: backward_train_ws stage %d is not 1, 2 or 3.\n", stage);
+    const bool scores = (stage & 4) != 0;
+    stage &= 3;
+    if (stage < 1) {
+        fprintf(stderr, "zt_attn: backward_train_ws stage %d is not 1, 2 or 3 (optionally | 4).\n", stage);
         return 1;
     }
     if (!lse || !out) {
@@ -585,9 +620,7 @@ int zt_attn_backward_train_ws(const float *q, const float *k, const float *v, co
         return 1;
     }
     float *delta = static_cast<float *>(workspace);
-    float *ds = need ? reinterpret_cast<float *>(static_cast<char *>(workspace) +
-                                                 align256((size_t)B * T * n_heads * sizeof(float)))
-                     : nullptr;
+    float *ds = need ? ws_tiles(workspace, B, T, n_heads) : nullptr;
     BwdArgs a;
     DeviceState *st = nullptr;
     char name_a[64], name_b[64];
@@ -601,6 +634,18 @@ int zt_attn_backward_train_ws(const float *q, const float *k, const float *v, co
         return 1;
     }
     a.ds_out = ds;
+    if (scores && scores_path(dim, n_heads, n_kv_heads, st->lds_limit)) {
+        // The forward left the scores in the dS tiles: the eight-wave kernel
+        // that reads them (64 keys x 2 head halves per workgroup).
+        a.scores_in = 1;
+        a.HS = 2;
+        a.n_key_tiles = (T + 63) / 64;
+        const unsigned long long blocks = (unsigned long long)a.n_key_tiles * n_kv_heads * B;
+        if (!grid_ok(blocks)) return 1;
+        blocks_b = (unsigned)blocks;
+        threads_b = 512;
+        snprintf(name_b, sizeof name_b, "zt_bwd_dkdv8s_d%d_hs2", pad32(dim));
+    }
     if (stage & 1) {
         const unsigned long long rows = (unsigned long long)B * T * n_heads;
         if (!grid_ok((rows + 15) / 16)) return 1;
@@ -925,6 +970,10 @@ int zt_attn_plan_train(int B, int T, int n_heads, int n_kv_heads, int dim, char 
     DeviceState *st = device_state();
     if (!st) return 1;
     snprintf(dq, len, "zt_gemm_dqds_%d", dqds_tile(B, T, n_heads, dim, st->cus));
+    if (scores_path(dim, n_heads, n_kv_heads, st->lds_limit)) {
+        snprintf(dkdv, len, "zt_bwd_dkdv8s_d%d_hs2", pad32(dim));
+        if (strncmp(fwd, "zt_fwd8p_d", 10) == 0) snprintf(fwd, len, "zt_fwd8ps_d%d_k32", pad32(dim));
+    }
     return 0;
 }
 

@@ -25,7 +25,7 @@ ABI_SYMBOLS = [
     "zt_attn_lds_limit", "zt_attn_plan", "zt_attn_forward_train", "zt_attn_backward_train",
     "zt_attn_bwd_dq_train", "zt_attn_bwd_dkdv_train", "zt_attn_plan_train", "zt_calibrate",
     "zt_matmul", "zt_weight_grad", "zt_input_grad", "zt_attn_backward_train_workspace",
-    "zt_attn_backward_train_ws",
+    "zt_attn_backward_train_ws", "zt_attn_forward_train_ws",
 ]
 HOLDER_SYMBOLS = [
     "zt_bytes_for", "zt_to_cint", "zt_forward_bounds", "zt_holder_init", "zt_holder_deinit",
@@ -76,6 +76,7 @@ def lib():
             "zt_attn_plan_train": (I, [I] * 5 + [P, P, P, Z]),
             "zt_attn_backward_train_workspace": (Z, [I] * 5),
             "zt_attn_backward_train_ws": (I, [P] * 10 + [Z] + [I] * 6 + [P]),
+            "zt_attn_forward_train_ws": (I, [P] * 6 + [Z] + [I] * 5 + [P]),
             "zt_matmul": (I, [P, P, P, I, I, I, P]),
             "zt_weight_grad": (I, [P, P, P, I, I, I, P]),
             "zt_input_grad": (I, [P, P, P, I, I, I, P]),
@@ -177,6 +178,18 @@ def forward_train(q, k, v, out, lse, T, n_heads, n_kv_heads, dim, B=1, stream=No
     _f32_cuda(q, k, v, out, lse)
     _check(lib().zt_attn_forward_train(_ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(lse), B, T, n_heads, n_kv_heads,
                                        dim, _stream(stream)), "zt_attn_forward_train")
+
+
+# include/zt_attn.h: stage flag of zt_attn_backward_train_ws, the workspace holds the forward's scores
+ZT_WS_SCORES = 4
+
+
+def forward_train_ws(q, k, v, out, lse, workspace, T, n_heads, n_kv_heads, dim, B=1, stream=None):
+    _f32_cuda(q, k, v, out, lse, workspace)
+    nbytes = workspace.numel() * workspace.element_size()
+    _check(lib().zt_attn_forward_train_ws(_ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(lse), _ptr(workspace), nbytes,
+                                          B, T, n_heads, n_kv_heads, dim, _stream(stream)),
+           "zt_attn_forward_train_ws")
 
 
 def backward_train(q, k, v, out, dout, lse, dq, dk, dv, delta, T, n_heads, n_kv_heads, dim, B=1, stream=None):
