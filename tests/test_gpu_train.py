@@ -185,3 +185,23 @@ def test_train_scores_plan_names_the_score_reading_kernel(gpu, zt):
     assert zt.plan_train(1, 4096, 32, 8, 128) == ("zt_fwd8ps_d128_k32", "zt_gemm_dqds_128", "zt_bwd_dkdv8s_d128_hs2")
     assert "dkdv8s" not in zt.plan_train(1, 256, 8, 8, 128)[2]   # MHA: no score-reading kernel
     assert "dkdv8s" not in zt.plan_train(1, 256, 8, 2, 256)[2]   # d = 256: no score-reading kernel
+
+
+@pytest.mark.parametrize("B,T,H,Hkv,D", [(1, 100, 8, 2, 80), (2, 45, 4, 2, 32), (1, 333, 8, 2, 128)])
+def test_train_scores_write_nothing_past_the_workspace(gpu, zt, oracle, B, T, H, Hkv, D):
+    """Ragged T: the score-reading dk/dv kernel stages 32 rows, so a stage can
+    end past the last row; no score or dS tile may be written outside the
+    workspace (a guard band after it keeps its fill) and the gradients hold."""
+    q, k, v, do = _inputs(gpu, zt, B, T, H, Hkv, D)
+    need = zt.backward_train_workspace_bytes(B, T, H, Hkv, D) // 4
+    guard = 1 << 16
+    whole = gpu.full((need + guard,), 12345.0, device="cuda", dtype=gpu.float32)
+    work = whole[:need]
+    out, lse = _nan(gpu, q.numel()), _nan(gpu, B * T * H)
+    dq, dk, dv = (_nan(gpu, n) for n in (q.numel(), k.numel(), k.numel()))
+    zt.forward_train_ws(q, k, v, out, lse, work, T, H, Hkv, D, B=B)
+    zt.backward_train_ws(q, k, v, out, do, lse, dq, dk, dv, work, T, H, Hkv, D, B=B, stage=3 | zt.ZT_WS_SCORES)
+    gpu.cuda.synchronize()
+    assert np.all(host(whole[need:]) == 12345.0)
+    rq, rk, rv = oracle.attention_backward(*(host(x) for x in (q, k, v, do)), B, T, H, Hkv, D)
+    assert max(rel_err(host(dq), rq), rel_err(host(dk), rk), rel_err(host(dv), rv)) <= BWD_REL

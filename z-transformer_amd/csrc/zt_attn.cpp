@@ -179,9 +179,9 @@ int dq_waves(int dp) {
     const int w = env_choice("ZT_ATTN_DQ_W", 4, {4, 8});
     return dp > 192 ? 4 : w;  // eight-wave dq spills above d = 192
 }
-size_t dkdv_bytes(int dp, int hs, int kw = 0) {
+size_t dkdv_bytes(int dp, int hs, int kw = 0, int rows = 16) {
     if (kw == 0) kw = 4 / hs;
-    const size_t stage = (size_t)2 * hs * 16 * (dp + 4) + (size_t)hs * 16 * 4;
+    const size_t stage = (size_t)2 * hs * rows * (dp + 4) + (size_t)hs * rows * 4;
     const size_t red = (size_t)(hs - 1) * kw * 64 * 2 * (dp / 16) * 4;
     return (stage > red ? stage : red) * sizeof(float);
 }
@@ -569,11 +569,12 @@ size_t zt_attn_backward_train_workspace(int B, int T, int n_heads, int n_kv_head
 }
 
 // Shapes whose dk/dv kernel can take the forward's scores instead of
-// rebuilding them: the eight-wave, two-way head split kernel (d <= 128, an
-// even head group).  The forward writes scores only for these.
+// rebuilding them: the eight-wave, two-way head split kernel with 32 query
+// rows per stage (d <= 128, an even head group).  The forward writes scores
+// only for these.
 static bool scores_path(int dim, int n_heads, int n_kv_heads, size_t lds_limit) {
     const int dp = pad32(dim);
-    return n_kv_heads > 0 && (n_heads / n_kv_heads) % 2 == 0 && dp <= 128 && dkdv_bytes(dp, 2, 4) <= lds_limit;
+    return n_kv_heads > 0 && (n_heads / n_kv_heads) % 2 == 0 && dp <= 128 && dkdv_bytes(dp, 2, 4, 32) <= lds_limit;
 }
 
 static float *ws_tiles(void *workspace, int B, int T, int n_heads) {
