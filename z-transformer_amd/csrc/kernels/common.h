@@ -48,15 +48,36 @@ DEVI float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 DEVI float wave_xor(float v, int mask) { return __shfl_xor(v, mask, 64); }
 
-DEVI float max4grp(float v) {  // max over the four lane groups sharing l16
-    v = fmaxf(v, wave_xor(v, 16));
-    v = fmaxf(v, wave_xor(v, 32));
-    return v;
+// Lane l's value and lane l ^ 16's (l ^ 32's), in some order, from gfx950's
+// row-swap instructions: v_permlane16_swap with both operands v exchanges the
+// odd 16-lane rows of the first copy with the even rows of the second, so each
+// copy then holds, per lane, one of the pair {v[l], v[l ^ 16]} and the other
+// copy the other; v_permlane32_swap does the same for the two 32-lane halves.
+// VALU only: no LDS round trip as a cross-row shuffle takes.
+DEVI void pair16(float v, float &a, float &b) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    a = __uint_as_float(r[0]);
+    b = __uint_as_float(r[1]);
 }
+DEVI void pair32(float v, float &a, float &b) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    a = __uint_as_float(r[0]);
+    b = __uint_as_float(r[1]);
+}
+
+DEVI float max4grp(float v) {  // max over the four lane groups sharing l16
+    float a, b;
+    pair16(v, a, b);
+    pair32(fmaxf(a, b), a, b);
+    return fmaxf(a, b);
+}
+// Sum over the four lane groups sharing l16 (each step adds one pair, and a
+// two-operand f32 add does not depend on operand order, so all four agree).
 DEVI float sum4grp(float v) {
-    v += wave_xor(v, 16);
-    v += wave_xor(v, 32);
-    return v;
+    float a, b;
+    pair16(v, a, b);
+    pair32(a + b, a, b);
+    return a + b;
 }
 
 DEVI f4 zero4() { return f4{0.f, 0.f, 0.f, 0.f}; }
