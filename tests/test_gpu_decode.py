@@ -30,6 +30,19 @@ def test_decode_c4(gpu, zt, oracle, threads):
     assert max_abs(out, ref) <= FWD_TOL
 
 
+@pytest.mark.parametrize("wgs", ["256", "512", "2048", "32768"])
+def test_decode_any_split(gpu, zt, oracle, threads, monkeypatch, wgs):
+    """However the key axis is split (the workgroup target, a tuning
+    variable), the answer holds: 8 sequences x 8 kv heads of 2000 rows run in
+    4, 8 or 32 chunks per sequence (the C4 test runs one chunk per sequence)."""
+    monkeypatch.setenv("ZT_DEC_WGS", wgs)
+    B, n_ctx, H, Hkv, D = 8, 2000, 32, 8, 128
+    n_keys = [2000, 1999, 1500, 1024, 1023, 600, 65, 1]
+    q, kc, vc, out = _decode(gpu, zt, B, n_ctx, H, Hkv, D, n_keys)
+    ref = oracle.attn_step(host(q), host(kc), host(vc), n_keys, B, n_ctx, H, Hkv, D, threads=threads)
+    assert max_abs(out, ref) <= FWD_TOL
+
+
 @pytest.mark.parametrize("B,n_ctx,H,Hkv,D", [
     (5, 300, 32, 8, 128), (3, 1000, 8, 8, 64), (4, 257, 16, 2, 256), (2, 100, 6, 3, 32),
     (7, 50, 4, 4, 80), (1, 1, 4, 2, 32), (70, 40, 8, 2, 128), (2, 999, 16, 1, 96), (3, 64, 12, 4, 34),

@@ -18,7 +18,8 @@
 // fewer cross-lane moves than one tree per (key, head).  p is broadcast back
 // through a small wave-private LDS table; P.V accumulates in registers.
 // Per-chunk (max, denominator, accumulator) partials go to a caller-provided
-// workspace and zt_dec_combine merges them.
+// workspace and zt_dec_combine merges them; with one chunk per sequence the
+// workgroup writes the output itself and no combine runs.
 #include "common.h"
 #include "args.h"
 
@@ -227,6 +228,21 @@ __device__ __forceinline__ void decode_body(const DecArgs &a) {
             const float f = Wm[ww][gi] == -INFINITY ? 0.f : fast_exp2(Wm[ww][gi] - M);
             L += Wl[ww][gi] * f;
             A += Wacc[ww][gi][sb] * f;
+        }
+        if (a.n_chunks == 1) {
+            // The whole row in one workgroup: the output itself, as the
+            // combine would form it (o * (1 / L), the partial's weight being 1).
+            const f4 o = A * (1.f / L);
+            float *po = a.out + (size_t)b * a.H * a.dim + (size_t)(h0 + gi) * a.dim;
+            if (4 * sb < a.dim) {
+                if (vec4) {
+                    *reinterpret_cast<f4 *>(po + 4 * sb) = o;
+                } else {
+                    po[4 * sb] = o.x; po[4 * sb + 1] = o.y;
+                    if (4 * sb + 2 < a.dim) { po[4 * sb + 2] = o.z; po[4 * sb + 3] = o.w; }
+                }
+            }
+            continue;
         }
         const size_t slot = ((size_t)b * a.H + (h0 + gi)) * a.n_chunks + c;
         float *pa = a.part_acc + slot * a.dim;

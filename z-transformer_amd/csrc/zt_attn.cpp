@@ -442,7 +442,10 @@ DecGeom decode_geom(int B, int n_ctx, int n_heads, int n_kv_heads, int dim) {
     g.dp = dim <= 32 ? 32 : dim <= 64 ? 64 : dim <= 128 ? 128 : 256;
     g.ks = 8 * (64 / (g.dp / 4));
     const long long pairs = (long long)B * n_kv_heads * g.n_gsub;
-    const long long target = env_choice("ZT_DEC_WGS", 2048, {1024, 2048, 4096, 8192, 16384, 32768});
+    // Workgroups to aim for: 512, two per CU of MI355X's 256 (the workspace
+    // size must not depend on the device). Measured on MI355X against 1024 / 2048
+    // (C4 643 -> 624 us; B = 1, 8192 keys 66 -> 41 us; B = 16, 4096 keys 106 -> 93 us).
+    const long long target = env_choice("ZT_DEC_WGS", 512, {256, 512, 768, 1024, 1536, 2048, 4096, 8192, 16384, 32768});
     long long per_seq = (target + pairs - 1) / pairs;
     if (per_seq < 1) per_seq = 1;
     long long chunk = (n_ctx + per_seq - 1) / per_seq;
@@ -742,7 +745,8 @@ int zt_attn_decode(const float *q, const float *k_cache, const float *v_cache, f
         const unsigned long long blocks = (unsigned long long)a.nb * g.n_chunks * n_kv_heads * g.n_gsub;
         if (!grid_ok(blocks)) return 1;
         if (launch(st, name, (unsigned)blocks, a, stream)) return 1;
-        if (launch(st, "zt_dec_combine", (unsigned)(a.nb * n_heads), a, stream)) return 1;
+        // One chunk per sequence: the decode kernel wrote the output itself.
+        if (g.n_chunks > 1 && launch(st, "zt_dec_combine", (unsigned)(a.nb * n_heads), a, stream)) return 1;
     }
     return 0;
 }
