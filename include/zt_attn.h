@@ -108,7 +108,8 @@ int zt_attn_bwd_dkdv(const float *q, const float *k, const float *v, const float
  * layout per sequence); sequence b attends its first n_keys[b] cached rows,
  * its query sitting at position n_keys[b]-1 (src/decode.zig:326-392).
  * n_keys is a HOST array of B ints in [1, n_ctx].  `workspace` is device
- * memory of at least zt_attn_decode_workspace(...) bytes (chunk partials).
+ * memory of at least zt_attn_decode_workspace(...) bytes (chunk partials),
+ * 16-byte aligned (as every workspace here; hipMalloc's are).
  * Refuses B < 1, n_ctx < 1, a refused width or group, an n_keys outside
  * [1, n_ctx], a null pointer, or a short workspace. */
 size_t zt_attn_decode_workspace(int B, int n_ctx, int n_heads, int n_kv_heads, int dim);
@@ -125,7 +126,7 @@ int zt_attn_decode(const float *q, const float *k_cache, const float *v_cache, f
  * src/decode.zig:206-298 does per layer.  q/out [B, n_heads*dim], k_new/v_new
  * [B, n_kv_heads*dim], caches [B, n_ctx, n_kv_heads*dim]; pos is a HOST array
  * of B ints in [0, n_ctx) (a full cache is refused, kv_cache.zig:91).
- * `workspace` holds zt_attn_decode_step_workspace(...) bytes. */
+ * `workspace` holds zt_attn_decode_step_workspace(...) bytes, 16-byte aligned. */
 size_t zt_attn_decode_step_workspace(int B, int n_ctx, int n_heads, int n_kv_heads, int dim);
 int zt_attn_decode_step(const float *q, const float *k_new, const float *v_new, float *k_cache, float *v_cache,
                         float *out, const int *pos, int B, int n_ctx, int n_heads, int n_kv_heads, int dim,
@@ -172,8 +173,8 @@ int zt_attn_bwd_dkdv_train(const float *q, const float *k, const float *v, const
 /* The same backward with dq formed from a stored dS instead of a third
  * kernel that rebuilds it: the dk/dv kernel writes dS[b, h, t, s] for every
  * causal pair into the workspace, and dq = dS k / sqrt(d) is then one causal
- * product per head.  Deterministic like the rest.  workspace: at least
- * zt_attn_backward_train_workspace(...) bytes (delta, then B * H * ceil(T/16)^2
+ * product per head.  Deterministic like the rest.  workspace: 16-byte aligned,
+ * at least zt_attn_backward_train_workspace(...) bytes (delta, then B * H * ceil(T/16)^2
  * 16 x 16 tiles of dS: 2 GiB at T = 4096 with 32 heads).  stage: 1 = delta + dk/dv
  * (+ dS), 2 = dq from dS, 3 = both; | ZT_WS_SCORES when the workspace holds
  * the scores zt_attn_forward_train_ws wrote for these q, k (the dk/dv kernel

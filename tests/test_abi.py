@@ -134,6 +134,8 @@ def test_decode_refusals(zt, capfd):
     nk2 = (ctypes.c_int * 2)(5, 8)
     assert L.zt_attn_decode(NULL, NULL, NULL, NULL, nk2, 2, 8, 4, 2, 32, NULL, ws - 1, NULL) == 1
     assert "workspace" in capfd.readouterr().err
+    assert L.zt_attn_decode(NULL, NULL, NULL, NULL, nk2, 2, 8, 4, 2, 32, 0x10004, ws, NULL) == 1
+    assert "not 16-byte aligned" in capfd.readouterr().err
     assert L.zt_attn_decode_workspace(0, 8, 4, 2, 32) == 0
 
 
@@ -157,6 +159,11 @@ def test_train_path_refusals(zt, capfd):
     assert "lse" in capfd.readouterr().err
     assert L.zt_attn_backward_train_ws(p, p, p, p, p, p, p, p, p, p, need, 1, 8, 4, 2, 32, 4, NULL) == 1
     assert "stage" in capfd.readouterr().err   # ZT_WS_SCORES alone names no stage
+    # Workspaces hold 16-byte vectors: a base that is not 16-byte aligned is refused.
+    assert L.zt_attn_forward_train_ws(p, p, p, p, p, p + 4, need, 1, 8, 4, 2, 32, NULL) == 1
+    assert "not 16-byte aligned" in capfd.readouterr().err
+    assert L.zt_attn_backward_train_ws(p, p, p, p, p, p, p, p, p, p + 8, need, 1, 8, 4, 2, 32, 3, NULL) == 1
+    assert "not 16-byte aligned" in capfd.readouterr().err
 
 
 def test_dense_product_refusals(zt, capfd):

@@ -238,6 +238,17 @@ bool grid_ok(unsigned long long blocks) {
 
 static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
+// Workspaces hold 16-byte vectors (tiles, partials) at 256-byte aligned
+// offsets from their base, so the base must be 16-byte aligned (hipMalloc
+// returns 256).
+static bool workspace_aligned(const void *ws, const char *who) {
+    if ((uintptr_t)ws & 15) {
+        fprintf(stderr, "zt_attn: %s workspace at %p is not 16-byte aligned.\n", who, ws);
+        return false;
+    }
+    return true;
+}
+
 // Rows are read with 16-byte vector loads when dim % 4 == 0 and with 8-byte
 // loads otherwise, so every tensor base (null ones aside) must be aligned to that.
 static bool rows_aligned(int dim, std::initializer_list<const void *> ptrs) {
@@ -597,6 +608,7 @@ int zt_attn_forward_train_ws(const float *q, const float *k, const float *v, flo
                 workspace_bytes, need);
         return 1;
     }
+    if (need != 0 && !workspace_aligned(workspace, "forward_train_ws")) return 1;
     DeviceState *st = need ? device_state() : nullptr;
     float *s_out = (st && scores_path(dim, n_heads, n_kv_heads, st->lds_limit)) ? ws_tiles(workspace, B, T, n_heads)
                                                                                 : nullptr;
@@ -623,6 +635,7 @@ int zt_attn_backward_train_ws(const float *q, const float *k, const float *v, co
                 workspace_bytes, need);
         return 1;
     }
+    if (need != 0 && !workspace_aligned(workspace, "backward_train_ws")) return 1;
     float *delta = static_cast<float *>(workspace);
     float *ds = need ? ws_tiles(workspace, B, T, n_heads) : nullptr;
     BwdArgs a;
@@ -721,6 +734,7 @@ int zt_attn_decode(const float *q, const float *k_cache, const float *v_cache, f
                 need);
         return 1;
     }
+    if (!workspace_aligned(workspace, "decode")) return 1;
     if (!q || !k_cache || !v_cache || !out) {
         fprintf(stderr, "zt_attn: a null tensor pointer is not launchable.\n");
         return 1;
@@ -787,6 +801,7 @@ int zt_attn_decode_step(const float *q, const float *k_new, const float *v_new, 
                 workspace_bytes, need);
         return 1;
     }
+    if (!workspace_aligned(workspace, "decode_step")) return 1;
     if (!q || !k_new || !v_new || !k_cache || !v_cache || !out) {
         fprintf(stderr, "zt_attn: a null tensor pointer is not launchable.\n");
         return 1;
