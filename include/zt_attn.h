@@ -189,9 +189,10 @@ int zt_attn_backward_train_ws(const float *q, const float *k, const float *v, co
 /* zt_attn_forward_train that also leaves the scaled scores q k log2(e)/sqrt(d)
  * of every causal 16 x 16 tile in the workspace's dS tiles, for
  * zt_attn_backward_train_ws(..., stage | ZT_WS_SCORES, ...).  Scores are kept
- * for the shapes whose dk/dv kernel reads them (head_dim <= 128, an even
- * number of query heads per kv head); for the others this is
- * zt_attn_forward_train and ZT_WS_SCORES is ignored.  The workspace is the
+ * for the shapes whose dk/dv kernel reads them (an even number of query heads
+ * per kv head, and head_dim <= 128 or a multiple of 32); for the others this
+ * is zt_attn_forward_train and ZT_WS_SCORES is ignored (so it is for a wide
+ * head whose q or dout rows are not 16-byte aligned).  The workspace is the
  * backward's (zt_attn_backward_train_workspace bytes).  No reference
  * counterpart. */
 int zt_attn_forward_train_ws(const float *q, const float *k, const float *v, float *out, float *lse, void *workspace,

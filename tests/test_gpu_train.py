@@ -154,7 +154,8 @@ def test_train_ws_stages_and_repeats(gpu, zt):
         zt.backward_train_ws(q, k, v, out, do, lse, dq, dk, dv, work[:16], T, H, Hkv, D, B=B)
 
 
-@pytest.mark.parametrize("B,T,H,Hkv,D", [(2, 130, 8, 2, 64), (1, 333, 8, 2, 128), (1, 45, 4, 2, 66)])
+@pytest.mark.parametrize("B,T,H,Hkv,D", [(2, 130, 8, 2, 64), (1, 333, 8, 2, 128), (1, 45, 4, 2, 66),
+                                         (2, 77, 8, 2, 256), (1, 100, 4, 2, 160)])
 def test_train_scores_stages_and_repeats(gpu, zt, B, T, H, Hkv, D):
     """The forward that keeps its scores gives the same out and lse bit for bit;
     the backward that reads them back repeats bit for bit, its stages equal the
@@ -184,10 +185,12 @@ def test_train_scores_stages_and_repeats(gpu, zt, B, T, H, Hkv, D):
 def test_train_scores_plan_names_the_score_reading_kernel(gpu, zt):
     assert zt.plan_train(1, 4096, 32, 8, 128) == ("zt_fwd8ps_d128_k32", "zt_gemm_dqds_128", "zt_bwd_dkdv8s_d128_hs2")
     assert "dkdv8s" not in zt.plan_train(1, 256, 8, 8, 128)[2]   # MHA: no score-reading kernel
-    assert "dkdv8s" not in zt.plan_train(1, 256, 8, 2, 256)[2]   # d = 256: no score-reading kernel
+    assert zt.plan_train(1, 256, 8, 2, 256)[2] == "zt_bwd_dkdv_dmas_d256_hs2"   # wide heads: staged asynchronously
+    assert "dmas" not in zt.plan_train(1, 256, 8, 2, 250)[2]   # rows not whole 32-float chunks: no scores
 
 
-@pytest.mark.parametrize("B,T,H,Hkv,D", [(1, 100, 8, 2, 80), (2, 45, 4, 2, 32), (1, 333, 8, 2, 128)])
+@pytest.mark.parametrize("B,T,H,Hkv,D", [(1, 100, 8, 2, 80), (2, 45, 4, 2, 32), (1, 333, 8, 2, 128),
+                                         (1, 70, 8, 2, 256)])
 def test_train_scores_write_nothing_past_the_workspace(gpu, zt, oracle, B, T, H, Hkv, D):
     """Ragged T: the score-reading dk/dv kernel stages 32 rows, so a stage can
     end past the last row; no score or dS tile may be written outside the

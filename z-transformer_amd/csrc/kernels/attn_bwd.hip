@@ -652,8 +652,9 @@ __device__ __forceinline__ void bwd_dkdv_body(const BwdArgs &a) {
 // other half of a double-buffered LDS tile (dma16, no registers) while stage s
 // computes, with one barrier per stage.  Requires dim == DP (every chunk of a
 // row is inside the head) and 16-byte aligned q/dout; the host falls back to
-// bwd_dkdv_body otherwise.  Same arithmetic as bwd_dkdv_body.
-template <int DP, int HS>
+// bwd_dkdv_body otherwise.  Same arithmetic as bwd_dkdv_body; with SIN it reads
+// the forward's scores from the dS tiles as bwd_dkdv_body does.
+template <int DP, int HS, bool SIN = false>
 __device__ __forceinline__ void bwd_dkdv_dma_body(const BwdArgs &a) {
     constexpr int DQ = DP / 4, NT = DP / 16, KW = 4 / HS, BQ = 16;
     constexpr int CPR = DP / 4;          // 16-byte chunks per row
@@ -680,8 +681,9 @@ __device__ __forceinline__ void bwd_dkdv_dma_body(const BwdArgs &a) {
 
     const int my_key = s0 + l16;
     const bool key_ok = my_key < a.T;
-    float kr[DQ], vr[DQ];
-    load_row_seg<DQ>(kr, a.k + kvoff + (size_t)my_key * kld, grp * DQ, DP, true, key_ok, a.scale_log2e);
+    float kr[SIN ? 1 : DQ], vr[DQ];  // with the forward's scores K is not needed
+    if constexpr (!SIN)
+        load_row_seg<DQ>(kr, a.k + kvoff + (size_t)my_key * kld, grp * DQ, DP, true, key_ok, a.scale_log2e);
     load_row_seg<DQ>(vr, a.v + kvoff + (size_t)my_key * kld, grp * DQ, DP, true, key_ok, 1.f);
 
     f4 dka[NT], dva[NT];
@@ -694,8 +696,18 @@ __device__ __forceinline__ void bwd_dkdv_dma_body(const BwdArgs &a) {
     // Issues the copies of stage `st` into buffer `buf`; the statistics go to
     // registers and are written to LDS by put_stats after the current compute.
     float sm2 = 0.f, sil = 0.f, sde = 0.f;
+    f4 sn = zero4(), sc = zero4();  // this wave's score tile of the next / this stage (SIN)
     auto issue = [&](int st, int buf) {
         const int hi = st / n_t, t0 = wg_s0 + (st % n_t) * BQ;
+        if constexpr (SIN) {
+            sn = zero4();
+            if (t0 + 15 >= s0 && s0 < a.T) {  // wave-uniform; t0 < T for every stage
+                const int nt = (a.T + 15) >> 4;
+                const size_t tile =
+                    (((size_t)b * a.H + kvh * group + hs * hpp + hi) * nt + (t0 >> 4)) * nt + (s0 >> 4);
+                sn = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(a.ds_out + tile * 256) + lane);
+            }
+        }
         if (tid < HS * BQ) {
             const int part = tid / BQ, t = t0 + tid % BQ;
             const int hh = kvh * group + part * hpp + hi;
@@ -730,6 +742,7 @@ __device__ __forceinline__ void bwd_dkdv_dma_body(const BwdArgs &a) {
     __syncthreads();
     for (int st = 0; st < n_stage; ++st) {
         const int buf = st & 1;
+        if constexpr (SIN) sc = sn;
         if (st + 1 < n_stage) issue(st + 1, buf ^ 1);
         const int t0 = wg_s0 + (st % n_t) * BQ;
         if (!(t0 + 15 < s0 || s0 >= a.T)) {
@@ -740,19 +753,35 @@ __device__ __forceinline__ void bwd_dkdv_dma_body(const BwdArgs &a) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) stv[r] = *reinterpret_cast<const f4 *>(sp + (4 * grp + r) * 4);
             f4 s = zero4(), dp = zero4();
+            if constexpr (SIN) {
+                // Scores from the forward; dP alone as two interleaved chains.
+                f4 dp2 = zero4();
+                s = sc;
 #pragma unroll
-            for (int kk = 0; kk < DQ; kk += 4) {
-                const int off = l16 * DP + 4 * swz<CPR>((grp * DQ + kk) >> 2, l16);
-                const f4 qx = *reinterpret_cast<const f4 *>(qs + off);
-                const f4 dx = *reinterpret_cast<const f4 *>(ds + off);
-                s = mfma16(qx.x, kr[kk + 0], s);
-                dp = mfma16(dx.x, vr[kk + 0], dp);
-                s = mfma16(qx.y, kr[kk + 1], s);
-                dp = mfma16(dx.y, vr[kk + 1], dp);
-                s = mfma16(qx.z, kr[kk + 2], s);
-                dp = mfma16(dx.z, vr[kk + 2], dp);
-                s = mfma16(qx.w, kr[kk + 3], s);
-                dp = mfma16(dx.w, vr[kk + 3], dp);
+                for (int kk = 0; kk < DQ; kk += 4) {
+                    const int off = l16 * DP + 4 * swz<CPR>((grp * DQ + kk) >> 2, l16);
+                    const f4 dx = *reinterpret_cast<const f4 *>(ds + off);
+                    dp = mfma16(dx.x, vr[kk + 0], dp);
+                    dp2 = mfma16(dx.y, vr[kk + 1], dp2);
+                    dp = mfma16(dx.z, vr[kk + 2], dp);
+                    dp2 = mfma16(dx.w, vr[kk + 3], dp2);
+                }
+                dp += dp2;
+            } else {
+#pragma unroll
+                for (int kk = 0; kk < DQ; kk += 4) {
+                    const int off = l16 * DP + 4 * swz<CPR>((grp * DQ + kk) >> 2, l16);
+                    const f4 qx = *reinterpret_cast<const f4 *>(qs + off);
+                    const f4 dx = *reinterpret_cast<const f4 *>(ds + off);
+                    s = mfma16(qx.x, kr[kk + 0], s);
+                    dp = mfma16(dx.x, vr[kk + 0], dp);
+                    s = mfma16(qx.y, kr[kk + 1], s);
+                    dp = mfma16(dx.y, vr[kk + 1], dp);
+                    s = mfma16(qx.z, kr[kk + 2], s);
+                    dp = mfma16(dx.z, vr[kk + 2], dp);
+                    s = mfma16(qx.w, kr[kk + 3], s);
+                    dp = mfma16(dx.w, vr[kk + 3], dp);
+                }
             }
             f4 p, dsv;
 #pragma unroll
@@ -864,6 +893,11 @@ __device__ __forceinline__ void bwd_dkdv_dma_body(const BwdArgs &a) {
     extern "C" __global__ void __launch_bounds__(256) zt_bwd_dkdv_dma_d##DP##_hs##HS(BwdArgs a) { \
         bwd_dkdv_dma_body<DP, HS>(a);                                                              \
     }
+// The asynchronously staged kernel reading the forward's scores (wide heads).
+#define ZT_BWD_DKDV_DMAS(DP)                                                                       \
+    extern "C" __global__ void __launch_bounds__(256) zt_bwd_dkdv_dmas_d##DP##_hs2(BwdArgs a) {  \
+        bwd_dkdv_dma_body<DP, 2, true>(a);                                                         \
+    }
 #define ZT_BWD_ALL(DP)                                                                             \
     ZT_BWD_DQ(DP, 32) ZT_BWD_DQ(DP, 64) ZT_BWD_DQ_PF(DP) ZT_BWD_DQ_LSE(DP) ZT_BWD_DKDV(DP, 1) ZT_BWD_DKDV(DP, 2) ZT_BWD_DKDV8(DP)    \
     ZT_BWD_DKDV_DMA(DP, 1) ZT_BWD_DKDV_DMA(DP, 2)
@@ -887,6 +921,7 @@ ZT_BWD_ALL(160)
 ZT_BWD_ALL(192)
 ZT_BWD_ALL(224)
 ZT_BWD_ALL(256)
+ZT_BWD_DKDV_DMAS(160) ZT_BWD_DKDV_DMAS(192) ZT_BWD_DKDV_DMAS(224) ZT_BWD_DKDV_DMAS(256)
 
 // delta[row] = sum_d o[row, d] * dout[row, d] over the B*T*H rows of dim
 // floats (the row statistic the dk/dv kernel needs, autograd.zig:774-797 as

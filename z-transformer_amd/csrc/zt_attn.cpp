@@ -583,12 +583,14 @@ size_t zt_attn_backward_train_workspace(int B, int T, int n_heads, int n_kv_head
 }
 
 // Shapes whose dk/dv kernel can take the forward's scores instead of
-// rebuilding them: the eight-wave, two-way head split kernel with 32 query
-// rows per stage (d <= 128, an even head group).  The forward writes scores
-// only for these.
+// rebuilding them, all with a two-way head split (an even head group): up to
+// d = 128 the eight-wave kernel with 32 query rows per stage, above it the
+// asynchronously staged kernel (whole-head rows: d a multiple of 32).  The
+// forward writes scores only for these.
 static bool scores_path(int dim, int n_heads, int n_kv_heads, size_t lds_limit) {
     const int dp = pad32(dim);
-    return n_kv_heads > 0 && (n_heads / n_kv_heads) % 2 == 0 && dp <= 128 && dkdv_bytes(dp, 2, 4, 32) <= lds_limit;
+    if (n_kv_heads <= 0 || (n_heads / n_kv_heads) % 2 != 0) return false;
+    return dp <= 128 ? dkdv_bytes(dp, 2, 4, 32) <= lds_limit : dim == dp && dkdv_dma_bytes(dp, 2) <= lds_limit;
 }
 
 static float *ws_tiles(void *workspace, int B, int T, int n_heads) {
@@ -651,17 +653,22 @@ int zt_attn_backward_train_ws(const float *q, const float *k, const float *v, co
         return 1;
     }
     a.ds_out = ds;
-    if (scores && scores_path(dim, n_heads, n_kv_heads, st->lds_limit)) {
-        // The forward left the scores in the dS tiles: the eight-wave kernel
-        // that reads them (64 keys x 2 head halves per workgroup).
+    const int dp = pad32(dim);
+    const bool qd_aligned = (uintptr_t)q % 16 == 0 && (uintptr_t)dout % 16 == 0;
+    if (scores && scores_path(dim, n_heads, n_kv_heads, st->lds_limit) && (dp <= 128 || qd_aligned)) {
+        // The forward left the scores in the dS tiles: a kernel that reads
+        // them, 2 head halves x 64 keys (eight waves, d <= 128) or x 32 keys
+        // (four waves, asynchronous staging, wider heads) per workgroup.
+        // (Wider heads on unaligned q / dout rows form Q K^T again.)
         a.scores_in = 1;
         a.HS = 2;
-        a.n_key_tiles = (T + 63) / 64;
+        const int keys = dp <= 128 ? 64 : 32;
+        a.n_key_tiles = (T + keys - 1) / keys;
         const unsigned long long blocks = (unsigned long long)a.n_key_tiles * n_kv_heads * B;
         if (!grid_ok(blocks)) return 1;
         blocks_b = (unsigned)blocks;
-        threads_b = 512;
-        snprintf(name_b, sizeof name_b, "zt_bwd_dkdv8s_d%d_hs2", pad32(dim));
+        threads_b = dp <= 128 ? 512 : 256;
+        snprintf(name_b, sizeof name_b, dp <= 128 ? "zt_bwd_dkdv8s_d%d_hs2" : "zt_bwd_dkdv_dmas_d%d_hs2", dp);
     }
     if (stage & 1) {
         const unsigned long long rows = (unsigned long long)B * T * n_heads;
@@ -991,8 +998,9 @@ int zt_attn_plan_train(int B, int T, int n_heads, int n_kv_heads, int dim, char 
     if (!st) return 1;
     snprintf(dq, len, "zt_gemm_dqds_%d", dqds_tile(B, T, n_heads, dim, st->cus));
     if (scores_path(dim, n_heads, n_kv_heads, st->lds_limit)) {
-        snprintf(dkdv, len, "zt_bwd_dkdv8s_d%d_hs2", pad32(dim));
-        if (strncmp(fwd, "zt_fwd8p_d", 10) == 0) snprintf(fwd, len, "zt_fwd8ps_d%d_k32", pad32(dim));
+        const int dp = pad32(dim);
+        snprintf(dkdv, len, dp <= 128 ? "zt_bwd_dkdv8s_d%d_hs2" : "zt_bwd_dkdv_dmas_d%d_hs2", dp);
+        if (strncmp(fwd, "zt_fwd8p_d", 10) == 0 && dp <= 128) snprintf(fwd, len, "zt_fwd8ps_d%d_k32", dp);
     }
     return 0;
 }
