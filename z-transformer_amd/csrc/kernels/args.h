@@ -124,7 +124,7 @@ struct DqDsArgs {
     const float *k;    // [B, T, Hkv * dim]
     float *dq;         // [B, T, H * dim]
     int B, T, H, Hkv, dim;
-    int tiles_m, tiles_n;
+    int tiles_m, tiles_n;  // row tiles; a workgroup takes tiles_m - 1 - p and p
     float scale;
     bool vec;          // 16-byte loads and stores along k and dq rows
 };

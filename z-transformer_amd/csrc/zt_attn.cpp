@@ -571,8 +571,9 @@ int zt_attn_bwd_dkdv_train(const float *q, const float *k, const float *v, const
 // Tile of the dq-from-dS product: 128 x 128 unless the head is 64 wide or less
 // or 128-tiles would leave CUs idle.
 static int dqds_tile(int B, int T, int n_heads, int dim, int cus) {
-    const unsigned long long tiles128 = (unsigned long long)((T + 127) / 128) * ((dim + 127) / 128) * B * n_heads;
-    return (dim > 64 && tiles128 >= (unsigned long long)cus) ? 128 : 64;
+    const unsigned long long wgs128 =
+        (unsigned long long)(((T + 127) / 128 + 1) / 2) * ((dim + 127) / 128) * B * n_heads;  // row-tile pairs
+    return (dim > 64 && wgs128 >= (unsigned long long)cus) ? 128 : 64;
 }
 
 size_t zt_attn_backward_train_workspace(int B, int T, int n_heads, int n_kv_heads, int dim) {
@@ -686,7 +687,7 @@ int zt_attn_backward_train_ws(const float *q, const float *k, const float *v, co
         const int bt = dqds_tile(B, T, n_heads, dim, st->cus);
         g.tiles_m = (T + bt - 1) / bt;
         g.tiles_n = (dim + bt - 1) / bt;
-        const unsigned long long blocks = (unsigned long long)g.tiles_m * g.tiles_n * B * n_heads;
+        const unsigned long long blocks = (unsigned long long)((g.tiles_m + 1) / 2) * g.tiles_n * B * n_heads;
         if (!grid_ok(blocks)) return 1;
         if (launch(st, bt == 128 ? "zt_gemm_dqds_128" : "zt_gemm_dqds_64", (unsigned)blocks, g, stream)) return 1;
     }
