@@ -70,6 +70,7 @@ def test_backward_any_tile_cap(gpu, zt, oracle, max_tile):
 
 @pytest.mark.parametrize("env", [
     {"ZT_ATTN_W8": "1", "ZT_ATTN_PF": "0"}, {"ZT_ATTN_W8": "1", "ZT_ATTN_PF": "1"},
+    {"ZT_ATTN_W8": "1", "ZT_ATTN_PF": "1", "ZT_ATTN_BPAIR": "0"}, {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "1", "ZT_ATTN_BPAIR": "0"},
     {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "0"}, {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "1"},
     {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "0", "ZT_ATTN_HS": "4"}, {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "1", "ZT_ATTN_HS": "4"},
     {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "0", "ZT_ATTN_HS": "1"}, {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "1", "ZT_ATTN_HS": "1"},
@@ -77,8 +78,8 @@ def test_backward_any_tile_cap(gpu, zt, oracle, max_tile):
 @pytest.mark.parametrize("B,T,H,Hkv,D", [(1, 200, 8, 2, 128), (2, 75, 4, 1, 64), (1, 100, 8, 2, 256)])
 def test_backward_every_dkdv_variant(gpu, zt, oracle, threads, monkeypatch, env, B, T, H, Hkv, D):
     """Each dk/dv kernel variant (eight-wave, register-staged, asynchronously
-    staged; 1/2/4-way head splits), forced through the library's tuning
-    variables, matches the twin."""
+    staged; 1/2/4-way head splits; paired or single key tiles per workgroup),
+    forced through the library's tuning variables, matches the twin."""
     for k_, v_ in env.items():
         monkeypatch.setenv(k_, v_)
     (q, k, v, do), (dq, dk, dv, *_) = _run(gpu, zt, B, T, H, Hkv, D)
@@ -91,6 +92,7 @@ def test_backward_every_dkdv_variant(gpu, zt, oracle, threads, monkeypatch, env,
     {"ZT_ATTN_BK": "32", "ZT_ATTN_QPF": "1", "ZT_ATTN_DQ_W": "8"},
     {"ZT_ATTN_BK": "32", "ZT_ATTN_QPF": "0", "ZT_ATTN_DQ_W": "8"},
     {"ZT_ATTN_BK": "64", "ZT_ATTN_QPF": "0", "ZT_ATTN_DQ_W": "4"},
+    {"ZT_ATTN_BK": "32", "ZT_ATTN_QPF": "1", "ZT_ATTN_DQ_W": "4", "ZT_ATTN_BPAIR": "0"},
 ])
 @pytest.mark.parametrize("B,T,H,Hkv,D", [(1, 200, 8, 2, 128), (2, 75, 4, 1, 64), (1, 61, 6, 3, 66)])
 def test_backward_every_dq_variant(gpu, zt, oracle, threads, monkeypatch, env, B, T, H, Hkv, D):

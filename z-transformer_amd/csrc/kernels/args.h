@@ -13,6 +13,7 @@ struct FwdArgs {
     // of every 16 x 16 tile on or below the diagonal, unmasked, in the dS tile
     // order of BwdArgs::ds_out, for a dk/dv kernel that reads them back.
     float *s_out;
+    int pair;          // a workgroup takes row tiles n_row_tiles - 1 - p and p
     int B, T, H, Hkv, dim;
     int q_offset, n_keys, kv_rows;
     int HW;            // query heads per workgroup (1, 2 or 4; divides H/Hkv)
@@ -42,6 +43,7 @@ struct BwdArgs {
     int B, T, H, Hkv, dim;
     int HW, n_row_tiles, n_head_blocks;  // dq kernel decomposition (as the forward)
     int HS, n_key_tiles;                 // dk/dv kernel: head split, ceil(T / (16 * 4/HS))
+    int pair;                            // both kernels: a workgroup takes tiles p and n - 1 - p
     float scale, scale_log2e;
 };
 

@@ -28,7 +28,7 @@
 
 
 template <int DP, int BK, int NW, bool PF = false>
-__device__ __forceinline__ void bwd_dq_body(const BwdArgs &a) {
+__device__ __forceinline__ void bwd_dq_tile(const BwdArgs &a, const int tile) {
     constexpr int LW = DP + 4, DQ = DP / 4, NT = DP / 16, NJ = BK / 16;
     __shared__ float Ks[BK * LW];
     __shared__ float Vs[BK * LW];
@@ -36,7 +36,6 @@ __device__ __forceinline__ void bwd_dq_body(const BwdArgs &a) {
     const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, grp = lane >> 4, w = tid >> 6;
     const int RB = NW / a.HW;  // 16-row blocks per head in this workgroup
     const int per_tile = a.n_head_blocks * a.B;
-    const int tile = a.n_row_tiles - 1 - (int)blockIdx.x / per_tile;
     const int rem = (int)blockIdx.x % per_tile;
     const int hb = rem % a.n_head_blocks, b = rem / a.n_head_blocks;
     const int group = a.H / a.Hkv;
@@ -219,7 +218,7 @@ __device__ __forceinline__ void bwd_dq_body(const BwdArgs &a) {
 // matmul units instead of the four the statistics-building kernel needs.
 // K/V tiles are register-prefetched as in bwd_dq_body.
 template <int DP, int BK, int NW>
-__device__ __forceinline__ void bwd_dq_lse_body(const BwdArgs &a) {
+__device__ __forceinline__ void bwd_dq_lse_tile(const BwdArgs &a, const int tile) {
     constexpr int LW = DP + 4, DQ = DP / 4, NT = DP / 16, NJ = BK / 16, NTH = 64 * NW, CPR = DP / 4;
     __shared__ float Ks[BK * LW];
     __shared__ float Vs[BK * LW];
@@ -227,7 +226,6 @@ __device__ __forceinline__ void bwd_dq_lse_body(const BwdArgs &a) {
     const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, grp = lane >> 4, w = tid >> 6;
     const int RB = NW / a.HW;
     const int per_tile = a.n_head_blocks * a.B;
-    const int tile = a.n_row_tiles - 1 - (int)blockIdx.x / per_tile;
     const int rem = (int)blockIdx.x % per_tile;
     const int hb = rem % a.n_head_blocks, b = rem / a.n_head_blocks;
     const int group = a.H / a.Hkv;
@@ -364,7 +362,7 @@ __device__ __forceinline__ void bwd_dq_lse_body(const BwdArgs &a) {
 }
 
 template <int DP, int HS, int KW, bool PF = false, int NU = 1, bool SIN = false>
-__device__ __forceinline__ void bwd_dkdv_body(const BwdArgs &a) {
+__device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile) {
     static_assert(!SIN || PF, "the scores are prefetched with the stage's rows");
     constexpr int LW = DP + 4, DQ = DP / 4, NT = DP / 16, NTH = 64 * KW * HS;
     constexpr int BQ = 16 * NU;  // query rows per stage: NU sub-tiles of 16
@@ -379,7 +377,6 @@ __device__ __forceinline__ void bwd_dkdv_body(const BwdArgs &a) {
     const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, grp = lane >> 4, w = tid >> 6;
     const int kbw = w % KW, hs = w / KW;
     const int per_tile = a.Hkv * a.B;
-    const int ktile = (int)blockIdx.x / per_tile;  // ascending = heaviest first
     const int rem = (int)blockIdx.x % per_tile;
     const int kvh = rem % a.Hkv, b = rem / a.Hkv;
     const int group = a.H / a.Hkv;
@@ -655,7 +652,7 @@ __device__ __forceinline__ void bwd_dkdv_body(const BwdArgs &a) {
 // bwd_dkdv_body otherwise.  Same arithmetic as bwd_dkdv_body; with SIN it reads
 // the forward's scores from the dS tiles as bwd_dkdv_body does.
 template <int DP, int HS, bool SIN = false>
-__device__ __forceinline__ void bwd_dkdv_dma_body(const BwdArgs &a) {
+__device__ __forceinline__ void bwd_dkdv_dma_tile(const BwdArgs &a, const int ktile) {
     constexpr int DQ = DP / 4, NT = DP / 16, KW = 4 / HS, BQ = 16;
     constexpr int CPR = DP / 4;          // 16-byte chunks per row
     constexpr int TILE = BQ * DP;        // floats per (part, array) tile
@@ -668,7 +665,6 @@ __device__ __forceinline__ void bwd_dkdv_dma_body(const BwdArgs &a) {
     const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, grp = lane >> 4, w = tid >> 6;
     const int kbw = w % KW, hs = w / KW;
     const int per_tile = a.Hkv * a.B;
-    const int ktile = (int)blockIdx.x / per_tile;
     const int rem = (int)blockIdx.x % per_tile;
     const int kvh = rem % a.Hkv, b = rem / a.Hkv;
     const int group = a.H / a.Hkv;
@@ -847,6 +843,48 @@ __device__ __forceinline__ void bwd_dkdv_dma_body(const BwdArgs &a) {
 // Up to d = 192 the dq kernel fits two waves per SIMD without spilling when
 // asked to (four accumulator/operand sets of DP/4 registers each); above that
 // it keeps one.
+// Grid order and pairing.  Row tiles (dq kernels) run latest first and key
+// tiles (dk/dv kernels) earliest first, heaviest first either way; with
+// a.pair a workgroup also takes the partner tile at the other end (p with
+// n - 1 - p), so every workgroup has the same causal work and those resident
+// together end together.
+template <int DP, int BK, int NW, bool PF = false>
+__device__ __forceinline__ void bwd_dq_body(const BwdArgs &a) {
+    const int p = (int)blockIdx.x / (a.n_head_blocks * a.B), n = a.n_row_tiles;
+    bwd_dq_tile<DP, BK, NW, PF>(a, n - 1 - p);
+    if (a.pair && p < n - 1 - p) {  // workgroup-uniform
+        __syncthreads();  // the first tile's last LDS reads before the second's writes
+        bwd_dq_tile<DP, BK, NW, PF>(a, p);
+    }
+}
+template <int DP, int BK, int NW>
+__device__ __forceinline__ void bwd_dq_lse_body(const BwdArgs &a) {
+    const int p = (int)blockIdx.x / (a.n_head_blocks * a.B), n = a.n_row_tiles;
+    bwd_dq_lse_tile<DP, BK, NW>(a, n - 1 - p);
+    if (a.pair && p < n - 1 - p) {
+        __syncthreads();
+        bwd_dq_lse_tile<DP, BK, NW>(a, p);
+    }
+}
+template <int DP, int HS, int KW, bool PF = false, int NU = 1, bool SIN = false>
+__device__ __forceinline__ void bwd_dkdv_body(const BwdArgs &a) {
+    const int p = (int)blockIdx.x / (a.Hkv * a.B), n = a.n_key_tiles;
+    bwd_dkdv_tile<DP, HS, KW, PF, NU, SIN>(a, p);
+    if (a.pair && n - 1 - p > p) {
+        __syncthreads();  // the head-split sum reads LDS; the next tile's staging writes it
+        bwd_dkdv_tile<DP, HS, KW, PF, NU, SIN>(a, n - 1 - p);
+    }
+}
+template <int DP, int HS, bool SIN = false>
+__device__ __forceinline__ void bwd_dkdv_dma_body(const BwdArgs &a) {
+    const int p = (int)blockIdx.x / (a.Hkv * a.B), n = a.n_key_tiles;
+    bwd_dkdv_dma_tile<DP, HS, SIN>(a, p);
+    if (a.pair && n - 1 - p > p) {
+        __syncthreads();  // the head-split sum reads LDS; the next tile's copies start at once
+        bwd_dkdv_dma_tile<DP, HS, SIN>(a, n - 1 - p);
+    }
+}
+
 #define ZT_BWD_DQ(DP, BK)                                                                          \
     extern "C" __global__ void __launch_bounds__(256, (DP) <= 192 ? 2 : 1)                        \
         zt_bwd_dq_d##DP##_k##BK(BwdArgs a) {                                                       \

@@ -22,7 +22,7 @@
 
 
 template <int DP, int BK, int NW, bool PF>
-__device__ __forceinline__ void attn_fwd_body(const FwdArgs &a) {
+__device__ __forceinline__ void attn_fwd_tile(const FwdArgs &a, const int tile) {
     constexpr int LW = DP + 4;  // LDS row stride: +16 B spreads row starts over banks
     constexpr int DQ = DP / 4;  // d values per lane group
     constexpr int NT = DP / 16; // 16-wide column tiles of the output
@@ -34,7 +34,6 @@ __device__ __forceinline__ void attn_fwd_body(const FwdArgs &a) {
     const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, grp = lane >> 4, w = tid >> 6;
     const int RB = NW / a.HW;  // 16-row blocks per head in this workgroup
     const int per_tile = a.n_head_blocks * a.B;
-    const int tile = a.n_row_tiles - 1 - (int)blockIdx.x / per_tile;
     const int rem = (int)blockIdx.x % per_tile;
     const int hb = rem % a.n_head_blocks, b = rem / a.n_head_blocks;
     const int group = a.H / a.Hkv;
@@ -195,6 +194,18 @@ __device__ __forceinline__ void attn_fwd_body(const FwdArgs &a) {
         float *orow = a.out + (size_t)b * a.T * qld + (size_t)my_row * qld + (size_t)h * a.dim;
 #pragma unroll
         for (int r = 0; r < 4; ++r) store_run<NT>(orow, 4 * grp + r, a.dim, vec4, o, r, inv);
+    }
+}
+
+// Row tile n - 1 - p (latest, heaviest first); with a.pair also row tile p,
+// so that every workgroup has the same causal work.
+template <int DP, int BK, int NW, bool PF>
+__device__ __forceinline__ void attn_fwd_body(const FwdArgs &a) {
+    const int p = (int)blockIdx.x / (a.n_head_blocks * a.B);
+    attn_fwd_tile<DP, BK, NW, PF>(a, a.n_row_tiles - 1 - p);
+    if (a.pair && p < a.n_row_tiles - 1 - p) {  // workgroup-uniform
+        __syncthreads();  // the first tile's last LDS reads before the second's writes
+        attn_fwd_tile<DP, BK, NW, PF>(a, p);
     }
 }
 

@@ -298,7 +298,10 @@ DEVI void dq_ds_body(const DqDsArgs &g) {
     const int bh = rem % (g.B * g.H);
     const int p = rem / (g.B * g.H);
     dq_ds_tile<BT>(g, g.tiles_m - 1 - p, tn, bh);
-    if (p < g.tiles_m - 1 - p) dq_ds_tile<BT>(g, p, tn, bh);  // workgroup-uniform
+    if (p < g.tiles_m - 1 - p) {  // workgroup-uniform
+        __syncthreads();  // the first tile's last LDS reads before the second's writes
+        dq_ds_tile<BT>(g, p, tn, bh);
+    }
 }
 
 }  // namespace
