@@ -35,11 +35,10 @@ struct BwdArgs {
     // 256 floats in lane order (lane l, element r) = (t = 16 tb + 4 (l >> 4) + r,
     // s = 16 sb + (l & 15)); masked pairs are 0.  Tiles above the diagonal are
     // never written.
+    // The score-reading dk/dv kernels (zt_bwd_dkdv8s_*, zt_bwd_dkdv_dmas_*)
+    // find the forward's scaled scores (FwdArgs::s_out) in ds_out on entry;
+    // each tile is read before its dS replaces it.
     float *ds_out;
-    // Scores mode (dk/dv kernels built for it): ds_out holds the forward's
-    // scaled scores (FwdArgs::s_out) on entry; each tile is read before its
-    // dS replaces it.
-    int scores_in;
     int B, T, H, Hkv, dim;
     int HW, n_row_tiles, n_head_blocks;  // dq kernel decomposition (as the forward)
     int HS, n_key_tiles;                 // dk/dv kernel: head split, ceil(T / (16 * 4/HS))

@@ -672,7 +672,6 @@ int zt_attn_backward_train_ws(const float *q, const float *k, const float *v, co
         // them, 2 head halves x 64 keys (eight waves, d <= 128) or x 32 keys
         // (four waves, asynchronous staging, wider heads) per workgroup.
         // (Wider heads on unaligned q / dout rows form Q K^T again.)
-        a.scores_in = 1;
         a.HS = 2;
         const int keys = dp <= 128 ? 64 : 32;
         a.n_key_tiles = (T + keys - 1) / keys;
