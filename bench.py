@@ -337,6 +337,17 @@ def main():
                          f"forward+backward of the C restatement of attention.zig/autograd.zig, 1 thread, "
                          f"{secs:.1f} s", "seconds": round(secs, 2)}
         log(f"CPU baseline: {cpu['value'] * 1e3:.3f} GFLOP/s on {W} rows ({secs:.1f} s)")
+        # The same sample with the restatement's OpenMP variants, which split the
+        # work by (sequence, head) / (sequence, kv head) and keep every element's
+        # operation order (bit-identical to one thread); 16 threads is one GPU's
+        # share of the box's host cores.
+        nthr = max(1, min(16, os.cpu_count() or 1))
+        t0 = time.perf_counter()
+        oracle.attention_forward(qh, kh, vh, B, T, H, Hkv, D, t_begin=T - W, threads=nthr)
+        oracle.attention_backward(qh, kh, vh, dh, B, T, H, Hkv, D, t_begin=T - W, threads=nthr)
+        tsecs = time.perf_counter() - t0
+        cpu["threaded"] = {"value": round(sflop / tsecs / 1e12, 6), "cores": nthr, "seconds": round(tsecs, 2)}
+        log(f"CPU baseline, {nthr} threads: {cpu['threaded']['value'] * 1e3:.3f} GFLOP/s ({tsecs:.1f} s)")
         del np
 
     line = {
