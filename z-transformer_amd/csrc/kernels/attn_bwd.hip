@@ -362,7 +362,7 @@ __device__ __forceinline__ void bwd_dq_lse_tile(const BwdArgs &a, const int tile
 }
 
 template <int DP, int HS, int KW, bool PF = false, int NU = 1, bool SIN = false>
-__device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile) {
+__device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile, const bool up) {
     static_assert(!SIN || PF, "the scores are prefetched with the stage's rows");
     constexpr int LW = DP + 4, DQ = DP / 4, NT = DP / 16, NTH = 64 * KW * HS;
     constexpr int BQ = 16 * NU;  // query rows per stage: NU sub-tiles of 16
@@ -398,13 +398,17 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile)
 #pragma unroll
     for (int i = 0; i < NT; ++i) { dka[i] = zero4(); dva[i] = zero4(); }
 
-    // Stages: (head of each part hi, 16-row tile t0 of the suffix t >= wg_s0),
-    // the tiles walked from the last row down so that the workgroups resident
-    // at one time -- which all reach the end of the sequence -- read the same
-    // Q/dO rows together and share them in L2.
+    // Stages: (row tile t0 of the suffix t >= wg_s0, head of each part hi),
+    // heads inner.  A workgroup's first key tile walks the rows from the last
+    // one down, its partner tile (up) from the diagonal to the end: the
+    // workgroups resident at one time then stand on the same row at the same
+    // time in either phase and read the same Q/dO rows from L2.
     const int n_t = (a.T - wg_s0 + BQ - 1) / BQ;
     const int n_stage = hpp * n_t;
-    auto tile_row = [&](int stg) { return wg_s0 + (n_t - 1 - stg % n_t) * BQ; };
+    auto tile_row = [&](int stg) {
+        const int ri = stg / hpp;
+        return wg_s0 + (up ? ri : n_t - 1 - ri) * BQ;
+    };
 
     // Register prefetch (PF): thread tid holds float4 chunks e = tid + n * NTH
     // of the stage's HS x {Q, dO} x 16 x DP block and one row's statistics;
@@ -417,7 +421,7 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile)
     float pm2 = 0.f, pil = 0.f, pde = 0.f;
     f4 sn[SIN ? NU : 1], sc[SIN ? NU : 1];  // scores of the next / this stage (SIN)
     auto fetch = [&](int stg) {
-        const int hi = stg / n_t, t0 = tile_row(stg);
+        const int hi = stg % hpp, t0 = tile_row(stg);
 #pragma unroll
         for (int n = 0; n < NPF; ++n) {
             const int e = tid + n * NTH;
@@ -485,7 +489,7 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile)
     // One stage's products for this wave, from the staged rows.
     const float *qs = Qs + hs * BQ * LW, *ds = Ds + hs * BQ * LW, *st = St + hs * BQ * 4;
     auto work = [&](int stg) {
-        const int hi = stg / n_t, t0 = tile_row(stg);
+        const int hi = stg % hpp, t0 = tile_row(stg);
         if (t0 + BQ - 1 < s0 || s0 >= a.T) return;  // wave-uniform: no visible pair
 
         // Sub-tile u holds query rows t0 + 16 u + [0, 16).  This lane's four
@@ -588,7 +592,7 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile)
             }
             if (stg + 1 < n_stage) fetch(stg + 1);
         } else {
-            const int hi = stg / n_t, t0 = tile_row(stg);
+            const int hi = stg % hpp, t0 = tile_row(stg);
             // Stage Q, dO rows [t0, t0+16) for every part's head.
             const int nvalid = min(BQ, a.T - t0);
             for (int part = 0; part < HS; ++part) {
@@ -869,10 +873,10 @@ __device__ __forceinline__ void bwd_dq_lse_body(const BwdArgs &a) {
 template <int DP, int HS, int KW, bool PF = false, int NU = 1, bool SIN = false>
 __device__ __forceinline__ void bwd_dkdv_body(const BwdArgs &a) {
     const int p = (int)blockIdx.x / (a.Hkv * a.B), n = a.n_key_tiles;
-    bwd_dkdv_tile<DP, HS, KW, PF, NU, SIN>(a, p);
+    bwd_dkdv_tile<DP, HS, KW, PF, NU, SIN>(a, p, false);
     if (a.pair && n - 1 - p > p) {
         __syncthreads();  // the head-split sum reads LDS; the next tile's staging writes it
-        bwd_dkdv_tile<DP, HS, KW, PF, NU, SIN>(a, n - 1 - p);
+        bwd_dkdv_tile<DP, HS, KW, PF, NU, SIN>(a, n - 1 - p, true);
     }
 }
 template <int DP, int HS, bool SIN = false>
