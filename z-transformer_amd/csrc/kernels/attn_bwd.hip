@@ -420,38 +420,56 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
     f4 pf[NPF];
     float pm2 = 0.f, pil = 0.f, pde = 0.f;
     f4 sn[SIN ? NU : 1], sc[SIN ? NU : 1];  // scores of the next / this stage (SIN)
+    // The statistics stay as loaded until put(): arithmetic on them here would
+    // wait for every load of the fetch and stall the stage's first products.
+    const bool whole_rows = a.dim == DP && vec4;  // workgroup-uniform
     auto fetch = [&](int stg) {
         const int hi = stg % hpp, t0 = tile_row(stg);
+        if (whole_rows) {
+            // Rows past T load the last row: finite values whose products the
+            // mask multiplies by zero (p = dS = 0 there).
 #pragma unroll
-        for (int n = 0; n < NPF; ++n) {
-            const int e = tid + n * NTH;
-            const int part = e / (2 * BQ * CPR), arr = (e / (BQ * CPR)) & 1;
-            const int r = (e / CPR) % BQ, c = (e % CPR) * 4;
-            const int hh = kvh * group + part * hpp + hi, t = t0 + r;
-            const float *src = (arr ? a.dout : a.q) + (size_t)b * a.T * qld + (size_t)t * qld + (size_t)hh * a.dim + c;
-            f4 x = zero4();
-            if (t < a.T && c < a.dim) {
-                if (vec4) {
-                    x = *reinterpret_cast<const f4 *>(src);
-                } else {
-                    const f2 lo = *reinterpret_cast<const f2 *>(src);
-                    x.x = lo.x; x.y = lo.y;
-                    if (c + 2 < a.dim) {
-                        const f2 hi2 = *reinterpret_cast<const f2 *>(src + 2);
-                        x.z = hi2.x; x.w = hi2.y;
+            for (int n = 0; n < NPF; ++n) {
+                const int e = tid + n * NTH;
+                const int part = e / (2 * BQ * CPR), arr = (e / (BQ * CPR)) & 1;
+                const int r = (e / CPR) % BQ, c = (e % CPR) * 4;
+                const int hh = kvh * group + part * hpp + hi, t = min(t0 + r, a.T - 1);
+                pf[n] = *reinterpret_cast<const f4 *>((arr ? a.dout : a.q) + (size_t)b * a.T * qld + (size_t)t * qld +
+                                                      (size_t)hh * DP + c);
+            }
+        } else {
+#pragma unroll
+            for (int n = 0; n < NPF; ++n) {
+                const int e = tid + n * NTH;
+                const int part = e / (2 * BQ * CPR), arr = (e / (BQ * CPR)) & 1;
+                const int r = (e / CPR) % BQ, c = (e % CPR) * 4;
+                const int hh = kvh * group + part * hpp + hi, t = t0 + r;
+                const float *src =
+                    (arr ? a.dout : a.q) + (size_t)b * a.T * qld + (size_t)t * qld + (size_t)hh * a.dim + c;
+                f4 x = zero4();
+                if (t < a.T && c < a.dim) {
+                    if (vec4) {
+                        x = *reinterpret_cast<const f4 *>(src);
+                    } else {
+                        const f2 lo = *reinterpret_cast<const f2 *>(src);
+                        x.x = lo.x; x.y = lo.y;
+                        if (c + 2 < a.dim) {
+                            const f2 hi2 = *reinterpret_cast<const f2 *>(src + 2);
+                            x.z = hi2.x; x.w = hi2.y;
+                        }
                     }
                 }
+                pf[n] = x;
             }
-            pf[n] = x;
         }
         if (tid < HS * BQ) {
             const int part = tid / BQ, t = t0 + tid % BQ;
             const int hh = kvh * group + part * hpp + hi;
-            pm2 = 0.f; pil = 0.f; pde = 0.f;
+            pm2 = 0.f; pil = 0.f; pde = 0.f;  // rows past T: m2 = 0, 1/l = 0, delta = 0
             if (t < a.T) {
                 const size_t o = ((size_t)b * a.T + t) * a.H + hh;
-                pm2 = (a.lse ? a.lse[o] : a.row_max[o]) * kLog2e;
-                pil = a.lse ? 1.f : 1.f / a.row_den[o];
+                pm2 = a.lse ? a.lse[o] : a.row_max[o];
+                pil = a.lse ? 1.f : a.row_den[o];
                 pde = a.row_del[o];
             }
         }
@@ -479,8 +497,8 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
             *reinterpret_cast<f4 *>((arr ? Ds : Qs) + (part * BQ + r) * LW + c) = pf[n];
         }
         if (tid < HS * BQ) {
-            St[tid * 4 + 0] = pm2;
-            St[tid * 4 + 1] = pil;
+            St[tid * 4 + 0] = pm2 * kLog2e;
+            St[tid * 4 + 1] = a.lse || pil == 0.f ? pil : 1.f / pil;  // l >= 1 on every row below T
             St[tid * 4 + 2] = pde;
         }
     };
@@ -711,11 +729,11 @@ __device__ __forceinline__ void bwd_dkdv_dma_tile(const BwdArgs &a, const int kt
         if (tid < HS * BQ) {
             const int part = tid / BQ, t = t0 + tid % BQ;
             const int hh = kvh * group + part * hpp + hi;
-            sm2 = 0.f; sil = 0.f; sde = 0.f;
+            sm2 = 0.f; sil = 0.f; sde = 0.f;  // as loaded; put_stats finishes them
             if (t < a.T) {
                 const size_t o = ((size_t)b * a.T + t) * a.H + hh;
-                sm2 = (a.lse ? a.lse[o] : a.row_max[o]) * kLog2e;
-                sil = a.lse ? 1.f : 1.f / a.row_den[o];
+                sm2 = a.lse ? a.lse[o] : a.row_max[o];
+                sil = a.lse ? 1.f : a.row_den[o];
                 sde = a.row_del[o];
             }
         }
@@ -732,7 +750,9 @@ __device__ __forceinline__ void bwd_dkdv_dma_tile(const BwdArgs &a, const int kt
     auto put_stats = [&](int buf) {
         if (tid < HS * BQ) {
             float *sp = stats + (buf * HS * BQ + tid) * 4;
-            sp[0] = sm2; sp[1] = sil; sp[2] = sde;
+            sp[0] = sm2 * kLog2e;
+            sp[1] = a.lse || sil == 0.f ? sil : 1.f / sil;  // l >= 1 on every row below T
+            sp[2] = sde;
         }
     };
 
