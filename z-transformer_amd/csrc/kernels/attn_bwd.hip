@@ -374,7 +374,8 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
     __shared__ float smem[STAGE_F > RED_F ? STAGE_F : RED_F];
     float *Qs = smem, *Ds = smem + HS * BQ * LW, *St = smem + 2 * HS * BQ * LW;
 
-    const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, grp = lane >> 4, w = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, grp = lane >> 4;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // in a scalar register: wave-uniform branches stay scalar
     const int kbw = w % KW, hs = w / KW;
     const int per_tile = a.Hkv * a.B;
     const int rem = (int)blockIdx.x % per_tile;
@@ -411,82 +412,61 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
     };
 
     // Register prefetch (PF): thread tid holds float4 chunks e = tid + n * NTH
-    // of the stage's HS x {Q, dO} x 16 x DP block and one row's statistics;
-    // they are loaded while the previous stage computes and written to LDS
-    // after the next barrier.  Rows >= T and columns >= dim load as zero.
+    // of the stage's HS x {Q, dO} x BQ x DP block, each lane of every wave
+    // one row's statistics, and each wave its score tiles (SIN); they are
+    // loaded while the previous stage computes and written to LDS after the
+    // next barrier.  Every load is unconditional and in bounds, so the pieces
+    // can be issued between the products: rows past T load row T - 1 and
+    // columns past dim the row's last four floats (the host requires dim % 4
+    // == 0 and 16-byte aligned q and dout), finite values that the causal
+    // mask (p = dS = 0 on rows past T) or the zero columns of K and V keep out
+    // of every stored result.  The statistics stay as loaded until put():
+    // arithmetic on them at the fetch would wait for the fetch's every load.
     constexpr int CPR = DP / 4;
     constexpr int NPF = PF ? HS * 2 * BQ * CPR / NTH : 1;
     static_assert(!PF || (HS * 2 * BQ * CPR) % NTH == 0, "prefetch split");
+    static_assert(!PF || HS * BQ <= 64, "one wave's lanes hold a stage's row statistics");
     f4 pf[NPF];
     float pm2 = 0.f, pil = 0.f, pde = 0.f;
+    bool prow = false;                      // the statistics' row is below T
     f4 sn[SIN ? NU : 1], sc[SIN ? NU : 1];  // scores of the next / this stage (SIN)
-    // The statistics stay as loaded until put(): arithmetic on them here would
-    // wait for every load of the fetch and stall the stage's first products.
-    const bool whole_rows = a.dim == DP && vec4;  // workgroup-uniform
-    auto fetch = [&](int stg) {
+    auto fetch_piece = [&](int n, int stg) {
         const int hi = stg % hpp, t0 = tile_row(stg);
-        if (whole_rows) {
-            // Rows past T load the last row: finite values whose products the
-            // mask multiplies by zero (p = dS = 0 there).
-#pragma unroll
-            for (int n = 0; n < NPF; ++n) {
-                const int e = tid + n * NTH;
-                const int part = e / (2 * BQ * CPR), arr = (e / (BQ * CPR)) & 1;
-                const int r = (e / CPR) % BQ, c = (e % CPR) * 4;
-                const int hh = kvh * group + part * hpp + hi, t = min(t0 + r, a.T - 1);
-                pf[n] = *reinterpret_cast<const f4 *>((arr ? a.dout : a.q) + (size_t)b * a.T * qld + (size_t)t * qld +
-                                                      (size_t)hh * DP + c);
-            }
-        } else {
-#pragma unroll
-            for (int n = 0; n < NPF; ++n) {
-                const int e = tid + n * NTH;
-                const int part = e / (2 * BQ * CPR), arr = (e / (BQ * CPR)) & 1;
-                const int r = (e / CPR) % BQ, c = (e % CPR) * 4;
-                const int hh = kvh * group + part * hpp + hi, t = t0 + r;
-                const float *src =
-                    (arr ? a.dout : a.q) + (size_t)b * a.T * qld + (size_t)t * qld + (size_t)hh * a.dim + c;
-                f4 x = zero4();
-                if (t < a.T && c < a.dim) {
-                    if (vec4) {
-                        x = *reinterpret_cast<const f4 *>(src);
-                    } else {
-                        const f2 lo = *reinterpret_cast<const f2 *>(src);
-                        x.x = lo.x; x.y = lo.y;
-                        if (c + 2 < a.dim) {
-                            const f2 hi2 = *reinterpret_cast<const f2 *>(src + 2);
-                            x.z = hi2.x; x.w = hi2.y;
-                        }
-                    }
-                }
-                pf[n] = x;
-            }
-        }
-        if (tid < HS * BQ) {
-            const int part = tid / BQ, t = t0 + tid % BQ;
-            const int hh = kvh * group + part * hpp + hi;
-            pm2 = 0.f; pil = 0.f; pde = 0.f;  // rows past T: m2 = 0, 1/l = 0, delta = 0
-            if (t < a.T) {
-                const size_t o = ((size_t)b * a.T + t) * a.H + hh;
-                pm2 = a.lse ? a.lse[o] : a.row_max[o];
-                pil = a.lse ? 1.f : a.row_den[o];
-                pde = a.row_del[o];
-            }
+        const int e = tid + n * NTH;
+        const int part = e / (2 * BQ * CPR), arr = (e / (BQ * CPR)) & 1;
+        const int r = min((e / CPR) % BQ, a.T - 1 - t0), c = min((e % CPR) * 4, a.dim - 4);
+        const float *base = (arr ? a.dout : a.q) + ((size_t)b * a.T + t0) * qld +
+                            (size_t)(kvh * group + part * hpp + hi) * a.dim;
+        pf[n] = *reinterpret_cast<const f4 *>(base + (r * (int)qld + c));
+    };
+    auto fetch_aux = [&](int stg) {
+        const int hi = stg % hpp, t0 = tile_row(stg);
+        {
+            const int part = (lane / BQ) % HS, r = lane % BQ;
+            prow = t0 + r < a.T;
+            const size_t o = ((size_t)b * a.T + min(t0 + r, a.T - 1)) * a.H + kvh * group + part * hpp + hi;
+            pm2 = (a.lse ? a.lse : a.row_max)[o];
+            pil = (a.lse ? a.row_del : a.row_den)[o];  // unused with lse
+            pde = a.row_del[o];
         }
         if constexpr (SIN) {
             // This wave's score tiles of the stage (lane order, as dS is stored).
-            const int hh = kvh * group + hs * hpp + hi;
-            const int nt = (a.T + 15) >> 4;
+            // A tile with no visible pair (past T, above the diagonal or past
+            // the last key) loads an in-bounds tile whose values the mask drops.
+            const int nt = (a.T + 15) >> 4, sb = min(s0, a.T - 1) >> 4;
+            const size_t hrow = ((size_t)b * a.H + kvh * group + hs * hpp + hi) * nt;
 #pragma unroll
             for (int u = 0; u < NU; ++u) {
-                sn[u] = zero4();
-                const int tu = t0 + 16 * u;
-                if (tu < a.T && tu + 15 >= s0 && s0 < a.T) {
-                    const size_t tile = (((size_t)b * a.H + hh) * nt + (tu >> 4)) * nt + (s0 >> 4);
-                    sn[u] = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(a.ds_out + tile * 256) + lane);
-                }
+                const int tb = min(t0 + 16 * u, a.T - 1) >> 4;
+                sn[u] = __builtin_nontemporal_load(
+                    reinterpret_cast<const f4 *>(a.ds_out + ((hrow + tb) * nt + sb) * 256) + lane);
             }
         }
+    };
+    auto fetch = [&](int stg) {
+        fetch_aux(stg);
+#pragma unroll
+        for (int n = 0; n < NPF; ++n) fetch_piece(n, stg);
     };
     auto put = [&]() {
 #pragma unroll
@@ -496,19 +476,32 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
             const int r = (e / CPR) % BQ, c = (e % CPR) * 4;
             *reinterpret_cast<f4 *>((arr ? Ds : Qs) + (part * BQ + r) * LW + c) = pf[n];
         }
-        if (tid < HS * BQ) {
-            St[tid * 4 + 0] = pm2 * kLog2e;
-            St[tid * 4 + 1] = a.lse || pil == 0.f ? pil : 1.f / pil;  // l >= 1 on every row below T
-            St[tid * 4 + 2] = pde;
+        if (tid < HS * BQ) {  // rows past T: m2 = 0, 1/l = 0, delta = 0
+            St[tid * 4 + 0] = prow ? pm2 * kLog2e : 0.f;
+            St[tid * 4 + 1] = prow ? (a.lse ? 1.f : 1.f / pil) : 0.f;
+            St[tid * 4 + 2] = prow ? pde : 0.f;
         }
     };
     if constexpr (PF) fetch(0);
 
     // One stage's products for this wave, from the staged rows.
     const float *qs = Qs + hs * BQ * LW, *ds = Ds + hs * BQ * LW, *st = St + hs * BQ * 4;
-    auto work = [&](int stg) {
+    // nx: the stage whose rows the prefetch loads meanwhile (PF).
+    auto work = [&](int stg, int nx) {
         const int hi = stg % hpp, t0 = tile_row(stg);
-        if (t0 + BQ - 1 < s0 || s0 >= a.T) return;  // wave-uniform: no visible pair
+        if (t0 + BQ - 1 < s0 || s0 >= a.T) {  // wave-uniform: no visible pair
+            if constexpr (PF) fetch(nx);
+            return;
+        }
+        // The prefetch pieces go out between the first products' groups.
+        constexpr int NI = DQ / 4;
+        auto fetch_after = [&](int i) {
+            if constexpr (PF) {
+                if (i == 0) fetch_aux(nx);
+#pragma unroll
+                for (int n = i * NPF / NI; n < (i + 1) * NPF / NI; ++n) fetch_piece(n, nx);
+            }
+        };
 
         // Sub-tile u holds query rows t0 + 16 u + [0, 16).  This lane's four
         // rows' statistics per sub-tile are read ahead of the MFMAs.
@@ -525,16 +518,27 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
             f4 dp2[NU];
 #pragma unroll
             for (int u = 0; u < NU; ++u) { s[u] = sc[u]; dp2[u] = zero4(); }
+            // dO operands read one group ahead of their products.
+            f4 dxn[NU];
+#pragma unroll
+            for (int u = 0; u < NU; ++u) dxn[u] = *reinterpret_cast<const f4 *>(ds + (16 * u + l16) * LW + grp * DQ);
 #pragma unroll
             for (int kk = 0; kk < DQ; kk += 4) {
+                f4 dx[NU];
 #pragma unroll
                 for (int u = 0; u < NU; ++u) {
-                    const f4 dx = *reinterpret_cast<const f4 *>(ds + (16 * u + l16) * LW + grp * DQ + kk);
-                    dp[u] = mfma16(dx.x, vr[kk + 0], dp[u]);
-                    dp2[u] = mfma16(dx.y, vr[kk + 1], dp2[u]);
-                    dp[u] = mfma16(dx.z, vr[kk + 2], dp[u]);
-                    dp2[u] = mfma16(dx.w, vr[kk + 3], dp2[u]);
+                    dx[u] = dxn[u];
+                    if (kk + 4 < DQ) dxn[u] = *reinterpret_cast<const f4 *>(ds + (16 * u + l16) * LW + grp * DQ + kk + 4);
                 }
+                __builtin_amdgcn_sched_barrier(0);  // keeps the reads ahead of this group's products
+#pragma unroll
+                for (int u = 0; u < NU; ++u) {
+                    dp[u] = mfma16(dx[u].x, vr[kk + 0], dp[u]);
+                    dp2[u] = mfma16(dx[u].y, vr[kk + 1], dp2[u]);
+                    dp[u] = mfma16(dx[u].z, vr[kk + 2], dp[u]);
+                    dp2[u] = mfma16(dx[u].w, vr[kk + 3], dp2[u]);
+                }
+                fetch_after(kk / 4);
             }
 #pragma unroll
             for (int u = 0; u < NU; ++u) dp[u] += dp2[u];
@@ -554,20 +558,34 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
                     s[u] = mfma16(qx.w, kr[kk + 3], s[u]);
                     dp[u] = mfma16(dx.w, vr[kk + 3], dp[u]);
                 }
+                fetch_after(kk / 4);
             }
         }
         // s[u][r] = S[t = t0 + 16 u + 4 grp + r][key = s0 + l16]
+        // With the forward's scores (log-sum-exp statistics) 1/l is 1.
         f4 p[NU], dsv[NU];
+        if (t0 >= s0 + 15 && t0 + BQ <= a.T) {  // wave-uniform: every pair of the stage is visible
 #pragma unroll
-        for (int u = 0; u < NU; ++u)
+            for (int u = 0; u < NU; ++u)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int t = t0 + 16 * u + 4 * grp + r;
-                const bool vis = (t < a.T) && (t >= my_key);
-                const float e = fast_exp2(s[u][r] - stv[u][r].x) * stv[u][r].y;
-                p[u][r] = vis ? e : 0.f;
-                dsv[u][r] = p[u][r] * (dp[u][r] - stv[u][r].z);
-            }
+                for (int r = 0; r < 4; ++r) {
+                    p[u][r] = SIN ? fast_exp2(s[u][r] - stv[u][r].x)
+                                  : fast_exp2(s[u][r] - stv[u][r].x) * stv[u][r].y;
+                    dsv[u][r] = p[u][r] * (dp[u][r] - stv[u][r].z);
+                }
+        } else {
+#pragma unroll
+            for (int u = 0; u < NU; ++u)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int t = t0 + 16 * u + 4 * grp + r;
+                    const bool vis = (t < a.T) && (t >= my_key);
+                    const float e = SIN ? fast_exp2(s[u][r] - stv[u][r].x)
+                                        : fast_exp2(s[u][r] - stv[u][r].x) * stv[u][r].y;
+                    p[u][r] = vis ? e : 0.f;
+                    dsv[u][r] = p[u][r] * (dp[u][r] - stv[u][r].z);
+                }
+        }
         // dS for a dq product outside this kernel, one 16 x 16 tile per (u) in lane
         // order; nontemporal, so the 1 GB stream does not evict the Q/dO rows
         // the other workgroups are about to reread.
@@ -608,7 +626,6 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
 #pragma unroll
                 for (int u = 0; u < NU; ++u) sc[u] = sn[u];
             }
-            if (stg + 1 < n_stage) fetch(stg + 1);
         } else {
             const int hi = stg % hpp, t0 = tile_row(stg);
             // Stage Q, dO rows [t0, t0+16) for every part's head.
@@ -635,7 +652,7 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
             }
             __syncthreads();
         }
-        work(stg);
+        work(stg, min(stg + 1, n_stage - 1));  // the last stage fetches its own rows again, unused
     }
 
     // Sum the head-split partials in a fixed order (part 0 + 1 + ...).

@@ -413,7 +413,8 @@ int backward_prepare(const float *q, const float *k, const float *v, const float
     else
         snprintf(name_dq, 64, nw_dq == 8 ? "zt_bwd_dq8_d%d_k%d" : "zt_bwd_dq_d%d_k%d", dp, bk);
     *threads_dq = 64u * nw_dq;
-    const bool pf = env_choice("ZT_ATTN_PF", 1, {0, 1}) == 1;
+    // The prefetching kernel loads whole 16-byte chunks unconditionally.
+    const bool pf = dim % 4 == 0 && aligned && env_choice("ZT_ATTN_PF", 1, {0, 1}) == 1;
     if (wide)
         snprintf(name_dkdv, 64, pf ? "zt_bwd_dkdv8p_d%d_hs2" : "zt_bwd_dkdv8_d%d_hs2", dp);
     else
@@ -595,13 +596,13 @@ size_t zt_attn_backward_train_workspace(int B, int T, int n_heads, int n_kv_head
 }
 
 // Shapes whose dk/dv kernel can take the forward's scores instead of
-// rebuilding them, all with a two-way head split (an even head group): up to
-// d = 128 the eight-wave kernel with 32 query rows per stage, above it the
-// asynchronously staged kernel (whole-head rows: d a multiple of 32).  The
-// forward writes scores only for these.
+// rebuilding them, all with a two-way head split (an even head group) and
+// 16-byte row chunks (d % 4 == 0): up to d = 128 the eight-wave kernel with
+// 32 query rows per stage, above it the asynchronously staged kernel
+// (whole-head rows: d a multiple of 32).  The forward writes scores only for these.
 static bool scores_path(int dim, int n_heads, int n_kv_heads, size_t lds_limit) {
     const int dp = pad32(dim);
-    if (n_kv_heads <= 0 || (n_heads / n_kv_heads) % 2 != 0) return false;
+    if (n_kv_heads <= 0 || (n_heads / n_kv_heads) % 2 != 0 || dim % 4 != 0) return false;
     return dp <= 128 ? dkdv_bytes(dp, 2, 4, 32) <= lds_limit : dim == dp && dkdv_dma_bytes(dp, 2) <= lds_limit;
 }
 
@@ -667,11 +668,11 @@ int zt_attn_backward_train_ws(const float *q, const float *k, const float *v, co
     a.ds_out = ds;
     const int dp = pad32(dim);
     const bool qd_aligned = (uintptr_t)q % 16 == 0 && (uintptr_t)dout % 16 == 0;
-    if (scores && scores_path(dim, n_heads, n_kv_heads, st->lds_limit) && (dp <= 128 || qd_aligned)) {
+    if (scores && scores_path(dim, n_heads, n_kv_heads, st->lds_limit) && qd_aligned) {
         // The forward left the scores in the dS tiles: a kernel that reads
         // them, 2 head halves x 64 keys (eight waves, d <= 128) or x 32 keys
         // (four waves, asynchronous staging, wider heads) per workgroup.
-        // (Wider heads on unaligned q / dout rows form Q K^T again.)
+        // (Unaligned q / dout rows form Q K^T again.)
         a.HS = 2;
         const int keys = dp <= 128 ? 64 : 32;
         a.n_key_tiles = (T + keys - 1) / keys;
