@@ -31,7 +31,8 @@ __device__ __forceinline__ void attn_fwd_tile(const FwdArgs &a, const int tile) 
     __shared__ float Ks[BK * LW];
     __shared__ float Vs[BK * LW];
 
-    const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, grp = lane >> 4, w = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, grp = lane >> 4;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // in a scalar register: wave-uniform branches stay scalar
     const int RB = NW / a.HW;  // 16-row blocks per head in this workgroup
     const int per_tile = a.n_head_blocks * a.B;
     const int rem = (int)blockIdx.x % per_tile;
@@ -61,39 +62,31 @@ __device__ __forceinline__ void attn_fwd_tile(const FwdArgs &a, const int tile) 
 
     // Register prefetch (PF): thread tid holds float4 chunks e = tid + n * NTH
     // of the next K/V tile (2 x BK x DP floats), loaded while the current tile
-    // computes and written to LDS after the next barrier.  Keys >= n_keys and
-    // columns >= dim load as zero.
+    // computes and written to LDS after the next barrier.  Every load is
+    // unconditional and in bounds, so the pieces can be issued between the
+    // score products: keys past n_keys load key n_keys - 1 (their scores are
+    // masked, so P is 0 there) and columns past dim the row's last four floats
+    // (met by Q's zero columns, or landing in output columns never stored); the
+    // host picks this kernel only for dim % 4 == 0, whose rows are 16-byte aligned.
     constexpr int CPR = DP / 4;
     constexpr int NPF = PF ? 2 * BK * CPR / NTH : 1;
     static_assert(!PF || (2 * BK * CPR) % NTH == 0, "prefetch split");
     f4 pf[NPF];
+    auto fetch_piece = [&](int n, int k0) {
+        const int e = tid + n * NTH;
+        const int arr = e / (BK * CPR), r = min((e / CPR) % BK, a.n_keys - 1 - k0), c = min((e % CPR) * 4, a.dim - 4);
+        pf[n] = *reinterpret_cast<const f4 *>((arr ? vb : kb) + (size_t)k0 * kld + (r * (int)kld + c));
+    };
     auto fetch = [&](int k0) {
 #pragma unroll
-        for (int n = 0; n < NPF; ++n) {
-            const int e = tid + n * NTH;
-            const int arr = e / (BK * CPR), r = (e / CPR) % BK, c = (e % CPR) * 4;
-            const int key = k0 + r;
-            const float *src = (arr ? vb : kb) + (size_t)key * kld + c;
-            f4 x = zero4();
-            if (key < a.n_keys && c < a.dim) {
-                if (vec4) {
-                    x = *reinterpret_cast<const f4 *>(src);
-                } else {
-                    const f2 lo = *reinterpret_cast<const f2 *>(src);
-                    x.x = lo.x; x.y = lo.y;
-                    if (c + 2 < a.dim) {
-                        const f2 hi = *reinterpret_cast<const f2 *>(src + 2);
-                        x.z = hi.x; x.w = hi.y;
-                    }
-                }
-            }
-            pf[n] = x;
-        }
+        for (int n = 0; n < NPF; ++n) fetch_piece(n, k0);
     };
     if constexpr (PF) fetch(0);
 
     for (int k0 = 0; k0 < kend_wg; k0 += BK) {
         __syncthreads();
+        // The tile the prefetch loads meanwhile (the last one loads itself again, unused).
+        const int kn = k0 + BK < kend_wg ? k0 + BK : k0;
         if constexpr (PF) {
 #pragma unroll
             for (int n = 0; n < NPF; ++n) {
@@ -102,14 +95,16 @@ __device__ __forceinline__ void attn_fwd_tile(const FwdArgs &a, const int tile) 
                 *reinterpret_cast<f4 *>((arr ? Vs : Ks) + r * LW + c) = pf[n];
             }
             __syncthreads();
-            if (k0 + BK < kend_wg) fetch(k0 + BK);
         } else {
             const int nvalid = min(BK, a.n_keys - k0);
             stage_rows<DP, LW, NTH>(Ks, kb + (size_t)k0 * kld, kld, BK, nvalid, a.dim, vec4, tid);
             stage_rows<DP, LW, NTH>(Vs, vb + (size_t)k0 * kld, kld, BK, nvalid, a.dim, vec4, tid);
             __syncthreads();
         }
-        if (k0 >= kend_w) continue;  // wave-uniform: nothing here is visible to this wave
+        if (k0 >= kend_w) {  // wave-uniform: nothing here is visible to this wave
+            if constexpr (PF) fetch(kn);
+            continue;
+        }
 
         // Scores for every 16-key sub-block, the NJ accumulation chains
         // interleaved so consecutive MFMAs are independent.  A sub-block that is
@@ -128,6 +123,11 @@ __device__ __forceinline__ void attn_fwd_tile(const FwdArgs &a, const int tile) 
                 s[j] = mfma16(kx.z, qr[kk + 2], s[j]);
                 s[j] = mfma16(kx.w, qr[kk + 3], s[j]);
             }
+            if constexpr (PF) {  // the prefetch pieces go out between the score products
+                constexpr int NI = DQ / 4;
+#pragma unroll
+                for (int n = (kk / 4) * NPF / NI; n < (kk / 4 + 1) * NPF / NI; ++n) fetch_piece(n, kn);
+            }
         }
         if (a.s_out) {
             // Element (t = row0 + l16, s = k0 + 16 j + 4 grp + r) goes to lane
@@ -144,12 +144,14 @@ __device__ __forceinline__ void attn_fwd_tile(const FwdArgs &a, const int tile) 
                 for (int r = 0; r < 4; ++r) srow[j * 256 + (4 * grp + r) * 4] = s[j][r];
             }
         }
+        if (k0 + BK - 1 > a.q_offset + row0 || k0 + BK > a.n_keys) {  // wave-uniform: a key past a row or past n_keys
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) {
+            for (int j = 0; j < NJ; ++j) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int key = k0 + 16 * j + 4 * grp + r;
-                if (key > qpos || key >= a.n_keys) s[j][r] = -INFINITY;
+                for (int r = 0; r < 4; ++r) {
+                    const int key = k0 + 16 * j + 4 * grp + r;
+                    if (key > qpos || key >= a.n_keys) s[j][r] = -INFINITY;
+                }
             }
         }
         float mt = -INFINITY;

@@ -168,8 +168,9 @@ int fwd_waves(int hw) { return env_choice("ZT_ATTN_FWD_W", hw == 4 ? 8 : 4, {4, 
 // register-prefetched variant (ZT_ATTN_FPF; default with eight waves, where
 // it measured C3 1.315 -> 1.225 ms and C5 0.758 -> 0.630 ms; with four waves
 // the prefetch registers cost occupancy and it loses).
-void fwd_kernel_name(char *name, size_t len, int dp, int bk, int nw) {
-    const bool pf = bk == 32 && env_choice("ZT_ATTN_FPF", nw == 8 ? 1 : 0, {0, 1}) == 1;
+void fwd_kernel_name(char *name, size_t len, int dim, int dp, int bk, int nw) {
+    // The prefetching kernels load 16-byte row chunks unconditionally (dim % 4 == 0).
+    const bool pf = bk == 32 && dim % 4 == 0 && env_choice("ZT_ATTN_FPF", nw == 8 ? 1 : 0, {0, 1}) == 1;
     if (pf)
         snprintf(name, len, nw == 8 ? "zt_fwd8p_d%d_k32" : "zt_fwdp_d%d_k32", dp);
     else
@@ -316,7 +317,7 @@ int forward_impl(const float *q, const float *k, const float *v, float *out, int
         (unsigned long long)(a.pair ? (a.n_row_tiles + 1) / 2 : a.n_row_tiles) * a.n_head_blocks * B;
     if (!grid_ok(blocks)) return 1;
     char name[64];
-    fwd_kernel_name(name, sizeof name, dp, bk, nw);
+    fwd_kernel_name(name, sizeof name, dim, dp, bk, nw);
     if (s_out && dp <= 128 && strncmp(name, "zt_fwd8p_d", 10) == 0)
         snprintf(name, sizeof name, "zt_fwd8ps_d%d_k32", dp);  // same kernel, named for its role
     return launch(st, name, (unsigned)blocks, a, stream, 64u * nw);
@@ -988,7 +989,7 @@ int zt_attn_plan(int B, int T, int n_heads, int n_kv_heads, int dim, int max_til
     const int dp = pad32(dim);
     int bk = key_tile(Tiled::Forward, dp, max_tile);
     if (fwd_tile_bytes(dp, bk) > st->lds_limit) bk = 32;
-    fwd_kernel_name(fwd, len, dp, bk, fwd_waves(heads_per_wg(n_heads / n_kv_heads)));
+    fwd_kernel_name(fwd, len, dim, dp, bk, fwd_waves(heads_per_wg(n_heads / n_kv_heads)));
     BwdArgs a;
     DeviceState *st2 = nullptr;
     unsigned ba = 0, bb = 0, ta = 0, tb = 0;
