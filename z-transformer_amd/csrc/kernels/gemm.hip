@@ -200,13 +200,14 @@ DEVI void gemm_body(const GemmArgs &g) {
 // index-contiguous orientation of A, so slabs are staged with 16-byte loads and
 // stores; tiles above the diagonal (never written) and rows past T read as 0.
 // Grid: row-tile pairs, then (sequence, head), then column tiles.
-template <int BT>
+template <int BT, bool VEC>
 DEVI void dq_ds_tile(const DqDsArgs &g, const int tm, const int tn, const int bh) {
     using TL = Tile<BT>;
     constexpr int TW = TL::TW, NCH = TL::NCH;
     __shared__ __attribute__((aligned(16))) float As[BK * TL::LIC];
     __shared__ __attribute__((aligned(16))) float Bs[BK * TL::LIC];
-    const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, grp = lane >> 4, w = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, grp = lane >> 4;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = TL::WT * (w >> 1), wn = TL::WT * (w & 1);
     const int b = bh / g.H, h = bh % g.H, kvh = h / (g.H / g.Hkv);
     const int m0 = tm * BT, n0 = tn * BT;
@@ -226,16 +227,39 @@ DEVI void dq_ds_tile(const DqDsArgs &g, const int tm, const int tn, const int bh
     // A slab: keys k0..k0+31 x queries m0..m0+BT-1 = (BT/16) x 2 tiles; chunk e
     // is (tile, lane-chunk); put() stores it at [key][query .. query+3].
     f4 pa[NCH], pb[NCH];
+    // With VEC (16-byte k rows) every load is unconditional and in bounds: a
+    // dS tile outside the causal triangle or the grid loads a written one and
+    // is zeroed by a select, and key rows past kend load row kend - 1 (met by
+    // those zero tiles) and columns past dim the row's last four floats
+    // (landing in dq columns never stored).
     auto fetch_a = [&](int k0) {
 #pragma unroll
         for (int n = 0; n < NCH; ++n) {
             const int e = tid + n * NTHR;
             const int tile = e >> 6, c = e & 63;         // 64 chunks per tile
             const int tb = (m0 >> 4) + tile % (BT / 16), sb = (k0 >> 4) + tile / (BT / 16);
-            f4 x = zero4();
-            if (sb <= tb && tb < nt)  // read once: nontemporal
-                x = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(A + ((size_t)tb * nt + sb) * 256) + c);
-            pa[n] = x;
+            const bool ok = sb <= tb && tb < nt;
+            if constexpr (VEC) {  // read once: nontemporal
+                const int tc = min(tb, nt - 1), sc = min(sb, tc);
+                const f4 x = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(A + ((size_t)tc * nt + sc) * 256) + c);
+                pa[n] = ok ? x : zero4();
+            } else {
+                f4 x = zero4();
+                if (ok) x = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(A + ((size_t)tb * nt + sb) * 256) + c);
+                pa[n] = x;
+            }
+        }
+    };
+    auto fetch_b = [&](int k0) {
+        if constexpr (VEC) {
+#pragma unroll
+            for (int n = 0; n < NCH; ++n) {
+                const int e = tid + n * NTHR;
+                const int k = min(k0 + e / (BT / 4), kend - 1), r = min(n0 + 4 * (e % (BT / 4)), g.dim - 4);
+                pb[n] = *reinterpret_cast<const f4 *>(Bm + (size_t)k * kld + r);
+            }
+        } else {
+            fetch<BT, false>(pb, Bm, (int)kld, n0, g.dim, k0, kend, false, tid);
         }
     };
     auto put_a = [&]() {
@@ -248,15 +272,16 @@ DEVI void dq_ds_tile(const DqDsArgs &g, const int tm, const int tn, const int bh
         }
     };
     fetch_a(0);
-    fetch<BT, false>(pb, Bm, (int)kld, n0, g.dim, 0, kend, g.vec, tid);
+    fetch_b(0);
     for (int k0 = 0; k0 < kend; k0 += BK) {
         __syncthreads();
         put_a();
         put<BT, false>(Bs, pb, tid);
         __syncthreads();
-        if (k0 + BK < kend) {
-            fetch_a(k0 + BK);
-            fetch<BT, false>(pb, Bm, (int)kld, n0, g.dim, k0 + BK, kend, g.vec, tid);
+        if (VEC || k0 + BK < kend) {  // the last slab fetches itself again, unused
+            const int kn = k0 + BK < kend ? k0 + BK : k0;
+            fetch_a(kn);
+            fetch_b(kn);
         }
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
@@ -297,10 +322,18 @@ DEVI void dq_ds_body(const DqDsArgs &g) {
     rem /= g.tiles_n;
     const int bh = rem % (g.B * g.H);
     const int p = rem / (g.B * g.H);
-    dq_ds_tile<BT>(g, g.tiles_m - 1 - p, tn, bh);
-    if (p < g.tiles_m - 1 - p) {  // workgroup-uniform
-        __syncthreads();  // the first tile's last LDS reads before the second's writes
-        dq_ds_tile<BT>(g, p, tn, bh);
+    if (g.vec) {
+        dq_ds_tile<BT, true>(g, g.tiles_m - 1 - p, tn, bh);
+        if (p < g.tiles_m - 1 - p) {  // workgroup-uniform
+            __syncthreads();  // the first tile's last LDS reads before the second's writes
+            dq_ds_tile<BT, true>(g, p, tn, bh);
+        }
+    } else {
+        dq_ds_tile<BT, false>(g, g.tiles_m - 1 - p, tn, bh);
+        if (p < g.tiles_m - 1 - p) {
+            __syncthreads();
+            dq_ds_tile<BT, false>(g, p, tn, bh);
+        }
     }
 }
 
