@@ -278,13 +278,13 @@ DEVI void dq_ds_tile(const DqDsArgs &g, const int tm, const int tn, const int bh
         put_a();
         put<BT, false>(Bs, pb, tid);
         __syncthreads();
-        if (VEC || k0 + BK < kend) {  // the last slab fetches itself again, unused
-            const int kn = k0 + BK < kend ? k0 + BK : k0;
-            fetch_a(kn);
-            fetch_b(kn);
-        }
+        // The next slab (the last one fetches itself again, unused): dS
+        // chunks now, K chunks between the two halves' products.
+        const int kn = k0 + BK < kend ? k0 + BK : k0;
+        if (VEC || k0 + BK < kend) fetch_a(kn);
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
+            if (hh == 1 && (VEC || k0 + BK < kend)) fetch_b(kn);
             f4 av[TW], bv[TW];
             operand<BT, false>(av, As, wm, l16, grp, hh);
             operand<BT, false>(bv, Bs, wn, l16, grp, hh);
