@@ -27,13 +27,21 @@
 #include "args.h"
 
 
-template <int DP, int BK, int NW, bool PF = false>
+// The K and V tiles of the dq kernels: one allocation per (DP, BK), shared by
+// a kernel's instantiations for aligned and unaligned rows.
+template <int DP, int BK>
+__device__ __forceinline__ float *dq_kv_tiles() {
+    __shared__ float kv[2 * BK * (DP + 4)];
+    return kv;
+}
+
+template <int DP, int BK, int NW, bool PF = false, bool VEC = false>
 __device__ __forceinline__ void bwd_dq_tile(const BwdArgs &a, const int tile) {
     constexpr int LW = DP + 4, DQ = DP / 4, NT = DP / 16, NJ = BK / 16;
-    __shared__ float Ks[BK * LW];
-    __shared__ float Vs[BK * LW];
+    float *const Ks = dq_kv_tiles<DP, BK>(), *const Vs = Ks + BK * LW;
 
-    const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, grp = lane >> 4, w = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, grp = lane >> 4;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // in a scalar register: wave-uniform branches stay scalar
     const int RB = NW / a.HW;  // 16-row blocks per head in this workgroup
     const int per_tile = a.n_head_blocks * a.B;
     const int rem = (int)blockIdx.x % per_tile;
@@ -67,11 +75,18 @@ __device__ __forceinline__ void bwd_dq_tile(const BwdArgs &a, const int tile) {
     constexpr int NPF = PF ? 2 * BK * CPR / NTH : 1;
     static_assert(!PF || (2 * BK * CPR) % NTH == 0, "prefetch split");
     f4 pf[NPF];
-    auto fetch = [&](int k0) {
-#pragma unroll
-        for (int n = 0; n < NPF; ++n) {
-            const int e = tid + n * NTH;
-            const int arr = e / (BK * CPR), r = (e / CPR) % BK, c = (e % CPR) * 4;
+    // VEC (dim % 4 == 0, 16-byte aligned rows): every load unconditional and
+    // in bounds, so the pieces go out between the score products -- keys past
+    // T load key T - 1 (masked, P = 0) and columns past dim the row's last
+    // chunk (met by Q's and dO's zero columns, or landing in dq columns never
+    // stored).  Otherwise guarded loads, all at the top of the tile.
+    auto fetch_piece = [&](int n, int k0) {
+        const int e = tid + n * NTH;
+        const int arr = e / (BK * CPR), r = (e / CPR) % BK, c = (e % CPR) * 4;
+        if constexpr (VEC) {
+            pf[n] = *reinterpret_cast<const f4 *>((arr ? vb : kb) + (size_t)k0 * kld +
+                                                  (min(r, a.T - 1 - k0) * (int)kld + min(c, a.dim - 4)));
+        } else {
             const int key = k0 + r;
             const float *src = (arr ? vb : kb) + (size_t)key * kld + c;
             f4 x = zero4();
@@ -90,10 +105,22 @@ __device__ __forceinline__ void bwd_dq_tile(const BwdArgs &a, const int tile) {
             pf[n] = x;
         }
     };
+    auto fetch = [&](int k0) {
+#pragma unroll
+        for (int n = 0; n < NPF; ++n) fetch_piece(n, k0);
+    };
+    // Pieces of group i of NI between the score products (VEC, up to d = 192).
+    auto fetch_group = [&](int i, int ni, int k0) {
+#pragma unroll
+        for (int n = i * NPF / ni; n < (i + 1) * NPF / ni; ++n) fetch_piece(n, k0);
+    };
     if constexpr (PF) fetch(0);
 
+    // Interleaved prefetch: VEC kernels whose score loop runs k-step outer.
+    constexpr bool ILV = PF && VEC && DP <= 192;
     for (int k0 = 0; k0 < kend_wg; k0 += BK) {
         __syncthreads();
+        const int kn = k0 + BK < kend_wg ? k0 + BK : k0;  // the last tile fetches itself again, unused
         if constexpr (PF) {
 #pragma unroll
             for (int n = 0; n < NPF; ++n) {
@@ -102,14 +129,19 @@ __device__ __forceinline__ void bwd_dq_tile(const BwdArgs &a, const int tile) {
                 *reinterpret_cast<f4 *>((arr ? Vs : Ks) + r * LW + c) = pf[n];
             }
             __syncthreads();
-            if (k0 + BK < kend_wg) fetch(k0 + BK);
+            if constexpr (!ILV) {
+                if (k0 + BK < kend_wg) fetch(k0 + BK);
+            }
         } else {
             const int nvalid = min(BK, a.T - k0);
             stage_rows<DP, LW, NTH>(Ks, kb + (size_t)k0 * kld, kld, BK, nvalid, a.dim, vec4, tid);
             stage_rows<DP, LW, NTH>(Vs, vb + (size_t)k0 * kld, kld, BK, nvalid, a.dim, vec4, tid);
             __syncthreads();
         }
-        if (k0 >= kend_w) continue;
+        if (k0 >= kend_w) {  // wave-uniform: nothing here is visible to this wave
+            if constexpr (ILV) fetch(kn);
+            continue;
+        }
 
         // S^T and dP^T for every 16-key sub-block.  Up to d = 192 the 2 * NJ
         // independent accumulation chains are interleaved so consecutive MFMAs
@@ -135,21 +167,25 @@ __device__ __forceinline__ void bwd_dq_tile(const BwdArgs &a, const int tile) {
         };
         if constexpr (DP <= 192) {
 #pragma unroll
-            for (int kk = 0; kk < DQ; kk += 4)
+            for (int kk = 0; kk < DQ; kk += 4) {
 #pragma unroll
                 for (int j = 0; j < NJ; ++j) score_step(j, kk);
+                if constexpr (ILV) fetch_group(kk / 4, DQ / 4, kn);
+            }
         } else {
 #pragma unroll
             for (int j = 0; j < NJ; ++j)
 #pragma unroll
                 for (int kk = 0; kk < DQ; kk += 4) score_step(j, kk);
         }
+        if (k0 + BK - 1 > row0 || k0 + BK > a.T) {  // wave-uniform: a key past a row or past T
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) {
+            for (int j = 0; j < NJ; ++j) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int key = k0 + 16 * j + 4 * grp + r;
-                if (key > my_row || key >= a.T) s[j][r] = -INFINITY;
+                for (int r = 0; r < 4; ++r) {
+                    const int key = k0 + 16 * j + 4 * grp + r;
+                    if (key > my_row || key >= a.T) s[j][r] = -INFINITY;
+                }
             }
         }
         float mt = -INFINITY;
@@ -217,13 +253,14 @@ __device__ __forceinline__ void bwd_dq_tile(const BwdArgs &a, const int tile) {
 // rescaling), dP^T = V dO^T, dS = P (dP - delta), dq^T += K^T dS^T -- three
 // matmul units instead of the four the statistics-building kernel needs.
 // K/V tiles are register-prefetched as in bwd_dq_body.
-template <int DP, int BK, int NW>
+template <int DP, int BK, int NW, bool VEC = false>
 __device__ __forceinline__ void bwd_dq_lse_tile(const BwdArgs &a, const int tile) {
     constexpr int LW = DP + 4, DQ = DP / 4, NT = DP / 16, NJ = BK / 16, NTH = 64 * NW, CPR = DP / 4;
-    __shared__ float Ks[BK * LW];
-    __shared__ float Vs[BK * LW];
+    constexpr bool PF = true;
+    float *const Ks = dq_kv_tiles<DP, BK>(), *const Vs = Ks + BK * LW;
 
-    const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, grp = lane >> 4, w = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, grp = lane >> 4;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // in a scalar register: wave-uniform branches stay scalar
     const int RB = NW / a.HW;
     const int per_tile = a.n_head_blocks * a.B;
     const int rem = (int)blockIdx.x % per_tile;
@@ -266,11 +303,18 @@ __device__ __forceinline__ void bwd_dq_lse_tile(const BwdArgs &a, const int tile
     constexpr int NPF = 2 * BK * CPR / NTH;
     static_assert((2 * BK * CPR) % NTH == 0, "prefetch split");
     f4 pf[NPF];
-    auto fetch = [&](int k0) {
-#pragma unroll
-        for (int n = 0; n < NPF; ++n) {
-            const int e = tid + n * NTH;
-            const int arr = e / (BK * CPR), r = (e / CPR) % BK, c = (e % CPR) * 4;
+    // VEC (dim % 4 == 0, 16-byte aligned rows): every load unconditional and
+    // in bounds, so the pieces go out between the score products -- keys past
+    // T load key T - 1 (masked, P = 0) and columns past dim the row's last
+    // chunk (met by Q's and dO's zero columns, or landing in dq columns never
+    // stored).  Otherwise guarded loads, all at the top of the tile.
+    auto fetch_piece = [&](int n, int k0) {
+        const int e = tid + n * NTH;
+        const int arr = e / (BK * CPR), r = (e / CPR) % BK, c = (e % CPR) * 4;
+        if constexpr (VEC) {
+            pf[n] = *reinterpret_cast<const f4 *>((arr ? vb : kb) + (size_t)k0 * kld +
+                                                  (min(r, a.T - 1 - k0) * (int)kld + min(c, a.dim - 4)));
+        } else {
             const int key = k0 + r;
             const float *src = (arr ? vb : kb) + (size_t)key * kld + c;
             f4 x = zero4();
@@ -289,10 +333,21 @@ __device__ __forceinline__ void bwd_dq_lse_tile(const BwdArgs &a, const int tile
             pf[n] = x;
         }
     };
+    auto fetch = [&](int k0) {
+#pragma unroll
+        for (int n = 0; n < NPF; ++n) fetch_piece(n, k0);
+    };
+    // Pieces of group i of NI between the score products (VEC, up to d = 192).
+    auto fetch_group = [&](int i, int ni, int k0) {
+#pragma unroll
+        for (int n = i * NPF / ni; n < (i + 1) * NPF / ni; ++n) fetch_piece(n, k0);
+    };
     fetch(0);
 
+    constexpr bool ILV = VEC && DP <= 192;  // interleaved prefetch, as in bwd_dq_tile
     for (int k0 = 0; k0 < kend_wg; k0 += BK) {
         __syncthreads();
+        const int kn = k0 + BK < kend_wg ? k0 + BK : k0;  // the last tile fetches itself again, unused
 #pragma unroll
         for (int n = 0; n < NPF; ++n) {
             const int e = tid + n * NTH;
@@ -300,8 +355,13 @@ __device__ __forceinline__ void bwd_dq_lse_tile(const BwdArgs &a, const int tile
             *reinterpret_cast<f4 *>((arr ? Vs : Ks) + r * LW + c) = pf[n];
         }
         __syncthreads();
-        if (k0 + BK < kend_wg) fetch(k0 + BK);
-        if (k0 >= kend_w) continue;
+        if constexpr (!ILV) {
+            if (k0 + BK < kend_wg) fetch(k0 + BK);
+        }
+        if (k0 >= kend_w) {  // wave-uniform: nothing here is visible to this wave
+            if constexpr (ILV) fetch(kn);
+            continue;
+        }
 
         f4 s[NJ], dp[NJ];
 #pragma unroll
@@ -322,9 +382,11 @@ __device__ __forceinline__ void bwd_dq_lse_tile(const BwdArgs &a, const int tile
         };
         if constexpr (DP <= 192) {
 #pragma unroll
-            for (int kk = 0; kk < DQ; kk += 4)
+            for (int kk = 0; kk < DQ; kk += 4) {
 #pragma unroll
                 for (int j = 0; j < NJ; ++j) score_step(j, kk);
+                if constexpr (ILV) fetch_group(kk / 4, DQ / 4, kn);
+            }
         } else {
 #pragma unroll
             for (int j = 0; j < NJ; ++j)
@@ -889,23 +951,39 @@ __device__ __forceinline__ void bwd_dkdv_dma_tile(const BwdArgs &a, const int kt
 // a.pair a workgroup also takes the partner tile at the other end (p with
 // n - 1 - p), so every workgroup has the same causal work and those resident
 // together end together.
-template <int DP, int BK, int NW, bool PF = false>
-__device__ __forceinline__ void bwd_dq_body(const BwdArgs &a) {
+template <int DP, int BK, int NW, bool PF = false, bool VEC = false>
+__device__ __forceinline__ void bwd_dq_pair(const BwdArgs &a) {
     const int p = (int)blockIdx.x / (a.n_head_blocks * a.B), n = a.n_row_tiles;
-    bwd_dq_tile<DP, BK, NW, PF>(a, n - 1 - p);
+    bwd_dq_tile<DP, BK, NW, PF, VEC>(a, n - 1 - p);
     if (a.pair && p < n - 1 - p) {  // workgroup-uniform
         __syncthreads();  // the first tile's last LDS reads before the second's writes
-        bwd_dq_tile<DP, BK, NW, PF>(a, p);
+        bwd_dq_tile<DP, BK, NW, PF, VEC>(a, p);
+    }
+}
+// The prefetching kernels take 16-byte row chunks unconditionally when dim %
+// 4 == 0 (rows the library requires 16-byte aligned), guarded loads otherwise.
+template <int DP, int BK, int NW, bool PF = false>
+__device__ __forceinline__ void bwd_dq_body(const BwdArgs &a) {
+    if constexpr (PF) {
+        if ((a.dim & 3) == 0) bwd_dq_pair<DP, BK, NW, true, true>(a);
+        else bwd_dq_pair<DP, BK, NW, true, false>(a);
+    } else {
+        bwd_dq_pair<DP, BK, NW, false, false>(a);
+    }
+}
+template <int DP, int BK, int NW, bool VEC>
+__device__ __forceinline__ void bwd_dq_lse_pair(const BwdArgs &a) {
+    const int p = (int)blockIdx.x / (a.n_head_blocks * a.B), n = a.n_row_tiles;
+    bwd_dq_lse_tile<DP, BK, NW, VEC>(a, n - 1 - p);
+    if (a.pair && p < n - 1 - p) {
+        __syncthreads();
+        bwd_dq_lse_tile<DP, BK, NW, VEC>(a, p);
     }
 }
 template <int DP, int BK, int NW>
 __device__ __forceinline__ void bwd_dq_lse_body(const BwdArgs &a) {
-    const int p = (int)blockIdx.x / (a.n_head_blocks * a.B), n = a.n_row_tiles;
-    bwd_dq_lse_tile<DP, BK, NW>(a, n - 1 - p);
-    if (a.pair && p < n - 1 - p) {
-        __syncthreads();
-        bwd_dq_lse_tile<DP, BK, NW>(a, p);
-    }
+    if ((a.dim & 3) == 0) bwd_dq_lse_pair<DP, BK, NW, true>(a);
+    else bwd_dq_lse_pair<DP, BK, NW, false>(a);
 }
 template <int DP, int HS, int KW, bool PF = false, int NU = 1, bool SIN = false>
 __device__ __forceinline__ void bwd_dkdv_body(const BwdArgs &a) {

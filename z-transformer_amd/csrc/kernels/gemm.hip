@@ -200,12 +200,18 @@ DEVI void gemm_body(const GemmArgs &g) {
 // index-contiguous orientation of A, so slabs are staged with 16-byte loads and
 // stores; tiles above the diagonal (never written) and rows past T read as 0.
 // Grid: row-tile pairs, then (sequence, head), then column tiles.
+// The dS and K slabs: one allocation per tile size, shared by the aligned and
+// unaligned instantiations.
+template <int BT>
+DEVI float *dq_ds_slabs() {
+    __shared__ __attribute__((aligned(16))) float slabs[2 * BK * Tile<BT>::LIC];
+    return slabs;
+}
 template <int BT, bool VEC>
 DEVI void dq_ds_tile(const DqDsArgs &g, const int tm, const int tn, const int bh) {
     using TL = Tile<BT>;
     constexpr int TW = TL::TW, NCH = TL::NCH;
-    __shared__ __attribute__((aligned(16))) float As[BK * TL::LIC];
-    __shared__ __attribute__((aligned(16))) float Bs[BK * TL::LIC];
+    float *const As = dq_ds_slabs<BT>(), *const Bs = As + BK * TL::LIC;
     const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, grp = lane >> 4;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = TL::WT * (w >> 1), wn = TL::WT * (w & 1);
