@@ -429,11 +429,15 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
     constexpr int LW = DP + 4, DQ = DP / 4, NT = DP / 16, NTH = 64 * KW * HS;
     constexpr int BQ = 16 * NU;  // query rows per stage: NU sub-tiles of 16
     // Per head-split part: Q rows, dO rows, and (m2, 1/l, delta) per row.
-    // One buffer: the staging tiles, reused at the end for the head-split sum
-    // ((HS-1) parts x KW blocks x 64 lanes x 2*NT float4).
+    // With the register prefetch (PF) two such stage buffers: stage s reads one
+    // while the prefetched rows of stage s + 1 are written to the other at its
+    // end, one barrier per stage (C3, scores read: 1.83 -> 1.80 ms; forming S
+    // again: 2.30 -> 2.23 ms).  The buffer is reused at the end for the
+    // head-split sum ((HS-1) parts x KW blocks x 64 lanes x 2*NT float4).
     constexpr int STAGE_F = 2 * HS * BQ * LW + HS * BQ * 4;
     constexpr int RED_F = (HS - 1) * KW * 64 * 2 * NT * 4;
-    __shared__ float smem[STAGE_F > RED_F ? STAGE_F : RED_F];
+    constexpr int BUF_F = PF ? 2 * STAGE_F : STAGE_F;
+    __shared__ float smem[BUF_F > RED_F ? BUF_F : RED_F];
     float *Qs = smem, *Ds = smem + HS * BQ * LW, *St = smem + 2 * HS * BQ * LW;
 
     const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, grp = lane >> 4;
@@ -530,18 +534,18 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
 #pragma unroll
         for (int n = 0; n < NPF; ++n) fetch_piece(n, stg);
     };
-    auto put = [&]() {
+    auto put = [&](int off) {
 #pragma unroll
         for (int n = 0; n < NPF; ++n) {
             const int e = tid + n * NTH;
             const int part = e / (2 * BQ * CPR), arr = (e / (BQ * CPR)) & 1;
             const int r = (e / CPR) % BQ, c = (e % CPR) * 4;
-            *reinterpret_cast<f4 *>((arr ? Ds : Qs) + (part * BQ + r) * LW + c) = pf[n];
+            *reinterpret_cast<f4 *>((arr ? Ds : Qs) + off + (part * BQ + r) * LW + c) = pf[n];
         }
         if (tid < HS * BQ) {  // rows past T: m2 = 0, 1/l = 0, delta = 0
-            St[tid * 4 + 0] = prow ? pm2 * kLog2e : 0.f;
-            St[tid * 4 + 1] = prow ? (a.lse ? 1.f : 1.f / pil) : 0.f;
-            St[tid * 4 + 2] = prow ? pde : 0.f;
+            St[off + tid * 4 + 0] = prow ? pm2 * kLog2e : 0.f;
+            St[off + tid * 4 + 1] = prow ? (a.lse ? 1.f : 1.f / pil) : 0.f;
+            St[off + tid * 4 + 2] = prow ? pde : 0.f;
         }
     };
     if constexpr (PF) fetch(0);
@@ -679,16 +683,20 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
         }
     };
 
-    for (int stg = 0; stg < n_stage; ++stg) {
+    if constexpr (PF) {
+        put(0);
         __syncthreads();
+    }
+    for (int stg = 0; stg < n_stage; ++stg) {
         if constexpr (PF) {
-            put();
-            __syncthreads();
+            const int off = (stg & 1) * STAGE_F;
+            qs = Qs + off + hs * BQ * LW; ds = Ds + off + hs * BQ * LW; st = St + off + hs * BQ * 4;
             if constexpr (SIN) {
 #pragma unroll
                 for (int u = 0; u < NU; ++u) sc[u] = sn[u];
             }
         } else {
+            __syncthreads();
             const int hi = stg % hpp, t0 = tile_row(stg);
             // Stage Q, dO rows [t0, t0+16) for every part's head.
             const int nvalid = min(BQ, a.T - t0);
@@ -715,6 +723,10 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
             __syncthreads();
         }
         work(stg, min(stg + 1, n_stage - 1));  // the last stage fetches its own rows again, unused
+        if constexpr (PF) {
+            if (stg + 1 < n_stage) put(((stg + 1) & 1) * STAGE_F);
+            __syncthreads();
+        }
     }
 
     // Sum the head-split partials in a fixed order (part 0 + 1 + ...).

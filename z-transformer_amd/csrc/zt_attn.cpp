@@ -11,6 +11,7 @@
 // the reason on stderr.
 #include <hip/hip_runtime_api.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
@@ -180,9 +181,10 @@ int dq_waves(int dp) {
     const int w = env_choice("ZT_ATTN_DQ_W", 4, {4, 8});
     return dp > 192 ? 4 : w;  // eight-wave dq spills above d = 192
 }
-size_t dkdv_bytes(int dp, int hs, int kw = 0, int rows = 16) {
+// bufs: stage buffers (2 in the register-prefetching kernels).
+size_t dkdv_bytes(int dp, int hs, int kw = 0, int rows = 16, int bufs = 1) {
     if (kw == 0) kw = 4 / hs;
-    const size_t stage = (size_t)2 * hs * rows * (dp + 4) + (size_t)hs * rows * 4;
+    const size_t stage = ((size_t)2 * hs * rows * (dp + 4) + (size_t)hs * rows * 4) * bufs;
     const size_t red = (size_t)(hs - 1) * kw * 64 * 2 * (dp / 16) * 4;
     return (stage > red ? stage : red) * sizeof(float);
 }
@@ -415,7 +417,8 @@ int backward_prepare(const float *q, const float *k, const float *v, const float
         snprintf(name_dq, 64, nw_dq == 8 ? "zt_bwd_dq8_d%d_k%d" : "zt_bwd_dq_d%d_k%d", dp, bk);
     *threads_dq = 64u * nw_dq;
     // The prefetching kernel loads whole 16-byte chunks unconditionally.
-    const bool pf = dim % 4 == 0 && aligned && env_choice("ZT_ATTN_PF", 1, {0, 1}) == 1;
+    const bool pf = dim % 4 == 0 && aligned && dkdv_bytes(dp, 2, 4, 16, 2) <= st->lds_limit &&
+                    env_choice("ZT_ATTN_PF", 1, {0, 1}) == 1;
     if (wide)
         snprintf(name_dkdv, 64, pf ? "zt_bwd_dkdv8p_d%d_hs2" : "zt_bwd_dkdv8_d%d_hs2", dp);
     else
@@ -504,6 +507,7 @@ size_t zt_attn_bwd_dkdv_shmem(int dim) {
     if (!zt_attn_dim_ok(dim)) return 0;
     const int dp = pad32(dim);
     size_t most = dkdv_bytes(dp, dp <= 128 ? 4 : 2);
+    if (dp <= 128) most = std::max(most, dkdv_bytes(dp, 2, 4, 32, 2));  // eight waves, two 32-row stage buffers
     for (int hs : {1, 2, 4})
         if (!(hs == 4 && dp > 128) && dkdv_dma_bytes(dp, hs) > most) most = dkdv_dma_bytes(dp, hs);
     return most;
@@ -604,7 +608,7 @@ size_t zt_attn_backward_train_workspace(int B, int T, int n_heads, int n_kv_head
 static bool scores_path(int dim, int n_heads, int n_kv_heads, size_t lds_limit) {
     const int dp = pad32(dim);
     if (n_kv_heads <= 0 || (n_heads / n_kv_heads) % 2 != 0 || dim % 4 != 0) return false;
-    return dp <= 128 ? dkdv_bytes(dp, 2, 4, 32) <= lds_limit : dim == dp && dkdv_dma_bytes(dp, 2) <= lds_limit;
+    return dp <= 128 ? dkdv_bytes(dp, 2, 4, 32, 2) <= lds_limit : dim == dp && dkdv_dma_bytes(dp, 2) <= lds_limit;
 }
 
 static float *ws_tiles(void *workspace, int B, int T, int n_heads) {
