@@ -580,7 +580,12 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
 #pragma unroll
         for (int u = 0; u < NU; ++u) { s[u] = zero4(); dp[u] = zero4(); }
         if constexpr (SIN) {
-            // Scores from the forward; dP alone as two interleaved chains.
+            // Scores from the forward; dP alone as two interleaved chains.  The
+            // two waves of a SIMD (head halves 0 and 1) run in step and the
+            // hardware favours the first, whose dV/dK products then starve the
+            // second's softmax; the second goes first through dP instead
+            // (C3: 1.80 -> 1.78 ms; the kernel that forms S again loses with it).
+            if (hs == 1) __builtin_amdgcn_s_setprio(2);
             f4 dp2[NU];
 #pragma unroll
             for (int u = 0; u < NU; ++u) { s[u] = sc[u]; dp2[u] = zero4(); }
@@ -608,6 +613,7 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
             }
 #pragma unroll
             for (int u = 0; u < NU; ++u) dp[u] += dp2[u];
+            __builtin_amdgcn_s_setprio(0);
         } else {
 #pragma unroll
             for (int kk = 0; kk < DQ; kk += 4) {
