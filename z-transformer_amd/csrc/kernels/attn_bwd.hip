@@ -256,7 +256,6 @@ __device__ __forceinline__ void bwd_dq_tile(const BwdArgs &a, const int tile) {
 template <int DP, int BK, int NW, bool VEC = false>
 __device__ __forceinline__ void bwd_dq_lse_tile(const BwdArgs &a, const int tile) {
     constexpr int LW = DP + 4, DQ = DP / 4, NT = DP / 16, NJ = BK / 16, NTH = 64 * NW, CPR = DP / 4;
-    constexpr bool PF = true;
     float *const Ks = dq_kv_tiles<DP, BK>(), *const Vs = Ks + BK * LW;
 
     const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, grp = lane >> 4;
@@ -961,7 +960,8 @@ __device__ __forceinline__ void bwd_dkdv_dma_tile(const BwdArgs &a, const int kt
     }
 }
 
-// Up to d = 192 the dq kernel fits two waves per SIMD without spilling when
+// Up to d = 192 (d = 128 with 64-key tiles, whose LDS holds one workgroup per
+// CU above it) the dq kernel fits two waves per SIMD without spilling when
 // asked to (four accumulator/operand sets of DP/4 registers each); above that
 // it keeps one.
 // Grid order and pairing.  Row tiles (dq kernels) run latest first and key
@@ -1023,7 +1023,7 @@ __device__ __forceinline__ void bwd_dkdv_dma_body(const BwdArgs &a) {
 }
 
 #define ZT_BWD_DQ(DP, BK)                                                                          \
-    extern "C" __global__ void __launch_bounds__(256, (DP) <= 192 ? 2 : 1)                        \
+    extern "C" __global__ void __launch_bounds__(256, (DP) <= ((BK) == 32 ? 192 : 128) ? 2 : 1)  \
         zt_bwd_dq_d##DP##_k##BK(BwdArgs a) {                                                       \
         bwd_dq_body<DP, BK, 4>(a);                                                                 \
     }                                                                                              \
