@@ -873,10 +873,15 @@ __device__ __forceinline__ void bwd_dkdv_dma_tile(const BwdArgs &a, const int kt
                 // Scores from the forward; dP alone as two interleaved chains.
                 f4 dp2 = zero4();
                 s = sc;
+                // One wave per SIMD here: each group's dO operand is read one
+                // group ahead, so no product waits for its LDS read.
+                f4 dxn = *reinterpret_cast<const f4 *>(ds + l16 * DP + 4 * swz<CPR>((grp * DQ) >> 2, l16));
 #pragma unroll
                 for (int kk = 0; kk < DQ; kk += 4) {
-                    const int off = l16 * DP + 4 * swz<CPR>((grp * DQ + kk) >> 2, l16);
-                    const f4 dx = *reinterpret_cast<const f4 *>(ds + off);
+                    const f4 dx = dxn;
+                    if (kk + 4 < DQ)
+                        dxn = *reinterpret_cast<const f4 *>(ds + l16 * DP + 4 * swz<CPR>((grp * DQ + kk + 4) >> 2, l16));
+                    __builtin_amdgcn_sched_barrier(0);
                     dp = mfma16(dx.x, vr[kk + 0], dp);
                     dp2 = mfma16(dx.y, vr[kk + 1], dp2);
                     dp = mfma16(dx.z, vr[kk + 2], dp);
@@ -884,11 +889,17 @@ __device__ __forceinline__ void bwd_dkdv_dma_tile(const BwdArgs &a, const int kt
                 }
                 dp += dp2;
             } else {
+                f4 qxn = *reinterpret_cast<const f4 *>(qs + l16 * DP + 4 * swz<CPR>((grp * DQ) >> 2, l16));
+                f4 dxn = *reinterpret_cast<const f4 *>(ds + l16 * DP + 4 * swz<CPR>((grp * DQ) >> 2, l16));
 #pragma unroll
                 for (int kk = 0; kk < DQ; kk += 4) {
-                    const int off = l16 * DP + 4 * swz<CPR>((grp * DQ + kk) >> 2, l16);
-                    const f4 qx = *reinterpret_cast<const f4 *>(qs + off);
-                    const f4 dx = *reinterpret_cast<const f4 *>(ds + off);
+                    const f4 qx = qxn, dx = dxn;
+                    if (kk + 4 < DQ) {
+                        const int off = l16 * DP + 4 * swz<CPR>((grp * DQ + kk + 4) >> 2, l16);
+                        qxn = *reinterpret_cast<const f4 *>(qs + off);
+                        dxn = *reinterpret_cast<const f4 *>(ds + off);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
                     s = mfma16(qx.x, kr[kk + 0], s);
                     dp = mfma16(dx.x, vr[kk + 0], dp);
                     s = mfma16(qx.y, kr[kk + 1], s);
@@ -914,13 +925,21 @@ __device__ __forceinline__ void bwd_dkdv_dma_tile(const BwdArgs &a, const int kt
                 const size_t tile = (((size_t)b * a.H + hh) * nt + (t0 >> 4)) * nt + (s0 >> 4);
                 __builtin_nontemporal_store(dsv, reinterpret_cast<f4 *>(a.ds_out + tile * 256) + lane);
             }
+            // dO^T, Q^T rows in the row-owner layout, read one row ahead.
+            float dxn[NT], qxn[NT];
+            lds_run_swz<NT, CPR>(dxn, ds, 4 * grp, l16);
+            lds_run_swz<NT, CPR>(qxn, qs, 4 * grp, l16);
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk) {
-                const int tr = 4 * grp + kk;
                 const float pv = p[kk], dv = dsv[kk];
-                float dx[NT], qx[NT];  // dO^T, Q^T rows in the row-owner layout
-                lds_run_swz<NT, CPR>(dx, ds, tr, l16);
-                lds_run_swz<NT, CPR>(qx, qs, tr, l16);
+                float dx[NT], qx[NT];
+#pragma unroll
+                for (int i = 0; i < NT; ++i) { dx[i] = dxn[i]; qx[i] = qxn[i]; }
+                if (kk + 1 < 4) {
+                    lds_run_swz<NT, CPR>(dxn, ds, 4 * grp + kk + 1, l16);
+                    lds_run_swz<NT, CPR>(qxn, qs, 4 * grp + kk + 1, l16);
+                }
+                __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int i = 0; i < NT; ++i) {
                     dva[i] = mfma16(dx[i], pv, dva[i]);
