@@ -155,7 +155,7 @@ def test_train_ws_stages_and_repeats(gpu, zt):
 
 
 @pytest.mark.parametrize("B,T,H,Hkv,D", [(2, 130, 8, 2, 64), (1, 333, 8, 2, 128), (1, 45, 4, 2, 66),
-                                         (2, 77, 8, 2, 256), (1, 100, 4, 2, 160)])
+                                         (2, 77, 8, 2, 256), (1, 100, 4, 2, 160), (1, 90, 8, 2, 192)])
 def test_train_scores_stages_and_repeats(gpu, zt, B, T, H, Hkv, D):
     """The forward that keeps its scores gives the same out and lse bit for bit;
     the backward that reads them back repeats bit for bit, its stages equal the
@@ -185,12 +185,31 @@ def test_train_scores_stages_and_repeats(gpu, zt, B, T, H, Hkv, D):
 def test_train_scores_plan_names_the_score_reading_kernel(gpu, zt):
     assert zt.plan_train(1, 4096, 32, 8, 128) == ("zt_fwd8ps_d128_k32", "zt_gemm_dqds_128", "zt_bwd_dkdv8s_d128_hs2")
     assert "dkdv8s" not in zt.plan_train(1, 256, 8, 8, 128)[2]   # MHA: no score-reading kernel
-    assert zt.plan_train(1, 256, 8, 2, 256)[2] == "zt_bwd_dkdv_dmas_d256_hs2"   # wide heads: staged asynchronously
+    assert zt.plan_train(1, 256, 8, 2, 256)[2] == "zt_bwd_dkdv8sd_d256_hs2"   # wide heads: columns split
+    assert zt.plan_train(1, 256, 8, 2, 192)[2] == "zt_bwd_dkdv8sd_d192_hs2"
+    assert zt.plan_train(1, 256, 8, 2, 160)[2] == "zt_bwd_dkdv_dmas_d160_hs2"   # halves not whole 32 columns
     assert "dmas" not in zt.plan_train(1, 256, 8, 2, 250)[2]   # rows not whole 32-float chunks: no scores
 
 
+@pytest.mark.parametrize("B,T,H,Hkv,D", [(2, 77, 8, 2, 256), (1, 90, 8, 2, 192)])
+def test_train_scores_wide_kernels_agree(gpu, zt, oracle, monkeypatch, B, T, H, Hkv, D):
+    """The column-split kernel and the asynchronously staged one (ZT_ATTN_DSPLIT=0)
+    give the same dS, dq, dk and dv to rounding, and both hold the oracle's gate."""
+    q, k, v, do = _inputs(gpu, zt, B, T, H, Hkv, D)
+    monkeypatch.setenv("ZT_ATTN_DSPLIT", "1")
+    assert "dkdv8sd" in zt.plan_train(B, T, H, Hkv, D)[2]
+    a = _train(gpu, zt, q, k, v, do, B, T, H, Hkv, D, ws="scores")
+    monkeypatch.setenv("ZT_ATTN_DSPLIT", "0")
+    assert "dkdv_dmas" in zt.plan_train(B, T, H, Hkv, D)[2]
+    b = _train(gpu, zt, q, k, v, do, B, T, H, Hkv, D, ws="scores")
+    for x, y in zip(a[2:5], b[2:5]):
+        assert rel_err(x, y) <= 1e-5
+    rq, rk, rv = oracle.attention_backward(*(host(x) for x in (q, k, v, do)), B, T, H, Hkv, D)
+    assert max(rel_err(a[2], rq), rel_err(a[3], rk), rel_err(a[4], rv)) <= BWD_REL
+
+
 @pytest.mark.parametrize("B,T,H,Hkv,D", [(1, 100, 8, 2, 80), (2, 45, 4, 2, 32), (1, 333, 8, 2, 128),
-                                         (1, 70, 8, 2, 256)])
+                                         (1, 70, 8, 2, 256), (1, 61, 8, 2, 192)])
 def test_train_scores_write_nothing_past_the_workspace(gpu, zt, oracle, B, T, H, Hkv, D):
     """Ragged T: the score-reading dk/dv kernel stages 32 rows, so a stage can
     end past the last row; no score or dS tile may be written outside the

@@ -422,10 +422,17 @@ __device__ __forceinline__ void bwd_dq_lse_tile(const BwdArgs &a, const int tile
     }
 }
 
-template <int DP, int HS, int KW, bool PF = false, int NU = 1, bool SIN = false>
+// DS = 2 (d-split, score-reading kernel for wide heads): a wave keeps half of
+// the head's columns -- its half of V and of the dK/dV accumulators -- so two
+// waves fit per SIMD; the partner wave holding the other half (w ^ KW*HS)
+// shares the partial dP through LDS, both form dP = own + partner (f32
+// addition commutes: the two copies are identical) and the same P and dS.
+template <int DP, int HS, int KW, bool PF = false, int NU = 1, bool SIN = false, int DS = 1>
 __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile, const bool up) {
     static_assert(!SIN || PF, "the scores are prefetched with the stage's rows");
-    constexpr int LW = DP + 4, DQ = DP / 4, NT = DP / 16, NTH = 64 * KW * HS;
+    static_assert(DS == 1 || (SIN && DS == 2 && (DP / 32) % 2 == 0), "d-split: score-reading, whole 32-column halves");
+    constexpr int LW = DP + 4, DQ = DP / 4, NT = DP / 16, NTH = 64 * KW * HS * DS;
+    constexpr int DPW = DP / DS, DQW = DPW / 4, NTW = DPW / 16;  // a wave's columns
     constexpr int BQ = 16 * NU;  // query rows per stage: NU sub-tiles of 16
     // Per head-split part: Q rows, dO rows, and (m2, 1/l, delta) per row.
     // With the register prefetch (PF) two such stage buffers: stage s reads one
@@ -434,14 +441,16 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
     // again: 2.30 -> 2.23 ms).  The buffer is reused at the end for the
     // head-split sum ((HS-1) parts x KW blocks x 64 lanes x 2*NT float4).
     constexpr int STAGE_F = 2 * HS * BQ * LW + HS * BQ * 4;
-    constexpr int RED_F = (HS - 1) * KW * 64 * 2 * NT * 4;
+    constexpr int RED_F = (HS - 1) * KW * DS * 64 * 2 * NTW * 4;
     constexpr int BUF_F = PF ? 2 * STAGE_F : STAGE_F;
-    __shared__ float smem[BUF_F > RED_F ? BUF_F : RED_F];
+    constexpr int MAIN_F = BUF_F > RED_F ? BUF_F : RED_F;
+    constexpr int XCH_F = DS > 1 ? KW * HS * DS * NU * 64 * 4 : 0;  // partial dP exchange (d-split)
+    __shared__ float smem[MAIN_F + XCH_F];
     float *Qs = smem, *Ds = smem + HS * BQ * LW, *St = smem + 2 * HS * BQ * LW;
 
     const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, grp = lane >> 4;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // in a scalar register: wave-uniform branches stay scalar
-    const int kbw = w % KW, hs = w / KW;
+    const int kbw = w % KW, hs = (w / KW) % HS, dh = w / (KW * HS);  // dh: the wave's column half (DS = 2)
     const int per_tile = a.Hkv * a.B;
     const int rem = (int)blockIdx.x % per_tile;
     const int kvh = rem % a.Hkv, b = rem / a.Hkv;
@@ -455,14 +464,15 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
 
     const int my_key = s0 + l16;
     const bool key_ok = my_key < a.T;
-    float kr[SIN ? 1 : DQ], vr[DQ];  // with the forward's scores K is not needed
+    float kr[SIN ? 1 : DQ], vr[DQW];  // with the forward's scores K is not needed
     if constexpr (!SIN)
         load_row_seg<DQ>(kr, a.k + kvoff + (size_t)my_key * kld, grp * DQ, a.dim, vec4, key_ok, a.scale_log2e);
-    load_row_seg<DQ>(vr, a.v + kvoff + (size_t)my_key * kld, grp * DQ, a.dim, vec4, key_ok, 1.f);
+    load_row_seg<DQW>(vr, a.v + kvoff + (size_t)my_key * kld + dh * DPW, grp * DQW, a.dim - dh * DPW, vec4, key_ok,
+                      1.f);
 
-    f4 dka[NT], dva[NT];
+    f4 dka[NTW], dva[NTW];
 #pragma unroll
-    for (int i = 0; i < NT; ++i) { dka[i] = zero4(); dva[i] = zero4(); }
+    for (int i = 0; i < NTW; ++i) { dka[i] = zero4(); dva[i] = zero4(); }
 
     // Stages: (row tile t0 of the suffix t >= wg_s0, head of each part hi),
     // heads inner.  A workgroup's first key tile walks the rows from the last
@@ -556,10 +566,11 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
         const int hi = stg % hpp, t0 = tile_row(stg);
         if (t0 + BQ - 1 < s0 || s0 >= a.T) {  // wave-uniform: no visible pair
             if constexpr (PF) fetch(nx);
+            if constexpr (DS > 1) __syncthreads();  // the partial-dP exchange's barrier, met by every wave
             return;
         }
         // The prefetch pieces go out between the first products' groups.
-        constexpr int NI = DQ / 4;
+        constexpr int NI = DQW / 4;
         auto fetch_after = [&](int i) {
             if constexpr (PF) {
                 if (i == 0) fetch_aux(nx);
@@ -584,21 +595,22 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
             // hardware favours the first, whose dV/dK products then starve the
             // second's softmax; the second goes first through dP instead
             // (C3: 1.80 -> 1.78 ms; the kernel that forms S again loses with it).
-            if (hs == 1) __builtin_amdgcn_s_setprio(2);
+            if (DS == 1 && hs == 1) __builtin_amdgcn_s_setprio(2);
             f4 dp2[NU];
 #pragma unroll
             for (int u = 0; u < NU; ++u) { s[u] = sc[u]; dp2[u] = zero4(); }
             // dO operands read one group ahead of their products.
+            const float *dsw = ds + dh * DPW + grp * DQW;
             f4 dxn[NU];
 #pragma unroll
-            for (int u = 0; u < NU; ++u) dxn[u] = *reinterpret_cast<const f4 *>(ds + (16 * u + l16) * LW + grp * DQ);
+            for (int u = 0; u < NU; ++u) dxn[u] = *reinterpret_cast<const f4 *>(dsw + (16 * u + l16) * LW);
 #pragma unroll
-            for (int kk = 0; kk < DQ; kk += 4) {
+            for (int kk = 0; kk < DQW; kk += 4) {
                 f4 dx[NU];
 #pragma unroll
                 for (int u = 0; u < NU; ++u) {
                     dx[u] = dxn[u];
-                    if (kk + 4 < DQ) dxn[u] = *reinterpret_cast<const f4 *>(ds + (16 * u + l16) * LW + grp * DQ + kk + 4);
+                    if (kk + 4 < DQW) dxn[u] = *reinterpret_cast<const f4 *>(dsw + (16 * u + l16) * LW + kk + 4);
                 }
                 __builtin_amdgcn_sched_barrier(0);  // keeps the reads ahead of this group's products
 #pragma unroll
@@ -613,6 +625,15 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
 #pragma unroll
             for (int u = 0; u < NU; ++u) dp[u] += dp2[u];
             __builtin_amdgcn_s_setprio(0);
+            if constexpr (DS > 1) {
+                float *xch = smem + MAIN_F;
+#pragma unroll
+                for (int u = 0; u < NU; ++u) reinterpret_cast<f4 *>(xch)[(w * NU + u) * 64 + lane] = dp[u];
+                __syncthreads();
+                const int pw = w ^ (KW * HS);
+#pragma unroll
+                for (int u = 0; u < NU; ++u) dp[u] += reinterpret_cast<const f4 *>(xch)[(pw * NU + u) * 64 + lane];
+            }
         } else {
 #pragma unroll
             for (int kk = 0; kk < DQ; kk += 4) {
@@ -660,7 +681,7 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
         // dS for a dq product outside this kernel, one 16 x 16 tile per (u) in lane
         // order; nontemporal, so the 1 GB stream does not evict the Q/dO rows
         // the other workgroups are about to reread.
-        if (a.ds_out) {
+        if (a.ds_out && dh == 0) {  // d-split: the partners hold the same dS; one stores it
             const int hh = kvh * group + hs * hpp + hi;
             const int nt = (a.T + 15) >> 4;
 #pragma unroll
@@ -675,12 +696,12 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
             if (t0 + 16 * u + 15 < s0) continue;  // wave-uniform: this sub-tile is wholly masked
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk) {
-                float dx[NT], qx[NT];  // dO^T, Q^T rows in the row-owner layout
-                lds_run<NT>(dx, ds + (16 * u + 4 * grp + kk) * LW, l16);
-                lds_run<NT>(qx, qs + (16 * u + 4 * grp + kk) * LW, l16);
+                float dx[NTW], qx[NTW];  // dO^T, Q^T rows in the row-owner layout (the wave's columns)
+                lds_run<NTW>(dx, ds + (16 * u + 4 * grp + kk) * LW + dh * DPW, l16);
+                lds_run<NTW>(qx, qs + (16 * u + 4 * grp + kk) * LW + dh * DPW, l16);
                 const float pv = p[u][kk], dv = dsv[u][kk];
 #pragma unroll
-                for (int i = 0; i < NT; ++i) {
+                for (int i = 0; i < NTW; ++i) {
                     dva[i] = mfma16(dx[i], pv, dva[i]);
                     dka[i] = mfma16(qx[i], dv, dka[i]);
                 }
@@ -736,29 +757,30 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
 
     // Sum the head-split partials in a fixed order (part 0 + 1 + ...).
     if constexpr (HS > 1) {
-        float *red = smem;  // (HS-1) parts x KW blocks x 64 lanes x 2*NT f4
+        float *red = smem;  // (HS-1) parts x DS halves x KW blocks x 64 lanes x 2*NTW f4
         __syncthreads();
         if (hs > 0) {
-            f4 *dst = reinterpret_cast<f4 *>(red) + (((hs - 1) * KW + kbw) * 64 + lane) * 2 * NT;
+            f4 *dst = reinterpret_cast<f4 *>(red) + ((((hs - 1) * DS + dh) * KW + kbw) * 64 + lane) * 2 * NTW;
 #pragma unroll
-            for (int i = 0; i < NT; ++i) { dst[i] = dka[i]; dst[NT + i] = dva[i]; }
+            for (int i = 0; i < NTW; ++i) { dst[i] = dka[i]; dst[NTW + i] = dva[i]; }
         }
         __syncthreads();
         if (hs == 0) {
             for (int part = 1; part < HS; ++part) {
-                const f4 *src = reinterpret_cast<const f4 *>(red) + (((part - 1) * KW + kbw) * 64 + lane) * 2 * NT;
+                const f4 *src =
+                    reinterpret_cast<const f4 *>(red) + ((((part - 1) * DS + dh) * KW + kbw) * 64 + lane) * 2 * NTW;
 #pragma unroll
-                for (int i = 0; i < NT; ++i) { dka[i] += src[i]; dva[i] += src[NT + i]; }
+                for (int i = 0; i < NTW; ++i) { dka[i] += src[i]; dva[i] += src[NTW + i]; }
             }
         }
     }
     if (hs == 0 && key_ok) {
-        float *dkrow = a.dk + kvoff + (size_t)my_key * kld;
-        float *dvrow = a.dv + kvoff + (size_t)my_key * kld;
+        float *dkrow = a.dk + kvoff + (size_t)my_key * kld + dh * DPW;
+        float *dvrow = a.dv + kvoff + (size_t)my_key * kld + dh * DPW;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            store_run<NT>(dkrow, 4 * grp + r, a.dim, vec4, dka, r, a.scale);
-            store_run<NT>(dvrow, 4 * grp + r, a.dim, vec4, dva, r, 1.f);
+            store_run<NTW>(dkrow, 4 * grp + r, a.dim - dh * DPW, vec4, dka, r, a.scale);
+            store_run<NTW>(dvrow, 4 * grp + r, a.dim - dh * DPW, vec4, dva, r, 1.f);
         }
     }
 }
@@ -1022,13 +1044,13 @@ __device__ __forceinline__ void bwd_dq_lse_body(const BwdArgs &a) {
     if ((a.dim & 3) == 0) bwd_dq_lse_pair<DP, BK, NW, true>(a);
     else bwd_dq_lse_pair<DP, BK, NW, false>(a);
 }
-template <int DP, int HS, int KW, bool PF = false, int NU = 1, bool SIN = false>
+template <int DP, int HS, int KW, bool PF = false, int NU = 1, bool SIN = false, int DS = 1>
 __device__ __forceinline__ void bwd_dkdv_body(const BwdArgs &a) {
     const int p = (int)blockIdx.x / (a.Hkv * a.B), n = a.n_key_tiles;
-    bwd_dkdv_tile<DP, HS, KW, PF, NU, SIN>(a, p, false);
+    bwd_dkdv_tile<DP, HS, KW, PF, NU, SIN, DS>(a, p, false);
     if (a.pair && n - 1 - p > p) {
         __syncthreads();  // the head-split sum reads LDS; the next tile's staging writes it
-        bwd_dkdv_tile<DP, HS, KW, PF, NU, SIN>(a, n - 1 - p, true);
+        bwd_dkdv_tile<DP, HS, KW, PF, NU, SIN, DS>(a, n - 1 - p, true);
     }
 }
 template <int DP, int HS, bool SIN = false>
@@ -1116,6 +1138,15 @@ ZT_BWD_ALL(192)
 ZT_BWD_ALL(224)
 ZT_BWD_ALL(256)
 ZT_BWD_DKDV_DMAS(160) ZT_BWD_DKDV_DMAS(192) ZT_BWD_DKDV_DMAS(224) ZT_BWD_DKDV_DMAS(256)
+// Score-reading dk/dv for wide heads with the head's columns split over two
+// waves (DS = 2): eight waves (2 key blocks x 2 head halves x 2 column halves),
+// two per SIMD, 16 query rows per stage in two buffers.  Heads whose halves
+// are whole 32-column groups (d = 192, 256).
+#define ZT_BWD_DKDV8SD(DP)                                                                         \
+    extern "C" __global__ void __launch_bounds__(512) zt_bwd_dkdv8sd_d##DP##_hs2(BwdArgs a) {   \
+        bwd_dkdv_body<DP, 2, 2, true, 1, true, 2>(a);                                              \
+    }
+ZT_BWD_DKDV8SD(192) ZT_BWD_DKDV8SD(256)
 
 // delta[row] = sum_d o[row, d] * dout[row, d] over the B*T*H rows of dim
 // floats (the row statistic the dk/dv kernel needs, autograd.zig:774-797 as

@@ -190,6 +190,16 @@ size_t dkdv_bytes(int dp, int hs, int kw = 0, int rows = 16, int bufs = 1) {
 }
 // The asynchronously staged dk/dv kernel: two buffers of unpadded tiles.
 size_t dkdv_dma_bytes(int dp, int hs) { return ((size_t)2 * hs * 2 * 16 * dp + (size_t)2 * hs * 16 * 4) * sizeof(float); }
+// The column-split score-reading kernel (d = 192, 256): two 16-row stage
+// buffers for two head halves plus the partial-dP exchange of its eight waves.
+size_t dkdv_ds_bytes(int dp) { return dkdv_bytes(dp, 2, 2, 16, 2) + (size_t)8 * 64 * 4 * sizeof(float); }
+// Score-reading dk/dv kernel for heads wider than 128: the column-split
+// eight-wave kernel where the head halves are whole 32-column groups (two
+// waves per SIMD instead of one), else the four-wave asynchronously staged
+// one.  ZT_ATTN_DSPLIT=0 forces the latter.
+bool dkdv_dsplit(int dp, size_t lds_limit) {
+    return (dp == 192 || dp == 256) && dkdv_ds_bytes(dp) <= lds_limit && env_choice("ZT_ATTN_DSPLIT", 1, {0, 1}) == 1;
+}
 
 int refuse_T(int T) {
     fprintf(stderr,
@@ -508,6 +518,7 @@ size_t zt_attn_bwd_dkdv_shmem(int dim) {
     const int dp = pad32(dim);
     size_t most = dkdv_bytes(dp, dp <= 128 ? 4 : 2);
     if (dp <= 128) most = std::max(most, dkdv_bytes(dp, 2, 4, 32, 2));  // eight waves, two 32-row stage buffers
+    if (dp == 192 || dp == 256) most = std::max(most, dkdv_ds_bytes(dp));  // column-split eight waves
     for (int hs : {1, 2, 4})
         if (!(hs == 4 && dp > 128) && dkdv_dma_bytes(dp, hs) > most) most = dkdv_dma_bytes(dp, hs);
     return most;
@@ -676,17 +687,21 @@ int zt_attn_backward_train_ws(const float *q, const float *k, const float *v, co
     if (scores && scores_path(dim, n_heads, n_kv_heads, st->lds_limit) && qd_aligned) {
         // The forward left the scores in the dS tiles: a kernel that reads
         // them, 2 head halves x 64 keys (eight waves, d <= 128) or x 32 keys
-        // (four waves, asynchronous staging, wider heads) per workgroup.
-        // (Unaligned q / dout rows form Q K^T again.)
+        // (wider heads: eight waves splitting the columns, or four waves with
+        // asynchronous staging) per workgroup.  (Unaligned q / dout rows form
+        // Q K^T again.)
         a.HS = 2;
         const int keys = dp <= 128 ? 64 : 32;
+        const bool dsplit = dp > 128 && dkdv_dsplit(dp, st->lds_limit);
         a.n_key_tiles = (T + keys - 1) / keys;
         const unsigned long long blocks =
             (unsigned long long)(a.pair ? (a.n_key_tiles + 1) / 2 : a.n_key_tiles) * n_kv_heads * B;
         if (!grid_ok(blocks)) return 1;
         blocks_b = (unsigned)blocks;
-        threads_b = dp <= 128 ? 512 : 256;
-        snprintf(name_b, sizeof name_b, dp <= 128 ? "zt_bwd_dkdv8s_d%d_hs2" : "zt_bwd_dkdv_dmas_d%d_hs2", dp);
+        threads_b = dp <= 128 || dsplit ? 512 : 256;
+        snprintf(name_b, sizeof name_b,
+                 dp <= 128 ? "zt_bwd_dkdv8s_d%d_hs2" : dsplit ? "zt_bwd_dkdv8sd_d%d_hs2" : "zt_bwd_dkdv_dmas_d%d_hs2",
+                 dp);
     }
     if (stage & 1) {
         const unsigned long long rows = (unsigned long long)B * T * n_heads;
@@ -1017,7 +1032,11 @@ int zt_attn_plan_train(int B, int T, int n_heads, int n_kv_heads, int dim, char 
     snprintf(dq, len, "zt_gemm_dqds_%d", dqds_tile(B, T, n_heads, dim, st->cus));
     if (scores_path(dim, n_heads, n_kv_heads, st->lds_limit)) {
         const int dp = pad32(dim);
-        snprintf(dkdv, len, dp <= 128 ? "zt_bwd_dkdv8s_d%d_hs2" : "zt_bwd_dkdv_dmas_d%d_hs2", dp);
+        snprintf(dkdv, len,
+                 dp <= 128                        ? "zt_bwd_dkdv8s_d%d_hs2"
+                 : dkdv_dsplit(dp, st->lds_limit) ? "zt_bwd_dkdv8sd_d%d_hs2"
+                                                  : "zt_bwd_dkdv_dmas_d%d_hs2",
+                 dp);
         if (strncmp(fwd, "zt_fwd8p_d", 10) == 0 && dp <= 128) snprintf(fwd, len, "zt_fwd8ps_d%d_k32", dp);
     }
     return 0;
