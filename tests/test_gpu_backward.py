@@ -68,18 +68,27 @@ def test_backward_any_tile_cap(gpu, zt, oracle, max_tile):
     assert max(rel_err(dq, rq), rel_err(dk, rk), rel_err(dv, rv)) <= BWD_REL
 
 
+_NO_DS = {"ZT_ATTN_DSPLIT": "0"}
+
+
 @pytest.mark.parametrize("env", [
     {"ZT_ATTN_W8": "1", "ZT_ATTN_PF": "0"}, {"ZT_ATTN_W8": "1", "ZT_ATTN_PF": "1"},
-    {"ZT_ATTN_W8": "1", "ZT_ATTN_PF": "1", "ZT_ATTN_BPAIR": "0"}, {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "1", "ZT_ATTN_BPAIR": "0"},
-    {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "0"}, {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "1"},
-    {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "0", "ZT_ATTN_HS": "4"}, {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "1", "ZT_ATTN_HS": "4"},
-    {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "0", "ZT_ATTN_HS": "1"}, {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "1", "ZT_ATTN_HS": "1"},
+    {"ZT_ATTN_W8": "1", "ZT_ATTN_PF": "1", "ZT_ATTN_BPAIR": "0"},
+    {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "1", "ZT_ATTN_BPAIR": "0", **_NO_DS},
+    {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "0", **_NO_DS}, {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "1", **_NO_DS},
+    {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "0", "ZT_ATTN_HS": "4", **_NO_DS},
+    {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "1", "ZT_ATTN_HS": "4", **_NO_DS},
+    {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "0", "ZT_ATTN_HS": "1", **_NO_DS},
+    {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "1", "ZT_ATTN_HS": "1", **_NO_DS},
+    {"ZT_ATTN_DSPLIT": "1"}, {"ZT_ATTN_DSPLIT": "1", "ZT_ATTN_BPAIR": "0"},
 ])
-@pytest.mark.parametrize("B,T,H,Hkv,D", [(1, 200, 8, 2, 128), (2, 75, 4, 1, 64), (1, 100, 8, 2, 256)])
+@pytest.mark.parametrize("B,T,H,Hkv,D", [(1, 200, 8, 2, 128), (2, 75, 4, 1, 64), (1, 100, 8, 2, 256),
+                                         (1, 70, 8, 2, 192)])
 def test_backward_every_dkdv_variant(gpu, zt, oracle, threads, monkeypatch, env, B, T, H, Hkv, D):
     """Each dk/dv kernel variant (eight-wave, register-staged, asynchronously
-    staged; 1/2/4-way head splits; paired or single key tiles per workgroup),
-    forced through the library's tuning variables, matches the twin."""
+    staged, columns split over two waves for d = 192 / 256; 1/2/4-way head
+    splits; paired or single key tiles per workgroup), forced through the
+    library's tuning variables, matches the twin."""
     for k_, v_ in env.items():
         monkeypatch.setenv(k_, v_)
     (q, k, v, do), (dq, dk, dv, *_) = _run(gpu, zt, B, T, H, Hkv, D)
@@ -186,3 +195,13 @@ def test_block_backward_through_rope_on_the_device(gpu, zt, oracle, threads, T, 
     assert rel_err(dv, rv) <= BWD_REL
     # The gradient before ropeBackward is not the answer (rows t > 0 rotate).
     assert rel_err(dq, want_q) > 10 * BWD_REL
+
+
+def test_plan_names_the_column_split_kernel(gpu, zt, monkeypatch):
+    """Heads of 192 or 256 with an even head group take the eight-wave kernel
+    that splits the columns over two waves; ZT_ATTN_DSPLIT=0 turns it off."""
+    assert zt.plan(1, 256, 8, 2, 256)[2] == "zt_bwd_dkdv8pd_d256_hs2"
+    assert zt.plan(1, 256, 8, 2, 192)[2] == "zt_bwd_dkdv8pd_d192_hs2"
+    assert "8pd" not in zt.plan(1, 256, 8, 2, 160)[2] and "8pd" not in zt.plan(1, 256, 8, 8, 256)[2]
+    monkeypatch.setenv("ZT_ATTN_DSPLIT", "0")
+    assert "8pd" not in zt.plan(1, 256, 8, 2, 256)[2]

@@ -430,7 +430,7 @@ __device__ __forceinline__ void bwd_dq_lse_tile(const BwdArgs &a, const int tile
 template <int DP, int HS, int KW, bool PF = false, int NU = 1, bool SIN = false, int DS = 1>
 __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile, const bool up) {
     static_assert(!SIN || PF, "the scores are prefetched with the stage's rows");
-    static_assert(DS == 1 || (SIN && DS == 2 && (DP / 32) % 2 == 0), "d-split: score-reading, whole 32-column halves");
+    static_assert(DS == 1 || (PF && DS == 2 && (DP / 32) % 2 == 0), "d-split: prefetching, whole 32-column halves");
     constexpr int LW = DP + 4, DQ = DP / 4, NT = DP / 16, NTH = 64 * KW * HS * DS;
     constexpr int DPW = DP / DS, DQW = DPW / 4, NTW = DPW / 16;  // a wave's columns
     constexpr int BQ = 16 * NU;  // query rows per stage: NU sub-tiles of 16
@@ -444,7 +444,7 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
     constexpr int RED_F = (HS - 1) * KW * DS * 64 * 2 * NTW * 4;
     constexpr int BUF_F = PF ? 2 * STAGE_F : STAGE_F;
     constexpr int MAIN_F = BUF_F > RED_F ? BUF_F : RED_F;
-    constexpr int XCH_F = DS > 1 ? KW * HS * DS * NU * 64 * 4 : 0;  // partial dP exchange (d-split)
+    constexpr int XCH_F = DS > 1 ? KW * HS * DS * NU * 64 * 4 * (SIN ? 1 : 2) : 0;  // partial S, dP exchange (d-split)
     __shared__ float smem[MAIN_F + XCH_F];
     float *Qs = smem, *Ds = smem + HS * BQ * LW, *St = smem + 2 * HS * BQ * LW;
 
@@ -464,9 +464,10 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
 
     const int my_key = s0 + l16;
     const bool key_ok = my_key < a.T;
-    float kr[SIN ? 1 : DQ], vr[DQW];  // with the forward's scores K is not needed
+    float kr[SIN ? 1 : DQW], vr[DQW];  // with the forward's scores K is not needed
     if constexpr (!SIN)
-        load_row_seg<DQ>(kr, a.k + kvoff + (size_t)my_key * kld, grp * DQ, a.dim, vec4, key_ok, a.scale_log2e);
+        load_row_seg<DQW>(kr, a.k + kvoff + (size_t)my_key * kld + dh * DPW, grp * DQW, a.dim - dh * DPW, vec4, key_ok,
+                          a.scale_log2e);
     load_row_seg<DQW>(vr, a.v + kvoff + (size_t)my_key * kld + dh * DPW, grp * DQW, a.dim - dh * DPW, vec4, key_ok,
                       1.f);
 
@@ -636,11 +637,12 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
             }
         } else {
 #pragma unroll
-            for (int kk = 0; kk < DQ; kk += 4) {
+            for (int kk = 0; kk < DQW; kk += 4) {
 #pragma unroll
                 for (int u = 0; u < NU; ++u) {
-                    const f4 qx = *reinterpret_cast<const f4 *>(qs + (16 * u + l16) * LW + grp * DQ + kk);
-                    const f4 dx = *reinterpret_cast<const f4 *>(ds + (16 * u + l16) * LW + grp * DQ + kk);
+                    const int col = dh * DPW + grp * DQW + kk;
+                    const f4 qx = *reinterpret_cast<const f4 *>(qs + (16 * u + l16) * LW + col);
+                    const f4 dx = *reinterpret_cast<const f4 *>(ds + (16 * u + l16) * LW + col);
                     s[u] = mfma16(qx.x, kr[kk + 0], s[u]);
                     dp[u] = mfma16(dx.x, vr[kk + 0], dp[u]);
                     s[u] = mfma16(qx.y, kr[kk + 1], s[u]);
@@ -651,6 +653,21 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
                     dp[u] = mfma16(dx.w, vr[kk + 3], dp[u]);
                 }
                 fetch_after(kk / 4);
+            }
+            if constexpr (DS > 1) {  // partial S and dP from the partner holding the other columns
+                f4 *xch = reinterpret_cast<f4 *>(smem + MAIN_F);
+#pragma unroll
+                for (int u = 0; u < NU; ++u) {
+                    xch[((w * NU + u) * 2 + 0) * 64 + lane] = s[u];
+                    xch[((w * NU + u) * 2 + 1) * 64 + lane] = dp[u];
+                }
+                __syncthreads();
+                const int pw = w ^ (KW * HS);
+#pragma unroll
+                for (int u = 0; u < NU; ++u) {
+                    s[u] += xch[((pw * NU + u) * 2 + 0) * 64 + lane];
+                    dp[u] += xch[((pw * NU + u) * 2 + 1) * 64 + lane];
+                }
             }
         }
         // s[u][r] = S[t = t0 + 16 u + 4 grp + r][key = s0 + l16]
@@ -1147,6 +1164,13 @@ ZT_BWD_DKDV_DMAS(160) ZT_BWD_DKDV_DMAS(192) ZT_BWD_DKDV_DMAS(224) ZT_BWD_DKDV_DM
         bwd_dkdv_body<DP, 2, 2, true, 1, true, 2>(a);                                              \
     }
 ZT_BWD_DKDV8SD(192) ZT_BWD_DKDV8SD(256)
+// The same column split for the kernel that forms S again (reference entry
+// point and the training path without scores), partial S and dP exchanged.
+#define ZT_BWD_DKDV8PD(DP)                                                                         \
+    extern "C" __global__ void __launch_bounds__(512) zt_bwd_dkdv8pd_d##DP##_hs2(BwdArgs a) {   \
+        bwd_dkdv_body<DP, 2, 2, true, 1, false, 2>(a);                                             \
+    }
+ZT_BWD_DKDV8PD(192) ZT_BWD_DKDV8PD(256)
 
 // delta[row] = sum_d o[row, d] * dout[row, d] over the B*T*H rows of dim
 // floats (the row statistic the dk/dv kernel needs, autograd.zig:774-797 as

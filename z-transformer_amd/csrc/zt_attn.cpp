@@ -193,6 +193,8 @@ size_t dkdv_dma_bytes(int dp, int hs) { return ((size_t)2 * hs * 2 * 16 * dp + (
 // The column-split score-reading kernel (d = 192, 256): two 16-row stage
 // buffers for two head halves plus the partial-dP exchange of its eight waves.
 size_t dkdv_ds_bytes(int dp) { return dkdv_bytes(dp, 2, 2, 16, 2) + (size_t)8 * 64 * 4 * sizeof(float); }
+// The same for the kernel that forms S again: partial S and dP exchanged.
+size_t dkdv_dspd_bytes(int dp) { return dkdv_bytes(dp, 2, 2, 16, 2) + (size_t)2 * 8 * 64 * 4 * sizeof(float); }
 // Score-reading dk/dv kernel for heads wider than 128: the column-split
 // eight-wave kernel where the head halves are whole 32-column groups (two
 // waves per SIMD instead of one), else the four-wave asynchronously staged
@@ -412,7 +414,12 @@ int backward_prepare(const float *q, const float *k, const float *v, const float
                         dkdv_dma_bytes(dp, hs) <= st->lds_limit;
     const bool dma_pays =
         dp >= 160 || (unsigned long long)a->n_key_tiles * n_kv_heads * B < 2ull * (unsigned long long)st->cus;
-    const bool dma = !wide && dma_ok && env_choice("ZT_ATTN_DMA", dma_pays ? 1 : 0, {0, 1}) == 1;
+    // Wide heads whose halves are whole 32-column groups: eight waves splitting
+    // the columns (two per SIMD) instead of the four-wave kernels (C5 and the
+    // reference entry points; ZT_ATTN_DSPLIT=0 forces the four-wave kernels).
+    const bool dsplit = !wide && hs == 2 && (dp == 192 || dp == 256) && dim == dp && aligned &&
+                        dkdv_dspd_bytes(dp) <= st->lds_limit && env_choice("ZT_ATTN_DSPLIT", 1, {0, 1}) == 1;
+    const bool dma = !wide && !dsplit && dma_ok && env_choice("ZT_ATTN_DMA", dma_pays ? 1 : 0, {0, 1}) == 1;
     a->scale = (float)(1.0 / std::sqrt((double)dim));
     a->scale_log2e = (float)(1.4426950408889634 / std::sqrt((double)dim));
     const unsigned long long blocks_a =
@@ -431,9 +438,11 @@ int backward_prepare(const float *q, const float *k, const float *v, const float
                     env_choice("ZT_ATTN_PF", 1, {0, 1}) == 1;
     if (wide)
         snprintf(name_dkdv, 64, pf ? "zt_bwd_dkdv8p_d%d_hs2" : "zt_bwd_dkdv8_d%d_hs2", dp);
+    else if (dsplit)
+        snprintf(name_dkdv, 64, "zt_bwd_dkdv8pd_d%d_hs2", dp);
     else
         snprintf(name_dkdv, 64, dma ? "zt_bwd_dkdv_dma_d%d_hs%d" : "zt_bwd_dkdv_d%d_hs%d", dp, hs);
-    *threads_dkdv = wide ? 512 : kThreads;
+    *threads_dkdv = wide || dsplit ? 512 : kThreads;
     *blocks_dq = (unsigned)blocks_a;
     *blocks_dkdv = (unsigned)blocks_b;
     *st_out = st;
@@ -518,7 +527,7 @@ size_t zt_attn_bwd_dkdv_shmem(int dim) {
     const int dp = pad32(dim);
     size_t most = dkdv_bytes(dp, dp <= 128 ? 4 : 2);
     if (dp <= 128) most = std::max(most, dkdv_bytes(dp, 2, 4, 32, 2));  // eight waves, two 32-row stage buffers
-    if (dp == 192 || dp == 256) most = std::max(most, dkdv_ds_bytes(dp));  // column-split eight waves
+    if (dp == 192 || dp == 256) most = std::max(most, dkdv_dspd_bytes(dp));  // column-split eight waves
     for (int hs : {1, 2, 4})
         if (!(hs == 4 && dp > 128) && dkdv_dma_bytes(dp, hs) > most) most = dkdv_dma_bytes(dp, hs);
     return most;
