@@ -395,9 +395,12 @@ int backward_prepare(const float *q, const float *k, const float *v, const float
     // dk/dv variant, measured on MI355X (C2/C3/C5 shapes):
     //  - eight-wave workgroups (4 key blocks x 2 head halves share each staged
     //    Q/dO tile) for a 2-way split up to d = 128 (C3: 2.91 ms vs 3.22 ms);
-    //  - asynchronous double-buffered staging for wider heads (C5: 1.97 ms vs
-    //    2.27 ms) and for grids too small to hide the staging latency with
-    //    other workgroups; it needs whole-head rows on 16-byte aligned q/dout;
+    //  - d = 192, 256: eight waves splitting the head's columns in two, two
+    //    per SIMD (C5: 1.32 ms vs 1.57 ms for the kernel below);
+    //  - asynchronous double-buffered staging for the other wide heads (C5
+    //    before the column split: 1.97 ms vs 2.27 ms) and for grids too small
+    //    to hide the staging latency with other workgroups; it needs
+    //    whole-head rows on 16-byte aligned q/dout;
     //  - otherwise the four-wave register-staged kernel.
     const bool wide = env_choice("ZT_ATTN_W8", 1, {0, 1}) == 1 && hs == 2 && dp <= 128 &&
                       dkdv_bytes(dp, 2, 4) <= st->lds_limit;
