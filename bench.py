@@ -11,8 +11,9 @@ seeded N(0,1) on the device and resident in HBM before timing.  The headline
 value is fwd+bwd TFLOP/s with the causal-pair FLOP count
 (fwd 2*B*H*d*T(T+1), bwd 5*B*H*d*T(T+1)).  The reference's own entry points
 (zt_attn_forward + zt_attn_backward, whose backward rebuilds the softmax
-statistics) are timed on the same inputs under "reference_abi".  The same
-line also carries the
+statistics) are timed on the same inputs under "reference_abi".  The other
+training configurations (C2: MHA d 64; C5: d 256) are timed the same two ways
+under "other_configs" (secondary figures).  The same line also carries the
 decode step (C4: B=64, 8192 cached keys, GB/s of K/V/q/out) and RMSNorm
 ([64,4096] and [4096,4096], GB/s over rotating buffers larger than the 256 MB
 MALL), per-kernel times from HIP events on the launch stream, the roofline of
@@ -220,6 +221,41 @@ def main():
                 "frac": round(dom["tflops"] / PEAK_MFMA_F32, 4), "traffic": traffic, "kernel": dom["kernel"]}
     del out, dq, dk, dv, do, q, k, v, rm, rl, rd, lse, delta, work
 
+    # ---------------- C2, C5: the other training configurations ----------------
+    # Secondary figures (C3 is the headline): the same training step -- the
+    # forward keeping its scores where the shape allows, then the backward --
+    # and the reference's own entry points, on the configurations' inputs
+    # (C5: N(0, 2), sigma = sqrt(2)).
+    other = {}
+    for cname, (Bo, To, Ho, Hkvo, Do, sig) in {"C2": (4, 1024, 8, 8, 64, 1.0),
+                                                "C5": (2, 2048, 16, 4, 256, 2.0 ** 0.5)}.items():
+        qo, do_ = normal(Bo * To * Ho * Do, SEEDS["q"], sig), normal(Bo * To * Ho * Do, SEEDS["do"], sig)
+        ko, vo = normal(Bo * To * Hkvo * Do, SEEDS["k"], sig), normal(Bo * To * Hkvo * Do, SEEDS["v"], sig)
+        oo, dqo = torch.empty_like(qo), torch.empty_like(qo)
+        dko, dvo = torch.empty_like(ko), torch.empty_like(vo)
+        lseo, rmo, rlo, rdo = (torch.empty(Bo * To * Ho, device=dev) for _ in range(4))
+        wo = torch.empty(zt.backward_train_workspace_bytes(Bo, To, Ho, Hkvo, Do) // 4, device=dev)
+        flop_o = 7 * 2 * Do * Bo * Ho * To * (To + 1) / 2
+
+        def train_o():
+            zt.forward_train_ws(qo, ko, vo, oo, lseo, wo, To, Ho, Hkvo, Do, B=Bo)
+            zt.backward_train_ws(qo, ko, vo, oo, do_, lseo, dqo, dko, dvo, wo, To, Ho, Hkvo, Do, B=Bo, stage=scores)
+
+        def ref_o():
+            zt.forward(qo, ko, vo, oo, To, Ho, Hkvo, Do, B=Bo)
+            zt.backward(qo, ko, vo, do_, dqo, dko, dvo, rmo, rlo, rdo, To, Ho, Hkvo, Do, B=Bo)
+
+        entry = {"workload": f"{cname} B={Bo} T={To} Hq={Ho} Hkv={Hkvo} d={Do} f32"}
+        for tag, fn in (("train", train_o), ("reference_abi", ref_o)):
+            for _ in range(args.warmup):
+                fn()
+            t_o = event_time(torch, fn, max(3, args.steps))
+            entry[tag] = {"ms_per_step": round(t_o, 4), "TFLOP/s": round(flop_o / (t_o * 1e-3) / 1e12, 3)}
+            log(f"{cname} step ({tag}): {t_o:.3f} ms, {flop_o / (t_o * 1e-3) / 1e12:.2f} TFLOP/s fwd+bwd")
+        entry["train"]["kernels"] = list(zt.plan_train(Bo, To, Ho, Hkvo, Do))
+        other[cname] = entry
+        del qo, ko, vo, do_, oo, dqo, dko, dvo, lseo, rmo, rlo, rdo, wo
+
     # ---------------- C4: decode step ----------------
     Bd, n_ctx = 64, 8192
     qd = normal(Bd * H * D, SEEDS["q"])
@@ -377,6 +413,7 @@ def main():
                           "kernels": [{k2: (round(v2, 4) if isinstance(v2, float) else v2) for k2, v2 in kk.items()}
                                       for kk in res["reference_abi"]["kernels"]]},
         "kernels": [{k2: (round(v2, 4) if isinstance(v2, float) else v2) for k2, v2 in kk.items()} for kk in kernels],
+        "other_configs": other,
         "decode": {"workload": "C4 B=64 n_keys=8192 Hq=32 Hkv=8 d=128 f32", "us": round(t_dec * 1e3, 2),
                    "GB/s": round(dec_gbs, 1), "bytes": dec_bytes, "frac_hbm": round(dec_gbs / PEAK_HBM, 4),
                    "step_us": round(t_step * 1e3, 2), "step_GB/s": round(step_gbs, 1)},
