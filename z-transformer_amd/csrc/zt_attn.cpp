@@ -199,6 +199,8 @@ size_t dkdv_dspd_bytes(int dp) { return dkdv_bytes(dp, 2, 2, 16, 2) + (size_t)2 
 // eight-wave kernel where the head halves are whole 32-column groups (two
 // waves per SIMD instead of one), else the four-wave asynchronously staged
 // one.  ZT_ATTN_DSPLIT=0 forces the latter.
+// Paired dk/dv key tiles by default only when the unpaired grid is larger than the CU count.
+int pair_pays(unsigned long long unpaired_blocks, int cus) { return unpaired_blocks > (unsigned long long)cus ? 1 : 0; }
 bool dkdv_dsplit(int dp, size_t lds_limit) {
     return (dp == 192 || dp == 256) && dkdv_ds_bytes(dp) <= lds_limit && env_choice("ZT_ATTN_DSPLIT", 1, {0, 1}) == 1;
 }
@@ -408,15 +410,20 @@ int backward_prepare(const float *q, const float *k, const float *v, const float
     a->n_key_tiles = (T + keys_per_wg - 1) / keys_per_wg;
     // Paired tiles (a workgroup takes tile p and its partner n - 1 - p): equal
     // causal work per workgroup; measured on MI355X, C3 dk/dv 2.47 -> 2.37 ms,
-    // reading scores 2.01 -> 1.93 ms, C5 1.49 -> 1.43 ms.
-    a->pair = env_choice("ZT_ATTN_BPAIR", 1, {0, 1});
+    // reading scores 2.01 -> 1.93 ms, C5 1.49 -> 1.43 ms.  Not when the
+    // unpaired grid already fits the CUs once: pairing would leave CUs idle
+    // (one MHA sequence, T 1024, d 64: 0.131 -> 0.122 ms without).
+    a->pair = env_choice("ZT_ATTN_BPAIR", pair_pays((unsigned long long)a->n_key_tiles * n_kv_heads * B, st->cus),
+                         {0, 1});
     const unsigned long long blocks_b =
         (unsigned long long)(a->pair ? (a->n_key_tiles + 1) / 2 : a->n_key_tiles) * n_kv_heads * B;
     const bool aligned = ((uintptr_t)q % 16 == 0) && ((uintptr_t)dout % 16 == 0);
     const bool dma_ok = dim == dp && aligned && !(hs == 4 && dp > 128) && !(hs == 1 && dp >= 224) &&
                         dkdv_dma_bytes(dp, hs) <= st->lds_limit;
+    // Asynchronous staging pays where at most one workgroup per CU runs (C2:
+    // 0.165 -> 0.137 ms) and for wide heads.
     const bool dma_pays =
-        dp >= 160 || (unsigned long long)a->n_key_tiles * n_kv_heads * B < 2ull * (unsigned long long)st->cus;
+        dp >= 160 || (unsigned long long)((a->n_key_tiles + 1) / 2) * n_kv_heads * B <= (unsigned long long)st->cus;
     // Wide heads whose halves are whole 32-column groups: eight waves splitting
     // the columns (two per SIMD) instead of the four-wave kernels (C5 and the
     // reference entry points; ZT_ATTN_DSPLIT=0 forces the four-wave kernels).
@@ -706,6 +713,8 @@ int zt_attn_backward_train_ws(const float *q, const float *k, const float *v, co
         const int keys = dp <= 128 ? 64 : 32;
         const bool dsplit = dp > 128 && dkdv_dsplit(dp, st->lds_limit);
         a.n_key_tiles = (T + keys - 1) / keys;
+        a.pair = env_choice("ZT_ATTN_BPAIR", pair_pays((unsigned long long)a.n_key_tiles * n_kv_heads * B, st->cus),
+                            {0, 1});
         const unsigned long long blocks =
             (unsigned long long)(a.pair ? (a.n_key_tiles + 1) / 2 : a.n_key_tiles) * n_kv_heads * B;
         if (!grid_ok(blocks)) return 1;
