@@ -79,16 +79,20 @@ _NO_DS = {"ZT_ATTN_DSPLIT": "0"}
     {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "0", "ZT_ATTN_HS": "4", **_NO_DS},
     {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "1", "ZT_ATTN_HS": "4", **_NO_DS},
     {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "0", "ZT_ATTN_HS": "1", **_NO_DS},
-    {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "1", "ZT_ATTN_HS": "1", **_NO_DS},
+    {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "1", "ZT_ATTN_HS": "1", "ZT_ATTN_RSPLIT": "0", **_NO_DS},
     {"ZT_ATTN_DSPLIT": "1"}, {"ZT_ATTN_DSPLIT": "1", "ZT_ATTN_BPAIR": "0"},
+    {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "1", "ZT_ATTN_HS": "1", "ZT_ATTN_RSPLIT": "1", **_NO_DS},
+    {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "1", "ZT_ATTN_HS": "1", "ZT_ATTN_RSPLIT": "1", "ZT_ATTN_BPAIR": "1", **_NO_DS},
+    {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "1", "ZT_ATTN_HS": "1", "ZT_ATTN_RSPLIT": "0", **_NO_DS},
 ])
 @pytest.mark.parametrize("B,T,H,Hkv,D", [(1, 200, 8, 2, 128), (2, 75, 4, 1, 64), (1, 100, 8, 2, 256),
-                                         (1, 70, 8, 2, 192)])
+                                         (1, 70, 8, 2, 192), (2, 90, 3, 3, 32), (1, 47, 6, 2, 96)])
 def test_backward_every_dkdv_variant(gpu, zt, oracle, threads, monkeypatch, env, B, T, H, Hkv, D):
     """Each dk/dv kernel variant (eight-wave, register-staged, asynchronously
-    staged, columns split over two waves for d = 192 / 256; 1/2/4-way head
-    splits; paired or single key tiles per workgroup), forced through the
-    library's tuning variables, matches the twin."""
+    staged, columns split over two waves for d = 192 / 256, rows split over
+    two parts for unsplit groups; 1/2/4-way head splits; paired or single key
+    tiles per workgroup), forced through the library's tuning variables,
+    matches the twin."""
     for k_, v_ in env.items():
         monkeypatch.setenv(k_, v_)
     (q, k, v, do), (dq, dk, dv, *_) = _run(gpu, zt, B, T, H, Hkv, D)

@@ -808,9 +808,14 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
 // row is inside the head) and 16-byte aligned q/dout; the host falls back to
 // bwd_dkdv_body otherwise.  Same arithmetic as bwd_dkdv_body; with SIN it reads
 // the forward's scores from the dS tiles as bwd_dkdv_body does.
-template <int DP, int HS, bool SIN = false>
+// RS (row split, for head groups that cannot be split): the HS parts take
+// alternate 16-row tiles of the same head instead of different heads, with
+// four key blocks, so a workgroup runs 4 x HS waves; the parts' partial dk/dv
+// are summed as the head halves' are.
+template <int DP, int HS, bool SIN = false, bool RS = false>
 __device__ __forceinline__ void bwd_dkdv_dma_tile(const BwdArgs &a, const int ktile) {
-    constexpr int DQ = DP / 4, NT = DP / 16, KW = 4 / HS, BQ = 16;
+    static_assert(!RS || (HS == 2 && !SIN), "row split: two parts, statistics path");
+    constexpr int DQ = DP / 4, NT = DP / 16, KW = RS ? 4 : 4 / HS, BQ = 16, NW = KW * HS;
     constexpr int CPR = DP / 4;          // 16-byte chunks per row
     constexpr int TILE = BQ * DP;        // floats per (part, array) tile
     constexpr int NI = BQ * CPR / 64;    // dma16 wave-instructions per tile
@@ -825,7 +830,7 @@ __device__ __forceinline__ void bwd_dkdv_dma_tile(const BwdArgs &a, const int kt
     const int rem = (int)blockIdx.x % per_tile;
     const int kvh = rem % a.Hkv, b = rem / a.Hkv;
     const int group = a.H / a.Hkv;
-    const int hpp = group / HS;
+    const int hpp = RS ? group : group / HS;
     const int wg_s0 = ktile * 16 * KW;
     const int s0 = wg_s0 + 16 * kbw;
     const size_t qld = (size_t)a.H * DP, kld = (size_t)a.Hkv * DP;
@@ -844,41 +849,54 @@ __device__ __forceinline__ void bwd_dkdv_dma_tile(const BwdArgs &a, const int kt
     for (int i = 0; i < NT; ++i) { dka[i] = zero4(); dva[i] = zero4(); }
 
     const int n_t = (a.T - wg_s0 + BQ - 1) / BQ;  // 16-row tiles of the suffix
-    const int n_stage = hpp * n_t;                // times the heads of a part
+    const int n_rt = RS ? (n_t + HS - 1) / HS : n_t;  // row-tile groups per head (RS: one tile per part)
+    const int n_stage = hpp * n_rt;                // times the heads of a part
+    // Part `part` of stage `st`: its head, first row, and whether it has rows
+    // (RS: the last group can leave a part without a tile; its copies and
+    // statistics then repeat the last tile and it computes nothing).
+    struct PartRows { int hh, t0; bool ok; };
+    auto part_rows = [&](int st, int part) {
+        const int hi = st / n_rt, rj = st % n_rt;
+        if constexpr (RS) {
+            const int ri = rj * HS + part;
+            return PartRows{kvh * group + hi, wg_s0 + min(ri, n_t - 1) * BQ, ri < n_t};
+        } else {
+            return PartRows{kvh * group + part * hpp + hi, wg_s0 + rj * BQ, true};
+        }
+    };
 
     // Issues the copies of stage `st` into buffer `buf`; the statistics go to
     // registers and are written to LDS by put_stats after the current compute.
     float sm2 = 0.f, sil = 0.f, sde = 0.f;
     f4 sn = zero4(), sc = zero4();  // this wave's score tile of the next / this stage (SIN)
     auto issue = [&](int st, int buf) {
-        const int hi = st / n_t, t0 = wg_s0 + (st % n_t) * BQ;
         if constexpr (SIN) {
+            const PartRows pr = part_rows(st, hs);
             sn = zero4();
-            if (t0 + 15 >= s0 && s0 < a.T) {  // wave-uniform; t0 < T for every stage
+            if (pr.t0 + 15 >= s0 && s0 < a.T) {  // wave-uniform; t0 < T for every stage
                 const int nt = (a.T + 15) >> 4;
-                const size_t tile =
-                    (((size_t)b * a.H + kvh * group + hs * hpp + hi) * nt + (t0 >> 4)) * nt + (s0 >> 4);
+                const size_t tile = (((size_t)b * a.H + pr.hh) * nt + (pr.t0 >> 4)) * nt + (s0 >> 4);
                 sn = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(a.ds_out + tile * 256) + lane);
             }
         }
         if (tid < HS * BQ) {
-            const int part = tid / BQ, t = t0 + tid % BQ;
-            const int hh = kvh * group + part * hpp + hi;
+            const PartRows pr = part_rows(st, tid / BQ);
+            const int t = pr.t0 + tid % BQ;
             sm2 = 0.f; sil = 0.f; sde = 0.f;  // as loaded; put_stats finishes them
-            if (t < a.T) {
-                const size_t o = ((size_t)b * a.T + t) * a.H + hh;
+            if (t < a.T && pr.ok) {
+                const size_t o = ((size_t)b * a.T + t) * a.H + pr.hh;
                 sm2 = a.lse ? a.lse[o] : a.row_max[o];
                 sil = a.lse ? 1.f : a.row_den[o];
                 sde = a.row_del[o];
             }
         }
-        for (int i = w; i < HS * 2 * NI; i += 4) {
+        for (int i = w; i < HS * 2 * NI; i += NW) {
             const int part = i / (2 * NI), arr = (i / NI) & 1, ii = i % NI;
-            const int hh = kvh * group + part * hpp + hi;
-            const float *src = (arr ? a.dout : a.q) + qbat + (size_t)hh * DP;
+            const PartRows pr = part_rows(st, part);
+            const float *src = (arr ? a.dout : a.q) + qbat + (size_t)pr.hh * DP;
             const int e = ii * 64 + lane;
             const int r = e / CPR, c = swz<CPR>(e % CPR, r);
-            const int t = min(t0 + r, a.T - 1);  // rows past T: a real row, masked below
+            const int t = min(pr.t0 + r, a.T - 1);  // rows past T: a real row, masked below
             dma16(src + (size_t)t * qld + 4 * c, smem + buf * STAGE + (part * 2 + arr) * TILE + ii * 256);
         }
     };
@@ -899,8 +917,9 @@ __device__ __forceinline__ void bwd_dkdv_dma_tile(const BwdArgs &a, const int kt
         const int buf = st & 1;
         if constexpr (SIN) sc = sn;
         if (st + 1 < n_stage) issue(st + 1, buf ^ 1);
-        const int t0 = wg_s0 + (st % n_t) * BQ;
-        if (!(t0 + 15 < s0 || s0 >= a.T)) {
+        const PartRows mine = part_rows(st, hs);
+        const int t0 = mine.t0;
+        if (mine.ok && !(t0 + 15 < s0 || s0 >= a.T)) {
             const float *qs = smem + buf * STAGE + (hs * 2 + 0) * TILE;
             const float *ds = smem + buf * STAGE + (hs * 2 + 1) * TILE;
             const float *sp = stats + buf * HS * BQ * 4 + hs * BQ * 4;
@@ -959,9 +978,8 @@ __device__ __forceinline__ void bwd_dkdv_dma_tile(const BwdArgs &a, const int kt
                 dsv[r] = p[r] * (dp[r] - stv[r].z);
             }
             if (a.ds_out) {  // dS for a dq product outside this kernel: the 16 x 16 tile in lane order
-                const int hh = kvh * group + hs * hpp + st / n_t;
                 const int nt = (a.T + 15) >> 4;
-                const size_t tile = (((size_t)b * a.H + hh) * nt + (t0 >> 4)) * nt + (s0 >> 4);
+                const size_t tile = (((size_t)b * a.H + mine.hh) * nt + (t0 >> 4)) * nt + (s0 >> 4);
                 __builtin_nontemporal_store(dsv, reinterpret_cast<f4 *>(a.ds_out + tile * 256) + lane);
             }
             // dO^T, Q^T rows in the row-owner layout, read one row ahead.
@@ -1070,13 +1088,13 @@ __device__ __forceinline__ void bwd_dkdv_body(const BwdArgs &a) {
         bwd_dkdv_tile<DP, HS, KW, PF, NU, SIN, DS>(a, n - 1 - p, true);
     }
 }
-template <int DP, int HS, bool SIN = false>
+template <int DP, int HS, bool SIN = false, bool RS = false>
 __device__ __forceinline__ void bwd_dkdv_dma_body(const BwdArgs &a) {
     const int p = (int)blockIdx.x / (a.Hkv * a.B), n = a.n_key_tiles;
-    bwd_dkdv_dma_tile<DP, HS, SIN>(a, p);
+    bwd_dkdv_dma_tile<DP, HS, SIN, RS>(a, p);
     if (a.pair && n - 1 - p > p) {
         __syncthreads();  // the head-split sum reads LDS; the next tile's copies start at once
-        bwd_dkdv_dma_tile<DP, HS, SIN>(a, n - 1 - p);
+        bwd_dkdv_dma_tile<DP, HS, SIN, RS>(a, n - 1 - p);
     }
 }
 
@@ -1146,6 +1164,13 @@ ZT_BWD_DKDV(32, 4)
 ZT_BWD_DKDV(64, 4)
 ZT_BWD_DKDV(96, 4)
 ZT_BWD_DKDV(128, 4)
+// Row-split asynchronously staged dk/dv (head groups that cannot be split,
+// such as MHA): eight waves, 4 key blocks x 2 row parts.
+#define ZT_BWD_DKDV_DMAR(DP)                                                                       \
+    extern "C" __global__ void __launch_bounds__(512) zt_bwd_dkdv_dmar_d##DP(BwdArgs a) {        \
+        bwd_dkdv_dma_body<DP, 2, false, true>(a);                                                  \
+    }
+ZT_BWD_DKDV_DMAR(32) ZT_BWD_DKDV_DMAR(64) ZT_BWD_DKDV_DMAR(96) ZT_BWD_DKDV_DMAR(128)
 ZT_BWD_DKDV_DMA(32, 4)
 ZT_BWD_DKDV_DMA(64, 4)
 ZT_BWD_DKDV_DMA(96, 4)

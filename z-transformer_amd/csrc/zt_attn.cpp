@@ -433,6 +433,10 @@ int backward_prepare(const float *q, const float *k, const float *v, const float
     const bool dsplit = !wide && hs == 2 && (dp == 192 || dp == 256) && dim == dp && aligned &&
                         dkdv_dspd_bytes(dp) <= st->lds_limit && env_choice("ZT_ATTN_DSPLIT", 1, {0, 1}) == 1;
     const bool dma = !wide && !dsplit && dma_ok && env_choice("ZT_ATTN_DMA", dma_pays ? 1 : 0, {0, 1}) == 1;
+    // A group that cannot be split (MHA, odd groups) on the asynchronously
+    // staged kernel: two row parts per workgroup instead, eight waves.
+    const bool rsplit = dma && hs == 1 && dp <= 128 && dkdv_dma_bytes(dp, 2) <= st->lds_limit &&
+                        env_choice("ZT_ATTN_RSPLIT", 1, {0, 1}) == 1;
     a->scale = (float)(1.0 / std::sqrt((double)dim));
     a->scale_log2e = (float)(1.4426950408889634 / std::sqrt((double)dim));
     const unsigned long long blocks_a =
@@ -453,9 +457,11 @@ int backward_prepare(const float *q, const float *k, const float *v, const float
         snprintf(name_dkdv, 64, pf ? "zt_bwd_dkdv8p_d%d_hs2" : "zt_bwd_dkdv8_d%d_hs2", dp);
     else if (dsplit)
         snprintf(name_dkdv, 64, "zt_bwd_dkdv8pd_d%d_hs2", dp);
+    else if (rsplit)
+        snprintf(name_dkdv, 64, "zt_bwd_dkdv_dmar_d%d", dp);
     else
         snprintf(name_dkdv, 64, dma ? "zt_bwd_dkdv_dma_d%d_hs%d" : "zt_bwd_dkdv_d%d_hs%d", dp, hs);
-    *threads_dkdv = wide || dsplit ? 512 : kThreads;
+    *threads_dkdv = wide || dsplit || rsplit ? 512 : kThreads;
     *blocks_dq = (unsigned)blocks_a;
     *blocks_dkdv = (unsigned)blocks_b;
     *st_out = st;
