@@ -19,7 +19,7 @@ decode step (C4: B=64, 8192 cached keys, GB/s of K/V/q/out) and RMSNorm
 MALL), per-kernel times from HIP events on the launch stream, the roofline of
 the dominant kernel, and the CPU restatement timed on a bounded sample.
 
-    python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--cpu-rows 64] [--no-cpu]
+    python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--cpu-rows 64] [--no-cpu] [--no-other]
 """
 import argparse
 import ctypes
@@ -73,6 +73,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--cpu-rows", type=int, default=48, help="query rows of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-other", action="store_true", help="skip the C2 / C5 figures (profiling runs)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -227,8 +228,8 @@ def main():
     # and the reference's own entry points, on the configurations' inputs
     # (C5: N(0, 2), sigma = sqrt(2)).
     other = {}
-    for cname, (Bo, To, Ho, Hkvo, Do, sig) in {"C2": (4, 1024, 8, 8, 64, 1.0),
-                                                "C5": (2, 2048, 16, 4, 256, 2.0 ** 0.5)}.items():
+    other_cfgs = {} if args.no_other else {"C2": (4, 1024, 8, 8, 64, 1.0), "C5": (2, 2048, 16, 4, 256, 2.0 ** 0.5)}
+    for cname, (Bo, To, Ho, Hkvo, Do, sig) in other_cfgs.items():
         qo, do_ = normal(Bo * To * Ho * Do, SEEDS["q"], sig), normal(Bo * To * Ho * Do, SEEDS["do"], sig)
         ko, vo = normal(Bo * To * Hkvo * Do, SEEDS["k"], sig), normal(Bo * To * Hkvo * Do, SEEDS["v"], sig)
         oo, dqo = torch.empty_like(qo), torch.empty_like(qo)
@@ -413,7 +414,7 @@ def main():
                           "kernels": [{k2: (round(v2, 4) if isinstance(v2, float) else v2) for k2, v2 in kk.items()}
                                       for kk in res["reference_abi"]["kernels"]]},
         "kernels": [{k2: (round(v2, 4) if isinstance(v2, float) else v2) for k2, v2 in kk.items()} for kk in kernels],
-        "other_configs": other,
+        "other_configs": other or None,
         "decode": {"workload": "C4 B=64 n_keys=8192 Hq=32 Hkv=8 d=128 f32", "us": round(t_dec * 1e3, 2),
                    "GB/s": round(dec_gbs, 1), "bytes": dec_bytes, "frac_hbm": round(dec_gbs / PEAK_HBM, 4),
                    "step_us": round(t_step * 1e3, 2), "step_GB/s": round(step_gbs, 1)},
