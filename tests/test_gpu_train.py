@@ -185,6 +185,8 @@ def test_train_scores_stages_and_repeats(gpu, zt, B, T, H, Hkv, D):
 def test_train_scores_plan_names_the_score_reading_kernel(gpu, zt):
     assert zt.plan_train(1, 4096, 32, 8, 128) == ("zt_fwd8ps_d128_k32", "zt_gemm_dqds_128", "zt_bwd_dkdv8s_d128_hs2")
     assert "dkdv8s" not in zt.plan_train(1, 256, 8, 8, 128)[2]   # MHA: no score-reading kernel
+    assert zt.plan_train(4, 1024, 8, 8, 64)[0] == "zt_fwdp_d64_k32"   # MHA: four waves, prefetched
+    assert zt.plan_train(1, 300, 4, 4, 66)[0] == "zt_fwd_d96_k32"     # rows not 16-byte chunks: no prefetch
     assert zt.plan_train(1, 256, 8, 2, 256)[2] == "zt_bwd_dkdv8sd_d256_hs2"   # wide heads: columns split
     assert zt.plan_train(1, 256, 8, 2, 192)[2] == "zt_bwd_dkdv8sd_d192_hs2"
     assert zt.plan_train(1, 256, 8, 2, 160)[2] == "zt_bwd_dkdv_dmas_d160_hs2"   # halves not whole 32 columns

@@ -146,12 +146,13 @@ int heads_per_wg(int group) { return group % 4 == 0 ? 4 : (group % 2 == 0 ? 2 : 
 // Key tile (keys staged in LDS per step) for a width and a caller cap: 64 or
 // 32.  Measured on MI355X (C2/C3/C5 shapes): the dq kernel takes 32 keys with
 // the next tile prefetched into registers (C3 2.43 -> 2.23 ms, C2 0.132 ->
-// 0.119 ms, C5 1.74 -> 1.65 ms against 64 keys without); the forward prefers
-// 64 only at d <= 64 -- above that the 32-key tile keeps one more workgroup
-// resident per CU (C5, d = 256: 0.84 ms vs 1.11 ms).
+// 0.119 ms, C5 1.74 -> 1.65 ms against 64 keys without); so does the forward
+// wherever rows are 16-byte chunks (dim % 4 == 0; C2 0.074 -> 0.057 ms), and
+// without the prefetch it prefers 64 only at d <= 64 -- above that the 32-key
+// tile keeps one more workgroup resident per CU (C5, d = 256: 0.84 ms vs 1.11 ms).
 enum class Tiled { Forward, Dq };
-int key_tile(Tiled which, int dp, int max_tile) {
-    const int dflt = (which == Tiled::Forward && dp <= 64) ? 64 : 32;
+int key_tile(Tiled which, int dp, int max_tile, int dim = 0) {
+    const int dflt = (which == Tiled::Forward && dp <= 64 && dim % 4 != 0) ? 64 : 32;
     const int preferred = env_choice("ZT_ATTN_BK", dflt, {32, 64});
     return max_tile >= 64 ? preferred : 32;
 }
@@ -166,12 +167,13 @@ size_t kv_tile_bytes(int dp, int bk) { return (size_t)2 * bk * (dp + 4) * sizeof
 int fwd_waves(int hw) { return env_choice("ZT_ATTN_FWD_W", hw == 4 ? 8 : 4, {4, 8}); }
 
 // Forward kernel name: waves per workgroup, key tile, and for 32-key tiles the
-// register-prefetched variant (ZT_ATTN_FPF; default with eight waves, where
-// it measured C3 1.315 -> 1.225 ms and C5 0.758 -> 0.630 ms; with four waves
-// the prefetch registers cost occupancy and it loses).
+// register-prefetched variant (ZT_ATTN_FPF=0 turns it off).  Measured on
+// MI355X: eight waves, C3 1.315 -> 1.225 ms and C5 0.758 -> 0.630 ms; four
+// waves (MHA and head groups of two), C2 0.074 -> 0.057 ms and one 16-head
+// sequence of 2048 rows at d = 128 0.30 -> 0.185 ms.
 void fwd_kernel_name(char *name, size_t len, int dim, int dp, int bk, int nw) {
     // The prefetching kernels load 16-byte row chunks unconditionally (dim % 4 == 0).
-    const bool pf = bk == 32 && dim % 4 == 0 && env_choice("ZT_ATTN_FPF", nw == 8 ? 1 : 0, {0, 1}) == 1;
+    const bool pf = bk == 32 && dim % 4 == 0 && env_choice("ZT_ATTN_FPF", 1, {0, 1}) == 1;
     if (pf)
         snprintf(name, len, nw == 8 ? "zt_fwd8p_d%d_k32" : "zt_fwdp_d%d_k32", dp);
     else
@@ -303,7 +305,7 @@ int forward_impl(const float *q, const float *k, const float *v, float *out, int
     DeviceState *st = require_device();
     if (!st) return 1;
     const int dp = pad32(dim);
-    int bk = key_tile(Tiled::Forward, dp, max_tile);
+    int bk = key_tile(Tiled::Forward, dp, max_tile, dim);
     if (fwd_tile_bytes(dp, bk) > st->lds_limit) bk = 32;
     if (fwd_tile_bytes(dp, bk) > st->lds_limit) {
         fprintf(stderr, "zt_attn: head_dim %d needs %zu bytes of LDS per workgroup even at a 32-key tile, and\n"
@@ -532,7 +534,7 @@ size_t zt_attn_forward_shmem(int dim, int tile, int group_q) {
     (void)group_q;
     if (!zt_attn_dim_ok(dim)) return 0;
     const int dp = pad32(dim);
-    return fwd_tile_bytes(dp, key_tile(Tiled::Forward, dp, tile));
+    return fwd_tile_bytes(dp, key_tile(Tiled::Forward, dp, tile, dim));
 }
 
 size_t zt_attn_bwd_dq_shmem(int dim, int tile) {
@@ -1036,7 +1038,7 @@ int zt_attn_plan(int B, int T, int n_heads, int n_kv_heads, int dim, int max_til
     DeviceState *st = device_state();
     if (!st) return 1;
     const int dp = pad32(dim);
-    int bk = key_tile(Tiled::Forward, dp, max_tile);
+    int bk = key_tile(Tiled::Forward, dp, max_tile, dim);
     if (fwd_tile_bytes(dp, bk) > st->lds_limit) bk = 32;
     fwd_kernel_name(fwd, len, dim, dp, bk, fwd_waves(heads_per_wg(n_heads / n_kv_heads)));
     BwdArgs a;
