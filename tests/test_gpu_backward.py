@@ -84,9 +84,11 @@ _NO_DS = {"ZT_ATTN_DSPLIT": "0"}
     {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "1", "ZT_ATTN_HS": "1", "ZT_ATTN_RSPLIT": "1", **_NO_DS},
     {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "1", "ZT_ATTN_HS": "1", "ZT_ATTN_RSPLIT": "1", "ZT_ATTN_BPAIR": "1", **_NO_DS},
     {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "1", "ZT_ATTN_HS": "1", "ZT_ATTN_RSPLIT": "0", **_NO_DS},
+    {"ZT_ATTN_HS": "1", "ZT_ATTN_DSPLIT": "1"}, {"ZT_ATTN_HS": "1", "ZT_ATTN_DSPLIT": "1", "ZT_ATTN_BPAIR": "1"},
 ])
 @pytest.mark.parametrize("B,T,H,Hkv,D", [(1, 200, 8, 2, 128), (2, 75, 4, 1, 64), (1, 100, 8, 2, 256),
-                                         (1, 70, 8, 2, 192), (2, 90, 3, 3, 32), (1, 47, 6, 2, 96)])
+                                         (1, 70, 8, 2, 192), (2, 90, 3, 3, 32), (1, 47, 6, 2, 96),
+                                         (1, 100, 4, 4, 256), (2, 61, 6, 2, 192)])
 def test_backward_every_dkdv_variant(gpu, zt, oracle, threads, monkeypatch, env, B, T, H, Hkv, D):
     """Each dk/dv kernel variant (eight-wave, register-staged, asynchronously
     staged, columns split over two waves for d = 192 / 256, rows split over
@@ -202,10 +204,14 @@ def test_block_backward_through_rope_on_the_device(gpu, zt, oracle, threads, T, 
 
 
 def test_plan_names_the_column_split_kernel(gpu, zt, monkeypatch):
-    """Heads of 192 or 256 with an even head group take the eight-wave kernel
-    that splits the columns over two waves; ZT_ATTN_DSPLIT=0 turns it off."""
+    """Heads of 192 or 256 take the eight-wave kernel that splits the columns
+    over two waves: two head halves of four key blocks for an even head group,
+    one part of four key blocks for MHA and odd groups; ZT_ATTN_DSPLIT=0 turns
+    it off."""
     assert zt.plan(1, 256, 8, 2, 256)[2] == "zt_bwd_dkdv8pd_d256_hs2"
     assert zt.plan(1, 256, 8, 2, 192)[2] == "zt_bwd_dkdv8pd_d192_hs2"
-    assert "8pd" not in zt.plan(1, 256, 8, 2, 160)[2] and "8pd" not in zt.plan(1, 256, 8, 8, 256)[2]
+    assert zt.plan(1, 256, 8, 8, 256)[2] == "zt_bwd_dkdv8pd_d256_hs1"
+    assert zt.plan(1, 256, 6, 2, 192)[2] == "zt_bwd_dkdv8pd_d192_hs1"
+    assert "8pd" not in zt.plan(1, 256, 8, 2, 160)[2] and "8pd" not in zt.plan(1, 256, 8, 8, 250)[2]
     monkeypatch.setenv("ZT_ATTN_DSPLIT", "0")
-    assert "8pd" not in zt.plan(1, 256, 8, 2, 256)[2]
+    assert "8pd" not in zt.plan(1, 256, 8, 2, 256)[2] and "8pd" not in zt.plan(1, 256, 8, 8, 256)[2]

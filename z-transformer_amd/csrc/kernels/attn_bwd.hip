@@ -1190,10 +1190,15 @@ ZT_BWD_DKDV_DMAS(160) ZT_BWD_DKDV_DMAS(192) ZT_BWD_DKDV_DMAS(224) ZT_BWD_DKDV_DM
     }
 ZT_BWD_DKDV8SD(192) ZT_BWD_DKDV8SD(256)
 // The same column split for the kernel that forms S again (reference entry
-// point and the training path without scores), partial S and dP exchanged.
+// point and the training path without scores), partial S and dP exchanged;
+// for groups that cannot be halved (MHA, odd groups) four key blocks x two
+// column halves of one part.
 #define ZT_BWD_DKDV8PD(DP)                                                                         \
     extern "C" __global__ void __launch_bounds__(512) zt_bwd_dkdv8pd_d##DP##_hs2(BwdArgs a) {   \
         bwd_dkdv_body<DP, 2, 2, true, 1, false, 2>(a);                                             \
+    }                                                                                              \
+    extern "C" __global__ void __launch_bounds__(512) zt_bwd_dkdv8pd_d##DP##_hs1(BwdArgs a) {   \
+        bwd_dkdv_body<DP, 1, 4, true, 1, false, 2>(a);                                             \
     }
 ZT_BWD_DKDV8PD(192) ZT_BWD_DKDV8PD(256)
 

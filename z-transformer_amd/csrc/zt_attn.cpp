@@ -195,8 +195,11 @@ size_t dkdv_dma_bytes(int dp, int hs) { return ((size_t)2 * hs * 2 * 16 * dp + (
 // The column-split score-reading kernel (d = 192, 256): two 16-row stage
 // buffers for two head halves plus the partial-dP exchange of its eight waves.
 size_t dkdv_ds_bytes(int dp) { return dkdv_bytes(dp, 2, 2, 16, 2) + (size_t)8 * 64 * 4 * sizeof(float); }
-// The same for the kernel that forms S again: partial S and dP exchanged.
-size_t dkdv_dspd_bytes(int dp) { return dkdv_bytes(dp, 2, 2, 16, 2) + (size_t)2 * 8 * 64 * 4 * sizeof(float); }
+// The same for the kernel that forms S again: partial S and dP exchanged
+// (hs 1: one part of four key blocks).
+size_t dkdv_dspd_bytes(int dp, int hs = 2) {
+    return dkdv_bytes(dp, hs, 4 / hs, 16, 2) + (size_t)2 * 8 * 64 * 4 * sizeof(float);
+}
 // Score-reading dk/dv kernel for heads wider than 128: the column-split
 // eight-wave kernel where the head halves are whole 32-column groups (two
 // waves per SIMD instead of one), else the four-wave asynchronously staged
@@ -431,9 +434,10 @@ int backward_prepare(const float *q, const float *k, const float *v, const float
         dp >= 160 || (unsigned long long)((a->n_key_tiles + 1) / 2) * n_kv_heads * B <= (unsigned long long)st->cus;
     // Wide heads whose halves are whole 32-column groups: eight waves splitting
     // the columns (two per SIMD) instead of the four-wave kernels (C5 and the
-    // reference entry points; ZT_ATTN_DSPLIT=0 forces the four-wave kernels).
-    const bool dsplit = !wide && hs == 2 && (dp == 192 || dp == 256) && dim == dp && aligned &&
-                        dkdv_dspd_bytes(dp) <= st->lds_limit && env_choice("ZT_ATTN_DSPLIT", 1, {0, 1}) == 1;
+    // reference entry points; with no head split, MHA and odd groups;
+    // ZT_ATTN_DSPLIT=0 forces the four-wave kernels).
+    const bool dsplit = !wide && hs <= 2 && (dp == 192 || dp == 256) && dim == dp && aligned &&
+                        dkdv_dspd_bytes(dp, hs) <= st->lds_limit && env_choice("ZT_ATTN_DSPLIT", 1, {0, 1}) == 1;
     const bool dma = !wide && !dsplit && dma_ok && env_choice("ZT_ATTN_DMA", dma_pays ? 1 : 0, {0, 1}) == 1;
     // A group that cannot be split (MHA, odd groups) on the asynchronously
     // staged kernel: two row parts per workgroup instead, eight waves.
@@ -458,7 +462,7 @@ int backward_prepare(const float *q, const float *k, const float *v, const float
     if (wide)
         snprintf(name_dkdv, 64, pf ? "zt_bwd_dkdv8p_d%d_hs2" : "zt_bwd_dkdv8_d%d_hs2", dp);
     else if (dsplit)
-        snprintf(name_dkdv, 64, "zt_bwd_dkdv8pd_d%d_hs2", dp);
+        snprintf(name_dkdv, 64, "zt_bwd_dkdv8pd_d%d_hs%d", dp, hs);
     else if (rsplit)
         snprintf(name_dkdv, 64, "zt_bwd_dkdv_dmar_d%d", dp);
     else
@@ -548,7 +552,8 @@ size_t zt_attn_bwd_dkdv_shmem(int dim) {
     const int dp = pad32(dim);
     size_t most = dkdv_bytes(dp, dp <= 128 ? 4 : 2);
     if (dp <= 128) most = std::max(most, dkdv_bytes(dp, 2, 4, 32, 2));  // eight waves, two 32-row stage buffers
-    if (dp == 192 || dp == 256) most = std::max(most, dkdv_dspd_bytes(dp));  // column-split eight waves
+    if (dp == 192 || dp == 256)  // column-split eight waves
+        most = std::max(most, std::max(dkdv_dspd_bytes(dp, 2), dkdv_dspd_bytes(dp, 1)));
     for (int hs : {1, 2, 4})
         if (!(hs == 4 && dp > 128) && dkdv_dma_bytes(dp, hs) > most) most = dkdv_dma_bytes(dp, hs);
     return most;
