@@ -85,6 +85,7 @@ _NO_DS = {"ZT_ATTN_DSPLIT": "0"}
     {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "1", "ZT_ATTN_HS": "1", "ZT_ATTN_RSPLIT": "1", "ZT_ATTN_BPAIR": "1", **_NO_DS},
     {"ZT_ATTN_W8": "0", "ZT_ATTN_DMA": "1", "ZT_ATTN_HS": "1", "ZT_ATTN_RSPLIT": "0", **_NO_DS},
     {"ZT_ATTN_HS": "1", "ZT_ATTN_DSPLIT": "1"}, {"ZT_ATTN_HS": "1", "ZT_ATTN_DSPLIT": "1", "ZT_ATTN_BPAIR": "1"},
+    {"ZT_ATTN_HS": "1", "ZT_ATTN_DMA": "0"}, {"ZT_ATTN_HS": "1", "ZT_ATTN_DMA": "0", "ZT_ATTN_BPAIR": "1"},
 ])
 @pytest.mark.parametrize("B,T,H,Hkv,D", [(1, 200, 8, 2, 128), (2, 75, 4, 1, 64), (1, 100, 8, 2, 256),
                                          (1, 70, 8, 2, 192), (2, 90, 3, 3, 32), (1, 47, 6, 2, 96),
@@ -206,12 +207,15 @@ def test_block_backward_through_rope_on_the_device(gpu, zt, oracle, threads, T, 
 def test_plan_names_the_column_split_kernel(gpu, zt, monkeypatch):
     """Heads of 192 or 256 take the eight-wave kernel that splits the columns
     over two waves: two head halves of four key blocks for an even head group,
-    one part of four key blocks for MHA and odd groups; ZT_ATTN_DSPLIT=0 turns
-    it off."""
+    one part of four key blocks for MHA and odd groups, which also take it at
+    64 and 128 where the DMA kernel is not chosen; ZT_ATTN_DSPLIT=0 turns it off."""
     assert zt.plan(1, 256, 8, 2, 256)[2] == "zt_bwd_dkdv8pd_d256_hs2"
     assert zt.plan(1, 256, 8, 2, 192)[2] == "zt_bwd_dkdv8pd_d192_hs2"
     assert zt.plan(1, 256, 8, 8, 256)[2] == "zt_bwd_dkdv8pd_d256_hs1"
     assert zt.plan(1, 256, 6, 2, 192)[2] == "zt_bwd_dkdv8pd_d192_hs1"
+    assert zt.plan(2, 2048, 16, 16, 128)[2] == "zt_bwd_dkdv8pd_d128_hs1"   # MHA, grid past the DMA kernel's
+    assert zt.plan(8, 1024, 32, 32, 64)[2] == "zt_bwd_dkdv8pd_d64_hs1"
+    assert zt.plan(4, 1024, 8, 8, 64)[2] == "zt_bwd_dkdv_dmar_d64"        # C2: the row-split DMA kernel
     assert "8pd" not in zt.plan(1, 256, 8, 2, 160)[2] and "8pd" not in zt.plan(1, 256, 8, 8, 250)[2]
     monkeypatch.setenv("ZT_ATTN_DSPLIT", "0")
     assert "8pd" not in zt.plan(1, 256, 8, 2, 256)[2] and "8pd" not in zt.plan(1, 256, 8, 8, 256)[2]

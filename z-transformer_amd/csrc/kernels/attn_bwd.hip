@@ -1192,7 +1192,7 @@ ZT_BWD_DKDV8SD(192) ZT_BWD_DKDV8SD(256)
 // The same column split for the kernel that forms S again (reference entry
 // point and the training path without scores), partial S and dP exchanged;
 // for groups that cannot be halved (MHA, odd groups) four key blocks x two
-// column halves of one part.
+// column halves of one part, also at d = 64 and 128.
 #define ZT_BWD_DKDV8PD(DP)                                                                         \
     extern "C" __global__ void __launch_bounds__(512) zt_bwd_dkdv8pd_d##DP##_hs2(BwdArgs a) {   \
         bwd_dkdv_body<DP, 2, 2, true, 1, false, 2>(a);                                             \
@@ -1201,6 +1201,11 @@ ZT_BWD_DKDV8SD(192) ZT_BWD_DKDV8SD(256)
         bwd_dkdv_body<DP, 1, 4, true, 1, false, 2>(a);                                             \
     }
 ZT_BWD_DKDV8PD(192) ZT_BWD_DKDV8PD(256)
+#define ZT_BWD_DKDV8PD1(DP)                                                                        \
+    extern "C" __global__ void __launch_bounds__(512) zt_bwd_dkdv8pd_d##DP##_hs1(BwdArgs a) {   \
+        bwd_dkdv_body<DP, 1, 4, true, 1, false, 2>(a);                                             \
+    }
+ZT_BWD_DKDV8PD1(64) ZT_BWD_DKDV8PD1(128)
 
 // delta[row] = sum_d o[row, d] * dout[row, d] over the B*T*H rows of dim
 // floats (the row statistic the dk/dv kernel needs, autograd.zig:774-797 as

@@ -432,13 +432,19 @@ int backward_prepare(const float *q, const float *k, const float *v, const float
     // 0.165 -> 0.137 ms) and for wide heads.
     const bool dma_pays =
         dp >= 160 || (unsigned long long)((a->n_key_tiles + 1) / 2) * n_kv_heads * B <= (unsigned long long)st->cus;
-    // Wide heads whose halves are whole 32-column groups: eight waves splitting
-    // the columns (two per SIMD) instead of the four-wave kernels (C5 and the
-    // reference entry points; with no head split, MHA and odd groups;
-    // ZT_ATTN_DSPLIT=0 forces the four-wave kernels).
-    const bool dsplit = !wide && hs <= 2 && (dp == 192 || dp == 256) && dim == dp && aligned &&
-                        dkdv_dspd_bytes(dp, hs) <= st->lds_limit && env_choice("ZT_ATTN_DSPLIT", 1, {0, 1}) == 1;
-    const bool dma = !wide && !dsplit && dma_ok && env_choice("ZT_ATTN_DMA", dma_pays ? 1 : 0, {0, 1}) == 1;
+    const bool dma_want = env_choice("ZT_ATTN_DMA", dma_pays ? 1 : 0, {0, 1}) == 1;
+    // Eight waves splitting the head's columns in two (two waves per SIMD)
+    // where the halves are whole 32-column groups: at d = 192, 256 instead of
+    // the four-wave kernels (C5 and the reference entry points); for a group
+    // that cannot be halved (MHA, odd groups) also at d = 64, 128 where the
+    // asynchronously staged kernel is not chosen (MHA, d = 128, B = 2, T = 2048:
+    // 1.13 -> 0.72 ms; d = 64, B = 8, T = 1024: 0.90 -> 0.80 ms; where that
+    // kernel is chosen it stays ahead, C2 0.105 ms against 0.125 ms).
+    // ZT_ATTN_DSPLIT=0 turns it off.
+    const bool dsplit = !wide && hs <= 2 && dim == dp && aligned && dkdv_dspd_bytes(dp, hs) <= st->lds_limit &&
+                        (dp == 192 || dp == 256 || (hs == 1 && (dp == 64 || dp == 128) && !dma_want)) &&
+                        env_choice("ZT_ATTN_DSPLIT", 1, {0, 1}) == 1;
+    const bool dma = !wide && !dsplit && dma_ok && dma_want;
     // A group that cannot be split (MHA, odd groups) on the asynchronously
     // staged kernel: two row parts per workgroup instead, eight waves.
     const bool rsplit = dma && hs == 1 && dp <= 128 && dkdv_dma_bytes(dp, 2) <= st->lds_limit &&
@@ -554,6 +560,7 @@ size_t zt_attn_bwd_dkdv_shmem(int dim) {
     if (dp <= 128) most = std::max(most, dkdv_bytes(dp, 2, 4, 32, 2));  // eight waves, two 32-row stage buffers
     if (dp == 192 || dp == 256)  // column-split eight waves
         most = std::max(most, std::max(dkdv_dspd_bytes(dp, 2), dkdv_dspd_bytes(dp, 1)));
+    if (dp == 64 || dp == 128) most = std::max(most, dkdv_dspd_bytes(dp, 1));
     for (int hs : {1, 2, 4})
         if (!(hs == 4 && dp > 128) && dkdv_dma_bytes(dp, hs) > most) most = dkdv_dma_bytes(dp, hs);
     return most;
