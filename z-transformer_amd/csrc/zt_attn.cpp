@@ -163,8 +163,10 @@ size_t kv_tile_bytes(int dp, int bk) { return (size_t)2 * bk * (dp + 4) * sizeof
 // Waves per forward / dq workgroup (4 or 8): eight waves share each staged K/V
 // tile between twice as many query rows.  Measured on MI355X: the forward
 // gains when four query heads share a kv group (C3 1.39 -> 1.33 ms, C5 0.84 ->
-// 0.76 ms) and loses for MHA (C2); the dq kernel loses at every shape tried.
-int fwd_waves(int hw) { return env_choice("ZT_ATTN_FWD_W", hw == 4 ? 8 : 4, {4, 8}); }
+// 0.76 ms) and, with the register prefetch, when two do (B = 4, T = 2048, 16
+// heads over 8, d = 128: 0.647 -> 0.581 ms; d = 256, B = 2: 0.711 -> 0.588 ms);
+// it loses for MHA (C2 0.057 -> 0.076 ms); the dq kernel loses at every shape tried.
+int fwd_waves(int hw) { return env_choice("ZT_ATTN_FWD_W", hw >= 2 ? 8 : 4, {4, 8}); }
 
 // Forward kernel name: waves per workgroup, key tile, and for 32-key tiles the
 // register-prefetched variant (ZT_ATTN_FPF=0 turns it off).  Measured on
