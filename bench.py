@@ -117,7 +117,8 @@ def main():
     dk, dv = torch.empty_like(k), torch.empty_like(v)
     rm, rl, rd = (torch.empty(B * T * H, device=dev) for _ in range(3))
     lse, delta = (torch.empty(B * T * H, device=dev) for _ in range(2))
-    work = torch.empty(zt.backward_train_workspace_bytes(B, T, H, Hkv, D) // 4, device=dev)  # delta + dS tiles
+    work_bytes = zt.backward_train_workspace_bytes(B, T, H, Hkv, D)  # delta + the causal dS tiles
+    work = torch.empty(work_bytes // 4, device=dev)
     pairs = B * H * T * (T + 1) / 2          # causal (query, key) pairs over all heads
     unit = 2 * D * pairs                      # FLOPs of one T x T x d causal matmul
     fwd_flop, bwd_flop = 2 * unit, 5 * unit
@@ -209,6 +210,34 @@ def main():
             f"{bwd_tflops:.2f} TFLOP/s ({100 * bwd_tflops / PEAK_MFMA_F32:.1f}%)")
         res[pname] = dict(ms_step=ms_step, value=val, kernels=kernels, fwd_tflops=fwd_tflops,
                           bwd_tflops=bwd_tflops)
+    # The drop-in holder (include/zt_holder.h, device.zig's Attn) on device-resident
+    # buffers: zt_holder_forward + zt_holder_backward as device.Attn.forward(1, 64) +
+    # backward(64) issue them, on the same C3 inputs (copied into the holder's buffers).
+    L = zt.lib()
+    hp = ctypes.c_void_p()
+    if L.zt_holder_init(T, H, Hkv, D, ctypes.byref(hp)) != 0:
+        raise RuntimeError("zt_holder_init refused at C3")
+    # The same seeded inputs, generated into the holder's own buffers, q and k rotated in place.
+    for which, n, seed in ((zt.ZT_BUF_Q, q.numel(), SEEDS["q"]), (zt.ZT_BUF_K, k.numel(), SEEDS["k"]),
+                           (zt.ZT_BUF_V, v.numel(), SEEDS["v"]), (zt.ZT_BUF_DOUT, do.numel(), SEEDS["do"])):
+        if L.zt_fill_normal(L.zt_holder_buffer(hp, which), n, seed, 0.0, 1.0, None):
+            raise RuntimeError("zt_fill_normal refused")
+    hq, hk = L.zt_holder_buffer(hp, zt.ZT_BUF_Q), L.zt_holder_buffer(hp, zt.ZT_BUF_K)
+    if L.zt_rope_qk_forward(hq, hk, hq, hk, B, T, H, Hkv, D, 0, THETA, None):
+        raise RuntimeError("zt_rope_qk_forward refused")
+    L.zt_holder_forget(hp)  # written through the raw pointers
+
+    def holder_step():
+        if L.zt_holder_forward(hp, 1, 64) or L.zt_holder_backward(hp, 64):
+            raise RuntimeError("holder refused")
+
+    for _ in range(args.warmup):
+        holder_step()
+    t_holder = event_time(torch, holder_step, max(3, args.steps))
+    holder_ws = L.zt_holder_workspace_bytes(hp)
+    L.zt_holder_deinit(hp)
+    log(f"C3 step (holder: zt_holder_forward + zt_holder_backward): {t_holder:.3f} ms, "
+        f"{(fwd_flop + bwd_flop) / (t_holder * 1e-3) / 1e12:.2f} TFLOP/s, workspace {holder_ws / 2 ** 30:.2f} GiB")
     ms_step, value = res["train"]["ms_step"], res["train"]["value"]
     kernels, fwd_tflops, bwd_tflops = res["train"]["kernels"], res["train"]["fwd_tflops"], res["train"]["bwd_tflops"]
     exec_flop = sum(kk["flop"] for kk in kernels)   # the matmuls the step's kernels execute
@@ -290,6 +319,27 @@ def main():
     t_step = event_time(torch, dec_step, max(10, args.steps))
     step_gbs = dec_bytes / (t_step * 1e-3) / 1e9
     log(f"C4 decode_step (rope + append + attention): {t_step * 1e3:.1f} us, {step_gbs:.0f} GB/s")
+
+    # The reference's own decode route (src/decode.zig:462): device.Attn.forwardAt(1, 64,
+    # n_keys - 1, n_keys, 1), i.e. zt_attn_forward with T = 1 once per sequence over that
+    # sequence's cache, called straight through the C entry point with resolved pointers.
+    fwd_c = zt.lib().zt_attn_forward
+    sp = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    rows = [(ctypes.c_void_p(qd.data_ptr() + b * H * D * 4), ctypes.c_void_p(kc.data_ptr() + b * n_ctx * Hkv * D * 4),
+             ctypes.c_void_p(vc.data_ptr() + b * n_ctx * Hkv * D * 4), ctypes.c_void_p(od.data_ptr() + b * H * D * 4))
+            for b in range(Bd)]
+
+    def dec_seam():
+        for qb, kb, vb, ob in rows:
+            if fwd_c(qb, kb, vb, ob, 1, H, Hkv, D, 1, 64, n_ctx - 1, n_ctx, sp):
+                raise RuntimeError("zt_attn_forward refused")
+
+    for _ in range(3):
+        dec_seam()
+    t_seam = event_time(torch, dec_seam, max(5, args.steps // 2))
+    seam_gbs = dec_bytes / (t_seam * 1e-3) / 1e9
+    log(f"C4 reference decode seam (zt_attn_forward, T=1, one call per sequence): {t_seam * 1e3:.1f} us, "
+        f"{seam_gbs:.0f} GB/s")
     del kc, vc, qd, od, ws, kn, vn, ws2
 
     # ---------------- dense products (tensor.matmul and its gradients) ----------------
@@ -386,7 +436,14 @@ def main():
         secs = time.perf_counter() - t0
         spairs = B * H * sum(t + 1 for t in range(T - W, T))
         sflop = 14 * D * spairs    # fwd 4d + bwd 10d FLOPs per causal pair, as the GPU figure counts
+        cpu_model = "unknown"
+        try:
+            with open("/proc/cpuinfo") as f:
+                cpu_model = next(l.split(":", 1)[1].strip() for l in f if l.startswith("model name"))
+        except (OSError, StopIteration):
+            pass
         cpu = {"value": round(sflop / secs / 1e12, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
+               "cpu_model": cpu_model, "host_threads": os.cpu_count(),
                "sample": f"C3 query rows {T - W}..{T - 1} ({W} of {T}, all {H} heads, full causal prefix), "
                          f"forward+backward of the C restatement of attention.zig/autograd.zig, 1 thread, "
                          f"{secs:.1f} s", "seconds": round(secs, 2)}
@@ -425,6 +482,12 @@ def main():
         "train_dq_kernel": {"step_path": "zt_attn_forward_train + zt_attn_backward_train",
                             "ms_per_step": round(res["train_dq_kernel"]["ms_step"], 4),
                             "TFLOP/s": round(res["train_dq_kernel"]["value"], 3)},
+        "workspace_bytes": work_bytes,
+        "holder": {"step_path": "zt_holder_forward + zt_holder_backward (device.Attn's forward(1, 64) + backward(64); "
+                                "saved log-sum-exp and scores in the holder's own workspace)",
+                   "ms_per_step": round(t_holder, 4),
+                   "TFLOP/s": round((fwd_flop + bwd_flop) / (t_holder * 1e-3) / 1e12, 3),
+                   "workspace_bytes": holder_ws},
         "reference_abi": {"step_path": "zt_attn_forward + zt_attn_backward",
                           "ms_per_step": round(res["reference_abi"]["ms_step"], 4),
                           "TFLOP/s": round(res["reference_abi"]["value"], 3),
@@ -434,7 +497,10 @@ def main():
         "other_configs": other or None,
         "decode": {"workload": "C4 B=64 n_keys=8192 Hq=32 Hkv=8 d=128 f32", "us": round(t_dec * 1e3, 2),
                    "GB/s": round(dec_gbs, 1), "bytes": dec_bytes, "frac_hbm": round(dec_gbs / PEAK_HBM, 4),
-                   "step_us": round(t_step * 1e3, 2), "step_GB/s": round(step_gbs, 1)},
+                   "step_us": round(t_step * 1e3, 2), "step_GB/s": round(step_gbs, 1),
+                   "reference_seam": {"path": "zt_attn_forward(T=1, q_offset=n_keys-1, n_keys) once per sequence, "
+                                              "as src/decode.zig:462 issues it",
+                                      "us": round(t_seam * 1e3, 2), "GB/s": round(seam_gbs, 1)}},
         "rmsnorm": norm,
         "matmul": mm,
         "calibration": {"mfma_f32_tflops": round(cal_tflops, 1), "read_GB/s": round(cal_gbs, 1),

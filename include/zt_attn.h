@@ -15,6 +15,11 @@
  *     only at the caller's next synchronising call);
  *   - return 1 = refused, with the reason on stderr; never exit();
  *   - outputs (out, dq, dk, dv) are assigned, never accumulated into.
+ * One difference: inputs must be finite.  The kernels remove a masked
+ * (query, key) pair with a zero weight instead of skipping its product, so an
+ * inf or NaN in the K or V (or Q, dout) row of a later position can reach the
+ * results of earlier rows that share its 16- or 32-row tile through 0 * inf,
+ * where the reference's loops never read a masked key (src/attention.zig:117-147).
  * Layout: dense row-major f32 (src/tensor.zig:3-54): q/out/dout/dq are
  * [T, n_heads*dim], k/v/dk/dv are [T, n_kv_heads*dim]; query head h reads kv
  * head h / (n_heads / n_kv_heads) (src/attention.zig:111-112).
@@ -174,12 +179,17 @@ int zt_attn_bwd_dkdv_train(const float *q, const float *k, const float *v, const
  * kernel that rebuilds it: the dk/dv kernel writes dS[b, h, t, s] for every
  * causal pair into the workspace, and dq = dS k / sqrt(d) is then one causal
  * product per head.  Deterministic like the rest.  workspace: 16-byte aligned,
- * at least zt_attn_backward_train_workspace(...) bytes (delta, then B * H * ceil(T/16)^2
- * 16 x 16 tiles of dS: 2 GiB at T = 4096 with 32 heads).  stage: 1 = delta + dk/dv
- * (+ dS), 2 = dq from dS, 3 = both; | ZT_WS_SCORES when the workspace holds
- * the scores zt_attn_forward_train_ws wrote for these q, k (the dk/dv kernel
- * then reads each score tile and overwrites it with dS instead of forming
- * Q K^T again).  No reference counterpart. */
+ * at least zt_attn_backward_train_workspace(...) bytes: delta, then the
+ * causal 16 x 16 tiles of dS only, B * H * nt (nt + 1) / 2 of them with
+ * nt = ceil(T / 16) (1.0 GiB at T = 4096 with 32 heads; 4.0 GiB at T = 8192).
+ * stage: 1 = delta + dk/dv (+ dS), 2 = dq from dS, 3 = both; | ZT_WS_SCORES
+ * when the workspace holds the scores zt_attn_forward_train_ws wrote for these
+ * q, k (the dk/dv kernel then reads each score tile and overwrites it with dS
+ * instead of forming Q K^T again).  ZT_WS_SCORES is single use: nothing
+ * checks what the tiles hold, so it is for the first stage 1 after the
+ * zt_attn_forward_train_ws of the same q, k and shape (after stage 1 the
+ * tiles hold dS, and a plain zt_attn_forward_train writes none); otherwise
+ * dq/dk/dv are wrong and the call still returns 0.  No reference counterpart. */
 #define ZT_WS_SCORES 4
 size_t zt_attn_backward_train_workspace(int B, int T, int n_heads, int n_kv_heads, int dim);
 int zt_attn_backward_train_ws(const float *q, const float *k, const float *v, const float *out, const float *dout,
@@ -256,6 +266,28 @@ int zt_fill_uniform(float *dst, size_t n, uint64_t seed, double lo, double hi, h
  * refused or no device is usable. */
 int zt_attn_plan(int B, int T, int n_heads, int n_kv_heads, int dim, int max_tile, char *fwd, char *dq,
                  char *dkdv, size_t len);
+
+/* Tuning variables (no reference counterpart; process-wide).  Every kernel
+ * variant is chosen from the shape; a sweep or a test may force one with
+ * zt_attn_set_tuning(name, value), and value -1 returns the variable to the
+ * shape rule.  Names and admitted values:
+ *   ZT_ATTN_BK 32|64 (keys per staged K/V tile: forward, dq kernels),
+ *   ZT_ATTN_FWD_W 4|8 (forward waves), ZT_ATTN_FPF 0|1 (forward register
+ *   prefetch), ZT_ATTN_FPAIR 0|1 (paired forward row tiles), ZT_ATTN_QPF 0|1
+ *   and ZT_ATTN_DQ_W 4|8 (dq kernel prefetch and waves), ZT_ATTN_HS 1|2|4
+ *   (dk/dv head split), ZT_ATTN_W8 0|1 and ZT_ATTN_PF 0|1 (eight-wave dk/dv,
+ *   its prefetch), ZT_ATTN_DMA 0|1 (asynchronously staged dk/dv),
+ *   ZT_ATTN_BPAIR 0|1 (paired dq / dk/dv tiles), ZT_ATTN_DSPLIT 0|1
+ *   (column-split dk/dv), ZT_ATTN_RSPLIT 0|1 (row-split dk/dv), ZT_DEC_WGS
+ *   256..32768 (decode workgroup target), ZT_GEMM_TILE 32|64|128 (dense
+ *   product tile), ZT_DQDS_TILE 64|128 (dq-from-dS product tile).
+ * Returns 0, or 1 (reason on stderr) for an unknown name or value.  The
+ * process environment is never read.  Not synchronised with launches in
+ * flight on other threads: set before launching. */
+int zt_attn_set_tuning(const char *name, int value);
+/* The forced value of a tuning variable, -1 when it follows the shape rule,
+ * -2 for an unknown name. */
+int zt_attn_get_tuning(const char *name);
 
 /* Library version string, and the LDS ceiling per workgroup the library read
  * for the current device (0 = no usable device / code object). */

@@ -48,16 +48,54 @@ enum zt_buffer {
 typedef struct zt_holder zt_holder;
 
 /* device.zig:221-299 (Attn.init): refuses via zt_attn_dim_ok and the group
- * check BEFORE allocating; on an allocation failure frees what it took. */
+ * check BEFORE allocating; on an allocation failure frees what it took.
+ * Beyond the eleven buffers it also tries to allocate the score workspace of
+ * the saved-statistics backward (zt_attn_backward_train_workspace bytes for
+ * one sequence of t rows: 1.0 GiB at t = 4096 with 32 heads); a failure there
+ * is no error, the holder then runs without it (see zt_holder_backward). */
 int zt_holder_init(size_t t, size_t n_heads, size_t n_kv_heads, size_t dim, zt_holder **out);
+/* The same holder running the reference pair only (zt_attn_forward then
+ * zt_attn_backward, which rebuilds the statistics): no workspace, and
+ * row_max / row_den hold the reference's max and denominator.  No reference
+ * counterpart (device.zig has one mode). */
+int zt_holder_init_exact(size_t t, size_t n_heads, size_t n_kv_heads, size_t dim, zt_holder **out);
 void zt_holder_deinit(zt_holder *h);                                   /* :328-330 */
-size_t zt_holder_total_bytes(const zt_holder *h);                     /* :332-341 */
+/* :332-341: the eleven buffers' bytes, as the reference counts them (the
+ * workspace is not included: zt_holder_workspace_bytes). */
+size_t zt_holder_total_bytes(const zt_holder *h);
+size_t zt_holder_workspace_bytes(const zt_holder *h);
+/* A buffer's device pointer.  Writing q, k, v, out or row_max through it
+ * between a forward and a backward is not seen by the holder: upload through
+ * zt_holder_upload, run the forward again, or call zt_holder_forget first. */
 float *zt_holder_buffer(const zt_holder *h, int which);
-int zt_holder_forward(const zt_holder *h, int group_q, int max_tile); /* :376-379 */
+/* :376-379.  The whole-cache forward.  It also keeps what the backward would
+ * otherwise rebuild (device.zig:400-402 requires the forward to run first on
+ * the same buffers): row_max receives each row's log-sum-exp and row_den 1.0,
+ * so p = exp(score - row_max) / row_den as in the reference's scratch, and the
+ * scores go to the holder's workspace.  group_q and max_tile are admitted as
+ * zt_attn_forward admits them (an argument it refuses is refused the same way). */
+int zt_holder_forward(const zt_holder *h, int group_q, int max_tile);
+/* :381-398.  forward_at with q_offset 0, n_keys t_cap and t t_cap is
+ * zt_holder_forward; any other (decode-shaped) call runs zt_attn_forward and
+ * drops the saved state. */
 int zt_holder_forward_at(const zt_holder *h, int group_q, int max_tile, int q_offset, int n_keys,
-                         int t);                                      /* :381-398 */
-int zt_holder_backward(const zt_holder *h, int max_tile);             /* :400-406 */
-/* :412-431: bounds-checked against the target buffer's real byte count. */
+                         int t);
+/* :400-406.  dq, dk, dv from the buffers.  After zt_holder_forward with no
+ * upload into q, k, v, out or row_max since, it runs the saved-statistics
+ * backward (zt_attn_backward_train_ws on the holder's workspace, reading the
+ * forward's scores on the first backward after that forward;
+ * zt_attn_backward_train without a workspace); row_del receives
+ * delta = sum_d out * dout.  Otherwise (no forward yet, a decode-shaped
+ * forward_at, an upload, zt_holder_forget, or a holder from
+ * zt_holder_init_exact) it runs zt_attn_backward, which rebuilds the
+ * statistics into row_max / row_den / row_del as the reference does.  dq, dk,
+ * dv agree between the two to rounding (same gates against the CPU twin). */
+int zt_holder_backward(const zt_holder *h, int max_tile);
+/* Drops the forward's saved state (no reference counterpart): the next
+ * backward rebuilds the statistics. */
+void zt_holder_forget(const zt_holder *h);
+/* :412-431: bounds-checked against the target buffer's real byte count.  An
+ * upload into q, k, v, out or row_max drops the forward's saved state. */
 int zt_holder_upload(const zt_holder *h, int which, const float *src, size_t n_floats);
 int zt_holder_download(const zt_holder *h, float *dst, int which, size_t n_floats);
 

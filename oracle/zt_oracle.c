@@ -8,6 +8,9 @@
  *   zto_attention_forward_at   src/cuda/attn_kernels.cu:233-283 (visibility),
  *                              src/attention.zig:111-149 (arithmetic)
  *   zto_attention_backward     src/autograd.zig:636-842
+ *   zto_attention_backward_groups, zto_attention_forward_groups
+ *                              the same two functions over whole kv groups,
+ *                              parallel and bit-identical to the serial forms
  *   zto_attention_row_stats    src/autograd.zig:723-797 (the rebuild), with the
  *                              quantities src/cuda/attn_kernels.cu:520-532 keeps
  *   zto_attn_step              src/decode.zig:326-392
@@ -143,61 +146,77 @@ int zto_attention_forward_at(const float *q, const float *k, const float *v, flo
     return 0;
 }
 
+/* autograd.zig:735-820 for query row t of head h: the softmax rebuilt in f64
+ * (probs[s], s <= t), d p and the Jacobian's dot, p_ds[s] = probs (dp - dot),
+ * and dq[t] narrowed once.  Shared by the serial backward and the two-phase
+ * group backward below, so both form every f64 value by the same operations. */
+static void backward_row(const float *q, const float *k, const float *v, const float *dout, float *dq,
+                         int H, int Hkv, int D, int h, int t, double *probs, double *d_probs, double *p_ds) {
+    const int group = H / Hkv;
+    const int kv = h / group;
+    const double scale = 1.0 / sqrt((double)D); /* :691 */
+    const size_t qc = (size_t)H * D, kc = (size_t)Hkv * D;
+    const float *q_head = q + (size_t)t * qc + (size_t)h * D;
+    const float *dh = dout + (size_t)t * qc + (size_t)h * D;
+    /* Rebuild the softmax (:735-770).  The 8-way unroll there keeps every
+     * value bit for bit what this scalar loop gives (:617-633). */
+    double row_max = -INFINITY;
+    for (int s = 0; s <= t; ++s) {
+        const float *k_head = k + (size_t)s * kc + (size_t)kv * D;
+        double dot = 0;
+        for (int j = 0; j < D; ++j) dot += (double)q_head[j] * (double)k_head[j];
+        probs[s] = dot * scale;
+        row_max = fmax(row_max, probs[s]);
+    }
+    double denom = 0;
+    for (int s = 0; s <= t; ++s) {
+        probs[s] = exp(probs[s] - row_max);
+        denom += probs[s];
+    }
+    for (int s = 0; s <= t; ++s) probs[s] /= denom;
+    /* d p and the Jacobian's dot (:774-797). */
+    double dot_pp = 0;
+    for (int s = 0; s <= t; ++s) {
+        const float *v_head = v + (size_t)s * kc + (size_t)kv * D;
+        double acc = 0;
+        for (int j = 0; j < D; ++j) acc += (double)dh[j] * (double)v_head[j];
+        d_probs[s] = acc;
+        dot_pp += probs[s] * acc;
+    }
+    for (int s = 0; s <= t; ++s) p_ds[s] = probs[s] * (d_probs[s] - dot_pp); /* :799 */
+    /* d q[t]: f64 accumulate of (p_ds * k) * scale, one narrowing (:803-820). */
+    for (int j = 0; j < D; ++j) {
+        double acc = 0;
+        for (int s = 0; s <= t; ++s) acc += p_ds[s] * (double)k[(size_t)s * kc + (size_t)kv * D + j] * scale;
+        dq[(size_t)t * qc + (size_t)h * D + j] = (float)acc;
+    }
+}
+
+/* autograd.zig:821-838: the f32 read-modify-write of one (t, s) term into
+ * dk[s] and dv[s], from row t's p_ds[s] and probs[s]. */
+static void backward_term(const float *q, const float *dout, float *dk, float *dv, int H, int Hkv, int D,
+                          int h, int t, int s, double p_ds_s, double probs_s) {
+    const int kv = h / (H / Hkv);
+    const double scale = 1.0 / sqrt((double)D);
+    const size_t qc = (size_t)H * D, kc = (size_t)Hkv * D;
+    const float *q_head = q + (size_t)t * qc + (size_t)h * D;
+    const float *dh = dout + (size_t)t * qc + (size_t)h * D;
+    float *dk_row = dk + (size_t)s * kc + (size_t)kv * D;
+    float *dv_row = dv + (size_t)s * kc + (size_t)kv * D;
+    for (int j = 0; j < D; ++j) {
+        dk_row[j] += (float)(p_ds_s * (double)q_head[j] * scale);
+        dv_row[j] += (float)(probs_s * (double)dh[j]);
+    }
+}
+
 /* autograd.zig:723-840 for one (batch, head), rows [t_begin, t_end). */
 static void backward_head(const float *q, const float *k, const float *v, const float *dout,
                           float *dq, float *dk, float *dv, int T, int H, int Hkv, int D, int h,
                           int t_begin, int t_end, double *probs, double *d_probs, double *p_ds) {
     (void)T;
-    const int group = H / Hkv;
-    const int kv = h / group;
-    const double scale = 1.0 / sqrt((double)D); /* :691 */
-    const size_t qc = (size_t)H * D, kc = (size_t)Hkv * D;
     for (int t = t_begin; t < t_end; ++t) {
-        const float *q_head = q + (size_t)t * qc + (size_t)h * D;
-        const float *dh = dout + (size_t)t * qc + (size_t)h * D;
-        /* Rebuild the softmax (:735-770).  The 8-way unroll there keeps every
-         * value bit for bit what this scalar loop gives (:617-633). */
-        double row_max = -INFINITY;
-        for (int s = 0; s <= t; ++s) {
-            const float *k_head = k + (size_t)s * kc + (size_t)kv * D;
-            double dot = 0;
-            for (int j = 0; j < D; ++j) dot += (double)q_head[j] * (double)k_head[j];
-            probs[s] = dot * scale;
-            row_max = fmax(row_max, probs[s]);
-        }
-        double denom = 0;
-        for (int s = 0; s <= t; ++s) {
-            probs[s] = exp(probs[s] - row_max);
-            denom += probs[s];
-        }
-        for (int s = 0; s <= t; ++s) probs[s] /= denom;
-        /* d p and the Jacobian's dot (:774-797). */
-        double dot_pp = 0;
-        for (int s = 0; s <= t; ++s) {
-            const float *v_head = v + (size_t)s * kc + (size_t)kv * D;
-            double acc = 0;
-            for (int j = 0; j < D; ++j) acc += (double)dh[j] * (double)v_head[j];
-            d_probs[s] = acc;
-            dot_pp += probs[s] * acc;
-        }
-        for (int s = 0; s <= t; ++s) p_ds[s] = probs[s] * (d_probs[s] - dot_pp); /* :799 */
-        /* d q[t]: f64 accumulate of (p_ds * k) * scale, one narrowing (:803-820). */
-        for (int j = 0; j < D; ++j) {
-            double acc = 0;
-            for (int s = 0; s <= t; ++s) acc += p_ds[s] * (double)k[(size_t)s * kc + (size_t)kv * D + j] * scale;
-            dq[(size_t)t * qc + (size_t)h * D + j] = (float)acc;
-        }
-        /* d k, d v: f32 read-modify-write per term (:821-838). */
-        for (int s = 0; s <= t; ++s) {
-            float *dk_row = dk + (size_t)s * kc + (size_t)kv * D;
-            float *dv_row = dv + (size_t)s * kc + (size_t)kv * D;
-            const double p_ds_s = p_ds[s];
-            const double probs_s = probs[s];
-            for (int j = 0; j < D; ++j) {
-                dk_row[j] += (float)(p_ds_s * (double)q_head[j] * scale);
-                dv_row[j] += (float)(probs_s * (double)dh[j]);
-            }
-        }
+        backward_row(q, k, v, dout, dq, H, Hkv, D, h, t, probs, d_probs, p_ds);
+        for (int s = 0; s <= t; ++s) backward_term(q, dout, dk, dv, H, Hkv, D, h, t, s, p_ds[s], probs[s]);
     }
 }
 
@@ -231,6 +250,115 @@ int zto_attention_backward_mt(const float *q, const float *k, const float *v, co
             backward_head(q + b * qs, k + b * ks, v + b * ks, dout + b * qs, dq + b * qs, dk + b * ks,
                           dv + b * ks, T, H, Hkv, D, h, t_begin, t_end, buf, buf + n, buf + 2 * n);
         free(buf);
+    }
+    (void)n_threads;
+    return 0;
+}
+
+/* The whole-group backward in two phases.  Phase 1 (parallel over rows):
+ * backward_row for every (sequence, head of the groups, row t), keeping the
+ * row's probs and p_ds in a packed lower triangle.  Phase 2 (parallel over
+ * blocks of 8 key rows s): backward_term for every term that reaches those
+ * rows, heads ascending, then t ascending -- for each dk/dv element the same
+ * terms in the same order as the serial h -> t -> s loop nest (:723-838), so
+ * every f32 rounding of the read-modify-write chain is the serial one. */
+int zto_attention_backward_groups(const float *q, const float *k, const float *v, const float *dout,
+                                  float *dq, float *dk, float *dv, int B, int T, int H, int Hkv, int D,
+                                  int kv_begin, int kv_end, int n_threads) {
+    if (!head_config_ok(H, Hkv, D)) return 1;
+    if (T < 0 || B < 0 || kv_begin < 0 || kv_end > Hkv || kv_begin > kv_end) return 2;
+    if (T == 0 || B == 0 || kv_begin == kv_end) return 0;
+    const int group = H / Hkv;
+    const int n_h = (kv_end - kv_begin) * group;  /* heads of the selected groups */
+    const size_t qs = (size_t)T * H * D, ks = (size_t)T * Hkv * D, kc = (size_t)Hkv * D;
+    const size_t tri = (size_t)T * (size_t)(T + 1) / 2;
+    double *pp = (double *)malloc(sizeof(double) * tri * (size_t)n_h * (size_t)B);
+    double *pd = (double *)malloc(sizeof(double) * tri * (size_t)n_h * (size_t)B);
+    if (!pp || !pd) {
+        free(pp);
+        free(pd);
+        return 3;
+    }
+    const size_t cols = sizeof(float) * (size_t)(kv_end - kv_begin) * D;  /* the groups' columns of a row */
+    for (int b = 0; b < B; ++b) {
+        for (int s = 0; s < T; ++s) {
+            memset(dk + b * ks + (size_t)s * kc + (size_t)kv_begin * D, 0, cols);
+            memset(dv + b * ks + (size_t)s * kc + (size_t)kv_begin * D, 0, cols);
+        }
+    }
+#ifdef _OPENMP
+    const int nt = n_threads > 0 ? n_threads : omp_get_max_threads();
+#endif
+    /* Phase 1: rows, heaviest (latest) first. */
+    const long long rows = (long long)B * n_h * T;
+#ifdef _OPENMP
+#pragma omp parallel num_threads(nt)
+#endif
+    {
+        double *d_probs = (double *)malloc(sizeof(double) * (size_t)T);
+#ifdef _OPENMP
+#pragma omp for schedule(dynamic, 4)
+#endif
+        for (long long job = 0; job < rows; ++job) {
+            const int t = T - 1 - (int)(job % T);
+            const int hi = (int)((job / T) % n_h), b = (int)(job / ((long long)T * n_h));
+            const int h = kv_begin * group + hi;
+            const size_t blk = ((size_t)b * n_h + hi) * tri + (size_t)t * (size_t)(t + 1) / 2;
+            backward_row(q + b * qs, k + b * ks, v + b * ks, dout + b * qs, dq + b * qs, H, Hkv, D, h, t, pp + blk,
+                         d_probs, pd + blk);
+        }
+        free(d_probs);
+    }
+    /* Phase 2: blocks of 8 key rows; within a block, per kv group, heads
+     * ascending, t ascending, the block's rows s <= t. */
+    const int n_sb = (T + 7) / 8;
+    const long long jobs = (long long)B * n_sb;
+#ifdef _OPENMP
+#pragma omp parallel for schedule(dynamic, 1) num_threads(nt)
+#endif
+    for (long long job = 0; job < jobs; ++job) {
+        const int b = (int)(job / n_sb), s0 = (int)(job % n_sb) * 8, s1 = s0 + 8 < T ? s0 + 8 : T;
+        for (int kvh = kv_begin; kvh < kv_end; ++kvh)
+            for (int h = kvh * group; h < (kvh + 1) * group; ++h) {
+                const int hi = h - kv_begin * group;
+                for (int t = s0; t < T; ++t) {
+                    const size_t blk = ((size_t)b * n_h + hi) * tri + (size_t)t * (size_t)(t + 1) / 2;
+                    const int s_hi = t + 1 < s1 ? t + 1 : s1;
+                    for (int s = s0; s < s_hi; ++s)
+                        backward_term(q + b * qs, dout + b * qs, dk + b * ks, dv + b * ks, H, Hkv, D, h, t, s,
+                                      pd[blk + s], pp[blk + s]);
+                }
+            }
+    }
+    free(pp);
+    free(pd);
+    (void)n_threads;
+    return 0;
+}
+
+/* All rows of the heads of kv groups [kv_begin, kv_end), parallel over
+ * 16-row chunks: rows are independent (attention.zig:111-149), so this is
+ * bit-identical to zto_attention_forward over those heads. */
+int zto_attention_forward_groups(const float *q, const float *k, const float *v, float *out, int B, int T,
+                                 int H, int Hkv, int D, int kv_begin, int kv_end, int n_threads) {
+    if (!head_config_ok(H, Hkv, D)) return 1;
+    if (T < 0 || B < 0 || kv_begin < 0 || kv_end > Hkv || kv_begin > kv_end) return 2;
+    const int group = H / Hkv;
+    const int n_h = (kv_end - kv_begin) * group, n_c = (T + 15) / 16;
+    const size_t qs = (size_t)T * H * D, ks = (size_t)T * Hkv * D;
+    const long long jobs = (long long)B * n_h * n_c;
+#ifdef _OPENMP
+    const int nt = n_threads > 0 ? n_threads : omp_get_max_threads();
+#pragma omp parallel for schedule(dynamic, 1) num_threads(nt)
+#endif
+    for (long long job = 0; job < jobs; ++job) {
+        const int c = n_c - 1 - (int)(job % n_c);
+        const int hi = (int)((job / n_c) % n_h), b = (int)(job / ((long long)n_c * n_h));
+        double *scores = (double *)malloc(sizeof(double) * (size_t)T);
+        const int t1 = 16 * c + 16 < T ? 16 * c + 16 : T;
+        forward_head(q + b * qs, k + b * ks, v + b * ks, out + b * qs, T, H, Hkv, D, kv_begin * group + hi, 16 * c,
+                     t1, scores);
+        free(scores);
     }
     (void)n_threads;
     return 0;

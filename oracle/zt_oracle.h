@@ -62,6 +62,24 @@ int zto_attention_backward_mt(const float *q, const float *k, const float *v, co
                               float *dq, float *dk, float *dv, int B, int T, int H, int Hkv, int D,
                               int t_begin, int t_end, int n_threads);
 
+/* attentionBackward for every row of the heads of kv groups [kv_begin,
+ * kv_end) (whole groups: a kv group's dk/dv receive terms only from its own
+ * heads).  dq of those heads (all rows) and dk/dv of those groups (zeroed
+ * first) are written; everything else is untouched.  Two phases, parallel:
+ * the per-row softmax rebuild, then dk/dv in blocks of key rows with each
+ * element's f32 read-modify-write chain in the serial h -> t -> s order, so
+ * the result is bit-identical to zto_attention_backward (tested).  Holds
+ * 16 * B * group * (kv_end - kv_begin) * T (T + 1) / 2 bytes while it runs.
+ * Returns 3 if that memory cannot be had. */
+int zto_attention_backward_groups(const float *q, const float *k, const float *v, const float *dout,
+                                  float *dq, float *dk, float *dv, int B, int T, int H, int Hkv, int D,
+                                  int kv_begin, int kv_end, int n_threads);
+
+/* attention.forward for every row of the heads of kv groups [kv_begin, kv_end),
+ * parallel over 16-row chunks; bit-identical to zto_attention_forward. */
+int zto_attention_forward_groups(const float *q, const float *k, const float *v, float *out, int B, int T,
+                                 int H, int Hkv, int D, int kv_begin, int kv_end, int n_threads);
+
 /* Per-row softmax statistics the device backward keeps as scratch
  * (src/cuda/attn_kernels.cu:520-532): row_max = max_s score, row_den =
  * sum_s exp(score - row_max), row_del = sum_s p * dp, all in f64 from the

@@ -28,6 +28,8 @@ def lib():
             "zto_attention_backward": (I, [P] * 7 + [I] * 7),
             "zto_attention_backward_mt": (I, [P] * 7 + [I] * 8),
             "zto_attention_row_stats": (I, [P] * 7 + [I] * 5),
+            "zto_attention_backward_groups": (I, [P] * 7 + [I] * 8),
+            "zto_attention_forward_groups": (I, [P] * 4 + [I] * 8),
             "zto_attn_step": (I, [P] * 5 + [I] * 5),
             "zto_attn_step_mt": (I, [P] * 5 + [I] * 6),
             "zto_rmsnorm": (None, [P, P, P, I, I, D]),
@@ -91,6 +93,31 @@ def attention_backward(q, k, v, dout, B, T, H, Hkv, D, t_begin=0, t_end=None, th
     dv = np.zeros(B * T * Hkv * D, np.float32)
     rc = lib().zto_attention_backward_mt(_p(q), _p(k), _p(v), _p(dout), _p(dq), _p(dk), _p(dv), B, T, H, Hkv, D,
                                          t_begin, t_end, threads)
+    if rc:
+        raise OracleRefused(f"rc={rc}")
+    return dq, dk, dv
+
+
+def attention_forward_groups(q, k, v, B, T, H, Hkv, D, kv_begin, kv_end, threads=16, out=None):
+    """attention.forward for every row of the heads of kv groups [kv_begin, kv_end);
+    the other heads' columns of `out` are left as given (zeros by default)."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    out = np.zeros(B * T * H * D, np.float32) if out is None else out
+    rc = lib().zto_attention_forward_groups(_p(q), _p(k), _p(v), _p(out), B, T, H, Hkv, D, kv_begin, kv_end, threads)
+    if rc:
+        raise OracleRefused(f"rc={rc}")
+    return out
+
+
+def attention_backward_groups(q, k, v, dout, B, T, H, Hkv, D, kv_begin, kv_end, threads=16):
+    """attentionBackward over whole kv groups [kv_begin, kv_end), bit-identical to
+    attention_backward there; returns (dq, dk, dv), zero outside those groups."""
+    q, k, v, dout = _f32(q), _f32(k), _f32(v), _f32(dout)
+    dq = np.zeros(B * T * H * D, np.float32)
+    dk = np.zeros(B * T * Hkv * D, np.float32)
+    dv = np.zeros(B * T * Hkv * D, np.float32)
+    rc = lib().zto_attention_backward_groups(_p(q), _p(k), _p(v), _p(dout), _p(dq), _p(dk), _p(dv), B, T, H, Hkv, D,
+                                             kv_begin, kv_end, threads)
     if rc:
         raise OracleRefused(f"rc={rc}")
     return dq, dk, dv

@@ -49,6 +49,23 @@ def gpu(zt):
     return torch
 
 
+@pytest.fixture
+def tune(zt):
+    """Forces kernel variants for one test through the library's tuning
+    variables (zt_attn_set_tuning) and returns every one it set to the shape
+    rule afterwards.  Call as tune({"ZT_ATTN_BPAIR": 1, ...})."""
+    touched = []
+
+    def apply(settings):
+        for name, value in settings.items():
+            zt.set_tuning(name, int(value))
+            touched.append(name)
+
+    yield apply
+    for name in touched:
+        zt.set_tuning(name, -1)
+
+
 @pytest.fixture(scope="session")
 def threads():
     return min(16, os.cpu_count() or 1)

@@ -283,3 +283,41 @@ def test_holder_init_refuses_before_allocating(zt):
     assert L.zt_holder_init(8, 65536, 1, 32, ctypes.byref(h)) == zt.ZT_CONFIG_REFUSED
     assert L.zt_holder_init(1 << 31, 4, 2, 32, ctypes.byref(h)) == zt.ZT_SHAPE_TOO_LARGE
     assert h.value is None
+
+
+def test_tuning_variables_are_set_only_through_the_setter(zt, capfd):
+    """Kernel variants follow the shape unless zt_attn_set_tuning forces one;
+    unknown names and values outside a variable's admitted set are refused,
+    and -1 returns a variable to its shape rule."""
+    L = zt.lib()
+    assert L.zt_attn_get_tuning(b"ZT_ATTN_BPAIR") == -1
+    assert L.zt_attn_set_tuning(b"ZT_ATTN_BPAIR", 0) == 0
+    assert L.zt_attn_get_tuning(b"ZT_ATTN_BPAIR") == 0
+    assert L.zt_attn_set_tuning(b"ZT_ATTN_BPAIR", 2) == 1
+    assert "not a value of the tuning variable ZT_ATTN_BPAIR" in capfd.readouterr().err
+    assert L.zt_attn_get_tuning(b"ZT_ATTN_BPAIR") == 0
+    assert L.zt_attn_set_tuning(b"ZT_ATTN_BPAIR", -1) == 0
+    assert L.zt_attn_get_tuning(b"ZT_ATTN_BPAIR") == -1
+    assert L.zt_attn_set_tuning(b"ZT_NO_SUCH_KNOB", 1) == 1
+    assert "is not a tuning variable" in capfd.readouterr().err
+    assert L.zt_attn_get_tuning(b"ZT_NO_SUCH_KNOB") == -2
+    assert L.zt_attn_set_tuning(None, 1) == 1
+    assert L.zt_attn_set_tuning(b"ZT_DEC_WGS", 32768) == 0 and L.zt_attn_get_tuning(b"ZT_DEC_WGS") == 32768
+    assert L.zt_attn_set_tuning(b"ZT_DEC_WGS", -1) == 0
+
+
+def test_library_reads_no_environment_variable(zt):
+    """No getenv reaches a launch: the shared object does not import it."""
+    import subprocess
+    out = subprocess.run(["nm", "-D", "--undefined-only", zt.LIB_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    assert "getenv" not in out
+
+
+def test_train_workspace_holds_only_the_causal_tiles(zt):
+    """B * H * nt (nt + 1) / 2 tiles of 16 x 16 after delta (1.0 GiB at C3, not 2)."""
+    for B, T, H, Hkv, D in ((1, 4096, 32, 8, 128), (2, 2048, 16, 4, 256), (1, 33, 4, 2, 32)):
+        nt = (T + 15) // 16
+        delta = (B * T * H * 4 + 255) // 256 * 256
+        assert zt.backward_train_workspace_bytes(B, T, H, Hkv, D) == delta + B * H * nt * (nt + 1) // 2 * 1024
+    assert zt.backward_train_workspace_bytes(1, 4096, 32, 8, 128) < 1.1 * 2 ** 30

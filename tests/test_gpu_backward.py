@@ -90,14 +90,13 @@ _NO_DS = {"ZT_ATTN_DSPLIT": "0"}
 @pytest.mark.parametrize("B,T,H,Hkv,D", [(1, 200, 8, 2, 128), (2, 75, 4, 1, 64), (1, 100, 8, 2, 256),
                                          (1, 70, 8, 2, 192), (2, 90, 3, 3, 32), (1, 47, 6, 2, 96),
                                          (1, 100, 4, 4, 256), (2, 61, 6, 2, 192)])
-def test_backward_every_dkdv_variant(gpu, zt, oracle, threads, monkeypatch, env, B, T, H, Hkv, D):
+def test_backward_every_dkdv_variant(gpu, zt, oracle, threads, tune, env, B, T, H, Hkv, D):
     """Each dk/dv kernel variant (eight-wave, register-staged, asynchronously
     staged, columns split over two waves for d = 192 / 256, rows split over
     two parts for unsplit groups; 1/2/4-way head splits; paired or single key
     tiles per workgroup), forced through the library's tuning variables,
     matches the twin."""
-    for k_, v_ in env.items():
-        monkeypatch.setenv(k_, v_)
+    tune(env)
     (q, k, v, do), (dq, dk, dv, *_) = _run(gpu, zt, B, T, H, Hkv, D)
     rq, rk, rv = oracle.attention_backward(q, k, v, do, B, T, H, Hkv, D, threads=threads)
     assert max(rel_err(dq, rq), rel_err(dk, rk), rel_err(dv, rv)) <= BWD_REL
@@ -111,11 +110,10 @@ def test_backward_every_dkdv_variant(gpu, zt, oracle, threads, monkeypatch, env,
     {"ZT_ATTN_BK": "32", "ZT_ATTN_QPF": "1", "ZT_ATTN_DQ_W": "4", "ZT_ATTN_BPAIR": "0"},
 ])
 @pytest.mark.parametrize("B,T,H,Hkv,D", [(1, 200, 8, 2, 128), (2, 75, 4, 1, 64), (1, 61, 6, 3, 66)])
-def test_backward_every_dq_variant(gpu, zt, oracle, threads, monkeypatch, env, B, T, H, Hkv, D):
+def test_backward_every_dq_variant(gpu, zt, oracle, threads, tune, env, B, T, H, Hkv, D):
     """Each dq kernel variant (four or eight waves, 32- or 64-key tiles, with
     and without register prefetch of the next K/V tile) matches the twin."""
-    for k_, v_ in env.items():
-        monkeypatch.setenv(k_, v_)
+    tune(env)
     (q, k, v, do), (dq, dk, dv, *_) = _run(gpu, zt, B, T, H, Hkv, D)
     rq, rk, rv = oracle.attention_backward(q, k, v, do, B, T, H, Hkv, D, threads=threads)
     assert max(rel_err(dq, rq), rel_err(dk, rk), rel_err(dv, rv)) <= BWD_REL
@@ -204,7 +202,7 @@ def test_block_backward_through_rope_on_the_device(gpu, zt, oracle, threads, T, 
     assert rel_err(dq, want_q) > 10 * BWD_REL
 
 
-def test_plan_names_the_column_split_kernel(gpu, zt, monkeypatch):
+def test_plan_names_the_column_split_kernel(gpu, zt, tune):
     """Heads of 192 or 256 take the eight-wave kernel that splits the columns
     over two waves: two head halves of four key blocks for an even head group,
     one part of four key blocks for MHA and odd groups, which also take it at
@@ -217,5 +215,5 @@ def test_plan_names_the_column_split_kernel(gpu, zt, monkeypatch):
     assert zt.plan(8, 1024, 32, 32, 64)[2] == "zt_bwd_dkdv8pd_d64_hs1"
     assert zt.plan(4, 1024, 8, 8, 64)[2] == "zt_bwd_dkdv_dmar_d64"        # C2: the row-split DMA kernel
     assert "8pd" not in zt.plan(1, 256, 8, 2, 160)[2] and "8pd" not in zt.plan(1, 256, 8, 8, 250)[2]
-    monkeypatch.setenv("ZT_ATTN_DSPLIT", "0")
+    tune({"ZT_ATTN_DSPLIT": "0"})
     assert "8pd" not in zt.plan(1, 256, 8, 2, 256)[2] and "8pd" not in zt.plan(1, 256, 8, 8, 256)[2]

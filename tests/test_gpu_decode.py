@@ -31,11 +31,11 @@ def test_decode_c4(gpu, zt, oracle, threads):
 
 
 @pytest.mark.parametrize("wgs", ["256", "512", "2048", "32768"])
-def test_decode_any_split(gpu, zt, oracle, threads, monkeypatch, wgs):
+def test_decode_any_split(gpu, zt, oracle, threads, tune, wgs):
     """However the key axis is split (the workgroup target, a tuning
     variable), the answer holds: 8 sequences x 8 kv heads of 2000 rows run in
     4, 8 or 32 chunks per sequence (the C4 test runs one chunk per sequence)."""
-    monkeypatch.setenv("ZT_DEC_WGS", wgs)
+    tune({"ZT_DEC_WGS": wgs})
     B, n_ctx, H, Hkv, D = 8, 2000, 32, 8, 128
     n_keys = [2000, 1999, 1500, 1024, 1023, 600, 65, 1]
     q, kc, vc, out = _decode(gpu, zt, B, n_ctx, H, Hkv, D, n_keys)

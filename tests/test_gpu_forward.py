@@ -50,8 +50,8 @@ def test_forward_matches_twin(gpu, zt, oracle, threads, B, T, H, Hkv, D):
 
 @pytest.mark.parametrize("bk", ["32", "64"])
 @pytest.mark.parametrize("B,T,H,Hkv,D", [(1, 150, 8, 2, 128), (2, 70, 4, 4, 256), (1, 99, 6, 3, 66)])
-def test_forward_both_key_tiles(gpu, zt, oracle, monkeypatch, bk, B, T, H, Hkv, D):
-    monkeypatch.setenv("ZT_ATTN_BK", bk)
+def test_forward_both_key_tiles(gpu, zt, oracle, tune, bk, B, T, H, Hkv, D):
+    tune({"ZT_ATTN_BK": bk})
     q, k, v = _inputs(gpu, zt, B, T, H, Hkv, D)
     out = _run(gpu, zt, q, k, v, B, T, H, Hkv, D)
     ref = oracle.attention_forward(host(q), host(k), host(v), B, T, H, Hkv, D)
@@ -63,13 +63,12 @@ def test_forward_both_key_tiles(gpu, zt, oracle, monkeypatch, bk, B, T, H, Hkv, 
                                  {"ZT_ATTN_FPF": "1", "ZT_ATTN_FWD_W": "8", "ZT_ATTN_FPAIR": "0"},
                                  {"ZT_ATTN_FPF": "0", "ZT_ATTN_FWD_W": "4", "ZT_ATTN_FPAIR": "0"}])
 @pytest.mark.parametrize("B,T,H,Hkv,D", [(1, 150, 8, 2, 128), (2, 70, 4, 4, 256), (1, 99, 6, 3, 66), (1, 45, 4, 1, 32)])
-def test_forward_every_variant(gpu, zt, oracle, monkeypatch, env, B, T, H, Hkv, D):
+def test_forward_every_variant(gpu, zt, oracle, tune, env, B, T, H, Hkv, D):
     """Four- and eight-wave workgroups, with and without register prefetch of
     the next K/V tile, paired or single row tiles per workgroup, forced through
     the library's tuning variables."""
-    monkeypatch.setenv("ZT_ATTN_BK", "32")
-    for k_, v_ in env.items():
-        monkeypatch.setenv(k_, v_)
+    tune({"ZT_ATTN_BK": "32"})
+    tune(env)
     q, k, v = _inputs(gpu, zt, B, T, H, Hkv, D)
     out = _run(gpu, zt, q, k, v, B, T, H, Hkv, D)
     ref = oracle.attention_forward(host(q), host(k), host(v), B, T, H, Hkv, D)

@@ -76,3 +76,124 @@ def test_holder_decode_seam_over_a_filling_cache(gpu, zt, oracle):
             assert _rel(out, ref) <= 1e-4, pos
     finally:
         zt.lib().zt_holder_deinit(p)
+
+
+def _fill(zt, p, which, n, seed, sigma=1.0):
+    assert zt.lib().zt_fill_normal(zt.lib().zt_holder_buffer(p, which), n, seed, 0.0, sigma, None) == 0
+
+
+def _inputs(zt, p, T, H, Hkv, D, rope=False):
+    from gpuhelp import SEED_DO, SEED_K, SEED_Q, SEED_V, THETA
+    L = zt.lib()
+    _fill(zt, p, zt.ZT_BUF_Q, T * H * D, SEED_Q)
+    _fill(zt, p, zt.ZT_BUF_K, T * Hkv * D, SEED_K)
+    _fill(zt, p, zt.ZT_BUF_V, T * Hkv * D, SEED_V)
+    _fill(zt, p, zt.ZT_BUF_DOUT, T * H * D, SEED_DO)
+    if rope:
+        qb, kb = L.zt_holder_buffer(p, zt.ZT_BUF_Q), L.zt_holder_buffer(p, zt.ZT_BUF_K)
+        assert L.zt_rope_qk_forward(qb, kb, qb, kb, 1, T, H, Hkv, D, 0, THETA, None) == 0
+    # Written through the raw pointers: drop any saved state, as zt_holder_buffer's contract asks.
+    L.zt_holder_forget(p)
+    return [_down(zt, p, w, n) for w, n in ((zt.ZT_BUF_Q, T * H * D), (zt.ZT_BUF_K, T * Hkv * D),
+                                           (zt.ZT_BUF_V, T * Hkv * D), (zt.ZT_BUF_DOUT, T * H * D))]
+
+
+def _grads(zt, p, T, H, Hkv, D):
+    return [_down(zt, p, w, n) for w, n in ((zt.ZT_BUF_DQ, T * H * D), (zt.ZT_BUF_DK, T * Hkv * D),
+                                           (zt.ZT_BUF_DV, T * Hkv * D))]
+
+
+@pytest.mark.parametrize("exact", [False, True], ids=["saved-statistics", "exact"])
+def test_holder_scratch_contract_in_both_modes(gpu, zt, oracle, exact):
+    """After forward + backward the row buffers satisfy the reference's scratch
+    contract p = exp(s - row_max) / row_den with row_del = delta: the exact
+    holder holds the max and the denominator, the default holder the
+    log-sum-exp and 1.0 (the same p)."""
+    T, H, Hkv, D = 200, 8, 2, 64
+    p = ctypes.c_void_p()
+    init = zt.lib().zt_holder_init_exact if exact else zt.lib().zt_holder_init
+    assert init(T, H, Hkv, D, ctypes.byref(p)) == 0
+    try:
+        assert (zt.lib().zt_holder_workspace_bytes(p) == 0) == exact
+        q, k, v, do = _inputs(zt, p, T, H, Hkv, D)
+        assert zt.lib().zt_holder_forward(p, 1, 64) == 0
+        assert zt.lib().zt_holder_backward(p, 64) == 0
+        m, l, d = oracle.attention_row_stats(q, k, v, do, 1, T, H, Hkv, D)
+        rm, rl, rd = (_down(zt, p, w, T * H) for w in (zt.ZT_BUF_ROW_MAX, zt.ZT_BUF_ROW_DEN, zt.ZT_BUF_ROW_DEL))
+        if exact:
+            assert np.max(np.abs(rm - m)) <= 1e-4 * max(1.0, np.abs(m).max())
+            assert np.max(np.abs(rl - l) / l) <= 1e-4
+        else:
+            lse = m + np.log(l)
+            assert np.max(np.abs(rm - lse)) <= 1e-5 * max(1.0, np.abs(lse).max())
+            assert np.all(rl == 1.0)
+        assert np.max(np.abs(rd - d)) <= 1e-4 * max(1.0, np.abs(d).max())
+        rq, rk, rv = oracle.attention_backward(q, k, v, do, 1, T, H, Hkv, D)
+        for got, want in zip(_grads(zt, p, T, H, Hkv, D), (rq, rk, rv)):
+            assert _rel(got, want) <= 1e-3
+    finally:
+        zt.lib().zt_holder_deinit(p)
+
+
+def test_holder_backward_follows_what_the_buffers_hold(gpu, zt, oracle):
+    """The saved state is used only while it describes the buffers: a second
+    backward, a backward after new q was uploaded, after a decode-shaped
+    forward_at and after zt_holder_forget all give the twin's gradients for
+    what the buffers hold."""
+    T, H, Hkv, D = 150, 4, 2, 128
+    p = _holder(zt, T, H, Hkv, D)
+    L = zt.lib()
+    try:
+        q, k, v, do = _inputs(zt, p, T, H, Hkv, D)
+
+        def check(qq):
+            rq, rk, rv = oracle.attention_backward(qq, k, v, do, 1, T, H, Hkv, D)
+            for got, want in zip(_grads(zt, p, T, H, Hkv, D), (rq, rk, rv)):
+                assert _rel(got, want) <= 1e-3
+
+        assert L.zt_holder_forward(p, 1, 64) == 0 and L.zt_holder_backward(p, 64) == 0
+        check(q)
+        assert L.zt_holder_backward(p, 64) == 0      # the score tiles now hold dS: rebuilt from lse
+        check(q)
+        q2 = (q * np.float32(0.5)).astype(np.float32)
+        assert L.zt_holder_forward(p, 1, 64) == 0
+        assert _up(zt, p, zt.ZT_BUF_Q, q2) == 0      # new q after the forward: lse and scores are stale
+        assert L.zt_holder_backward(p, 64) == 0
+        check(q2)
+        assert L.zt_holder_forward(p, 1, 64) == 0
+        assert L.zt_holder_forward_at(p, 1, 64, T - 1, T, 1) == 0   # a decode step over the same buffers
+        assert L.zt_holder_backward(p, 64) == 0
+        check(q2)
+        assert L.zt_holder_forward(p, 1, 64) == 0
+        L.zt_holder_forget(p)
+        assert L.zt_holder_backward(p, 64) == 0
+        check(q2)
+        # A group_q the reference refuses is refused by the fast forward too.
+        assert L.zt_holder_forward(p, 65, 64) == zt.ZT_CONFIG_REFUSED
+        assert L.zt_holder_forward(p, 1, 0) == zt.ZT_CONFIG_REFUSED
+    finally:
+        L.zt_holder_deinit(p)
+
+
+def test_holder_at_c3_whole_kv_group(gpu, zt, oracle, threads):
+    """The drop-in holder at the headline shape (C3, RoPE'd Q/K): its default
+    forward + backward graded on every row of kv group 7 against the twin."""
+    T, H, Hkv, D, kv = 4096, 32, 8, 128, 7
+    p = _holder(zt, T, H, Hkv, D)
+    L = zt.lib()
+    try:
+        q, k, v, do = _inputs(zt, p, T, H, Hkv, D, rope=True)
+        assert L.zt_holder_forward(p, 1, 64) == 0 and L.zt_holder_backward(p, 64) == 0
+        out = _down(zt, p, zt.ZT_BUF_OUT, T * H * D)
+        dq, dk, dv = _grads(zt, p, T, H, Hkv, D)
+        ro = oracle.attention_forward_groups(q, k, v, 1, T, H, Hkv, D, kv, kv + 1, threads=threads)
+        rq, rk, rv = oracle.attention_backward_groups(q, k, v, do, 1, T, H, Hkv, D, kv, kv + 1, threads=threads)
+        g = H // Hkv
+        hq = lambda x: x.reshape(T, H, D)[:, kv * g:(kv + 1) * g]
+        hk = lambda x: x.reshape(T, Hkv, D)[:, kv]
+        assert np.max(np.abs(hq(out) - hq(ro))) <= 1e-4
+        assert _rel(hq(dq), hq(rq)) <= 1e-3
+        assert _rel(hk(dk), hk(rk)) <= 1e-3
+        assert _rel(hk(dv), hk(rv)) <= 1e-3
+    finally:
+        L.zt_holder_deinit(p)

@@ -112,10 +112,10 @@ def test_matmul_refusals(gpu, zt):
 
 @pytest.mark.parametrize("tile", ["128", "64", "32"])
 @pytest.mark.parametrize("M,K,N", [(200, 70, 150), (33, 129, 65), (128, 64, 256)])
-def test_every_tile_size_passes_the_gate(gpu, zt, monkeypatch, tile, M, K, N):
+def test_every_tile_size_passes_the_gate(gpu, zt, tune, tile, M, K, N):
     """Each workgroup tile (forced through ZT_GEMM_TILE), for all three
     products, on ragged shapes."""
-    monkeypatch.setenv("ZT_GEMM_TILE", tile)
+    tune({"ZT_GEMM_TILE": tile})
     rng = np.random.default_rng(M * K + N)
     a = rng.uniform(-1, 1, (M, K)).astype(np.float32)
     b = rng.uniform(-1, 1, (K, N)).astype(np.float32)

@@ -178,6 +178,65 @@ def test_backward_row_subset_and_threads_are_bit_identical(oracle):
     assert np.array_equal(dq, mq) and np.array_equal(dk, mk) and np.array_equal(dv, mv)
 
 
+def _bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+@pytest.mark.parametrize("B,T,H,Hkv,D,kv0,kv1", [(2, 70, 8, 2, 32, 0, 1), (2, 70, 8, 2, 32, 1, 2),
+                                                 (1, 45, 6, 3, 34, 0, 3), (1, 33, 4, 4, 16, 2, 3),
+                                                 (1, 9, 2, 1, 8, 0, 1)])
+def test_group_backward_is_bit_identical_to_the_serial_restatement(oracle, B, T, H, Hkv, D, kv0, kv1):
+    """The two-phase parallel backward over whole kv groups gives every dq, dk
+    and dv bit of the serial h -> t -> s restatement on those groups and
+    leaves the rest zero (T not a multiple of the 8-row key blocks, 1-4 heads
+    per group, several threads)."""
+    rng = np.random.default_rng(B * 1000 + T)
+    q, k, v, do = (_rand(rng, B, T, H * D), _rand(rng, B, T, Hkv * D), _rand(rng, B, T, Hkv * D),
+                   _rand(rng, B, T, H * D))
+    dq, dk, dv = oracle.attention_backward(q, k, v, do, B, T, H, Hkv, D)
+    gq, gk, gv = oracle.attention_backward_groups(q, k, v, do, B, T, H, Hkv, D, kv0, kv1, threads=5)
+    g = H // Hkv
+    hq, hk = slice(kv0 * g, kv1 * g), slice(kv0, kv1)
+    q4, gq4 = dq.reshape(B, T, H, D), gq.reshape(B, T, H, D)
+    assert np.array_equal(_bits(q4[:, :, hq]), _bits(gq4[:, :, hq]))
+    for ref, got in ((dk, gk), (dv, gv)):
+        r4, g4 = ref.reshape(B, T, Hkv, D), got.reshape(B, T, Hkv, D)
+        assert np.array_equal(_bits(r4[:, :, hk]), _bits(g4[:, :, hk]))
+        rest = np.ones(Hkv, bool)
+        rest[hk] = False
+        assert not np.any(g4[:, :, rest])
+    rest = np.ones(H, bool)
+    rest[hq] = False
+    assert not np.any(gq4[:, :, rest])
+
+
+def test_group_backward_keeps_the_f32_read_modify_write_order(oracle):
+    """What the bit-identity above rests on: at this size the f32 chain of dk
+    / dv terms differs from the same terms summed in f64 and rounded once, so
+    a group backward that reordered or widened the chain would not match."""
+    from npref import attention_backward_f64
+    rng = np.random.default_rng(3)
+    B, T, H, Hkv, D = 1, 64, 4, 2, 32
+    q, k, v, do = (_rand(rng, B, T, H * D), _rand(rng, B, T, Hkv * D), _rand(rng, B, T, Hkv * D),
+                   _rand(rng, B, T, H * D))
+    _, gk, gv = oracle.attention_backward_groups(q, k, v, do, B, T, H, Hkv, D, 0, Hkv, threads=4)
+    _, fk, fv = attention_backward_f64(q, k, v, do, T, H, Hkv, D)
+    assert not np.array_equal(_bits(gk), _bits(np.float32(fk)))
+    assert not np.array_equal(_bits(gv), _bits(np.float32(fv)))
+    assert np.max(np.abs(gk - fk)) <= 1e-5 * np.abs(fk).max()
+
+
+@pytest.mark.parametrize("B,T,H,Hkv,D,kv0,kv1", [(2, 70, 8, 2, 32, 1, 2), (1, 45, 6, 3, 34, 0, 3)])
+def test_group_forward_is_bit_identical_to_the_serial_restatement(oracle, B, T, H, Hkv, D, kv0, kv1):
+    rng = np.random.default_rng(T)
+    q, k, v = _rand(rng, B, T, H * D), _rand(rng, B, T, Hkv * D), _rand(rng, B, T, Hkv * D)
+    ref = oracle.attention_forward(q, k, v, B, T, H, Hkv, D).reshape(B, T, H, D)
+    got = oracle.attention_forward_groups(q, k, v, B, T, H, Hkv, D, kv0, kv1, threads=3).reshape(B, T, H, D)
+    g = H // Hkv
+    assert np.array_equal(_bits(ref[:, :, kv0 * g:kv1 * g]), _bits(got[:, :, kv0 * g:kv1 * g]))
+    assert not np.any(got[:, :, :kv0 * g]) and not np.any(got[:, :, kv1 * g:])
+
+
 def test_row_stats_match_forward_identity(oracle):
     # delta = sum_s p dp = dO . O, the identity the device backward relies on.
     rng = np.random.default_rng(8)

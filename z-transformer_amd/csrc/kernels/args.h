@@ -22,6 +22,13 @@ struct FwdArgs {
     float scale_log2e; // log2(e) / sqrt(dim)
 };
 
+// Causal 16 x 16 score / dS tiles, packed by rows: row tile tb holds the tiles
+// sb = 0..tb (none above the diagonal), tile (tb, sb) at tb (tb + 1) / 2 + sb of
+// its (sequence, head) block of zt_tri_count(nt) tiles, nt = ceil(T / 16).
+// constexpr: callable from the host launcher and from device code.
+constexpr long long zt_tri_count(int nt) { return (long long)nt * (nt + 1) / 2; }
+constexpr long long zt_tri_index(int tb, int sb) { return (long long)tb * (tb + 1) / 2 + sb; }
+
 struct BwdArgs {
     const float *q, *k, *v, *dout;       // q/dout [B,T,H*dim]; k/v [B,T,Hkv*dim]
     float *dq, *dk, *dv;                 // assigned, never accumulated into
@@ -31,10 +38,10 @@ struct BwdArgs {
     // row_del = sum_d o * dO itself.
     const float *o, *lse;
     // If non-null, the dk/dv kernel writes dS here in 16 x 16 tiles: tile
-    // (b, h, t / 16, s / 16) at ((b*H + h) * nt + t/16) * nt + s/16 (nt = ceil(T/16)),
-    // 256 floats in lane order (lane l, element r) = (t = 16 tb + 4 (l >> 4) + r,
-    // s = 16 sb + (l & 15)); masked pairs are 0.  Tiles above the diagonal are
-    // never written.
+    // (b, h, t / 16, s / 16) at (b*H + h) * zt_tri_count(nt) + zt_tri_index(t/16, s/16)
+    // (nt = ceil(T/16)), 256 floats in lane order (lane l, element r) =
+    // (t = 16 tb + 4 (l >> 4) + r, s = 16 sb + (l & 15)); masked pairs are 0.
+    // Tiles above the diagonal have no slot and are never written.
     // The score-reading dk/dv kernels (zt_bwd_dkdv8s_*, zt_bwd_dkdv_dmas_*)
     // find the forward's scaled scores (FwdArgs::s_out) in ds_out on entry;
     // each tile is read before its dS replaces it.

@@ -530,12 +530,12 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
             // A tile with no visible pair (past T, above the diagonal or past
             // the last key) loads an in-bounds tile whose values the mask drops.
             const int nt = (a.T + 15) >> 4, sb = min(s0, a.T - 1) >> 4;
-            const size_t hrow = ((size_t)b * a.H + kvh * group + hs * hpp + hi) * nt;
+            const size_t hblk = ((size_t)b * a.H + kvh * group + hs * hpp + hi) * zt_tri_count(nt);
 #pragma unroll
             for (int u = 0; u < NU; ++u) {
                 const int tb = min(t0 + 16 * u, a.T - 1) >> 4;
                 sn[u] = __builtin_nontemporal_load(
-                    reinterpret_cast<const f4 *>(a.ds_out + ((hrow + tb) * nt + sb) * 256) + lane);
+                    reinterpret_cast<const f4 *>(a.ds_out + (hblk + zt_tri_index(tb, min(sb, tb))) * 256) + lane);
             }
         }
     };
@@ -703,8 +703,9 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
             const int nt = (a.T + 15) >> 4;
 #pragma unroll
             for (int u = 0; u < NU; ++u) {
-                if (t0 + 16 * u >= a.T) continue;  // wave-uniform: a sub-tile past the last row has no tile
-                const size_t tile = (((size_t)b * a.H + hh) * nt + ((t0 >> 4) + u)) * nt + (s0 >> 4);
+                // wave-uniform: a sub-tile past the last row or above the diagonal has no slot
+                if (t0 + 16 * u >= a.T || t0 + 16 * u + 15 < s0) continue;
+                const size_t tile = ((size_t)b * a.H + hh) * zt_tri_count(nt) + zt_tri_index((t0 >> 4) + u, s0 >> 4);
                 __builtin_nontemporal_store(dsv[u], reinterpret_cast<f4 *>(a.ds_out + tile * 256) + lane);
             }
         }
@@ -875,7 +876,7 @@ __device__ __forceinline__ void bwd_dkdv_dma_tile(const BwdArgs &a, const int kt
             sn = zero4();
             if (pr.t0 + 15 >= s0 && s0 < a.T) {  // wave-uniform; t0 < T for every stage
                 const int nt = (a.T + 15) >> 4;
-                const size_t tile = (((size_t)b * a.H + pr.hh) * nt + (pr.t0 >> 4)) * nt + (s0 >> 4);
+                const size_t tile = ((size_t)b * a.H + pr.hh) * zt_tri_count(nt) + zt_tri_index(pr.t0 >> 4, s0 >> 4);
                 sn = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(a.ds_out + tile * 256) + lane);
             }
         }
@@ -979,7 +980,7 @@ __device__ __forceinline__ void bwd_dkdv_dma_tile(const BwdArgs &a, const int kt
             }
             if (a.ds_out) {  // dS for a dq product outside this kernel: the 16 x 16 tile in lane order
                 const int nt = (a.T + 15) >> 4;
-                const size_t tile = (((size_t)b * a.H + mine.hh) * nt + (t0 >> 4)) * nt + (s0 >> 4);
+                const size_t tile = ((size_t)b * a.H + mine.hh) * zt_tri_count(nt) + zt_tri_index(t0 >> 4, s0 >> 4);
                 __builtin_nontemporal_store(dsv, reinterpret_cast<f4 *>(a.ds_out + tile * 256) + lane);
             }
             // dO^T, Q^T rows in the row-owner layout, read one row ahead.

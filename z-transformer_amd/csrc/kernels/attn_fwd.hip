@@ -134,8 +134,10 @@ __device__ __forceinline__ void attn_fwd_tile(const FwdArgs &a, const int tile) 
             // (s & 15) + 16 ((t & 15) >> 2), element t & 3 of its tile: four
             // lanes write each 16-byte run.  (A quad transpose to one 16-byte
             // store per lane measured no faster.)
+            // Row tile row0 / 16 keeps its tiles 0..row0 / 16 contiguous, so
+            // sub-block j of this key tile is j tiles after its first.
             const int nt = (a.T + 15) >> 4;
-            float *srow = a.s_out + ((((size_t)b * a.H + h) * nt + (row0 >> 4)) * nt + (k0 >> 4)) * 256 +
+            float *srow = a.s_out + (((size_t)b * a.H + h) * zt_tri_count(nt) + zt_tri_index(row0 >> 4, k0 >> 4)) * 256 +
                           (16 * (l16 >> 2)) * 4 + (l16 & 3);
 #pragma unroll
             for (int j = 0; j < NJ; ++j) {

@@ -219,7 +219,7 @@ DEVI void dq_ds_tile(const DqDsArgs &g, const int tm, const int tn, const int bh
     const int m0 = tm * BT, n0 = tn * BT;
     const size_t qld = (size_t)g.H * g.dim, kld = (size_t)g.Hkv * g.dim;
     const int nt = (g.T + 15) >> 4;
-    const float *A = g.ds + (size_t)bh * nt * nt * 256;
+    const float *A = g.ds + (size_t)bh * zt_tri_count(nt) * 256;
     const float *Bm = g.k + (size_t)b * g.T * kld + (size_t)kvh * g.dim;
     float *C = g.dq + (size_t)b * g.T * qld + (size_t)h * g.dim;
     const int kend = min(g.T, m0 + BT);
@@ -247,11 +247,11 @@ DEVI void dq_ds_tile(const DqDsArgs &g, const int tm, const int tn, const int bh
             const bool ok = sb <= tb && tb < nt;
             if constexpr (VEC) {  // read once: nontemporal
                 const int tc = min(tb, nt - 1), sc = min(sb, tc);
-                const f4 x = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(A + ((size_t)tc * nt + sc) * 256) + c);
+                const f4 x = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(A + zt_tri_index(tc, sc) * 256) + c);
                 pa[n] = ok ? x : zero4();
             } else {
                 f4 x = zero4();
-                if (ok) x = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(A + ((size_t)tb * nt + sb) * 256) + c);
+                if (ok) x = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(A + zt_tri_index(tb, sb) * 256) + c);
                 pa[n] = x;
             }
         }

@@ -12,6 +12,7 @@
 #include <hip/hip_runtime_api.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
@@ -127,16 +128,44 @@ int launch(DeviceState *st, const char *name, unsigned blocks, const Args &args,
     return 0;
 }
 
-// Tuning knobs for sweeps (validated; anything else falls back to the default).
-int env_choice(const char *name, int dflt, std::initializer_list<int> allowed) {
-    const char *s = getenv(name);
-    if (!s || !*s) return dflt;
-    char *end = nullptr;
-    const long v = strtol(s, &end, 10);
-    if (*end) return dflt;
-    for (int a : allowed)
-        if (v == a) return a;
-    return dflt;
+// Tuning variables: every kernel variant is chosen from the shape unless one of
+// these is set, which happens only through zt_attn_set_tuning (sweeps and the
+// tests that force each variant).  The process environment is never read, so
+// nothing outside the caller's own calls changes which kernel runs.  A plain
+// array of atomics: the launchers read it without a lock.
+enum Tune {
+    kTuneBK, kTuneFwdW, kTuneFPF, kTuneFPair, kTuneQPF, kTuneDqW, kTuneHS, kTuneW8, kTunePF, kTuneDMA, kTuneBPair,
+    kTuneDSplit, kTuneRSplit, kTuneDecWgs, kTuneGemmTile, kTuneDqdsTile, kTuneCount
+};
+struct TuneSpec {
+    const char *name;
+    int allowed[10];
+    int n_allowed;
+};
+const TuneSpec kTuneSpecs[kTuneCount] = {
+    {"ZT_ATTN_BK", {32, 64}, 2},
+    {"ZT_ATTN_FWD_W", {4, 8}, 2},
+    {"ZT_ATTN_FPF", {0, 1}, 2},
+    {"ZT_ATTN_FPAIR", {0, 1}, 2},
+    {"ZT_ATTN_QPF", {0, 1}, 2},
+    {"ZT_ATTN_DQ_W", {4, 8}, 2},
+    {"ZT_ATTN_HS", {1, 2, 4}, 3},
+    {"ZT_ATTN_W8", {0, 1}, 2},
+    {"ZT_ATTN_PF", {0, 1}, 2},
+    {"ZT_ATTN_DMA", {0, 1}, 2},
+    {"ZT_ATTN_BPAIR", {0, 1}, 2},
+    {"ZT_ATTN_DSPLIT", {0, 1}, 2},
+    {"ZT_ATTN_RSPLIT", {0, 1}, 2},
+    {"ZT_DEC_WGS", {256, 512, 768, 1024, 1536, 2048, 4096, 8192, 16384, 32768}, 10},
+    {"ZT_GEMM_TILE", {32, 64, 128}, 3},
+    {"ZT_DQDS_TILE", {64, 128}, 2},
+};
+std::atomic<int> g_tune[kTuneCount] = {};  // 0 = unset (no allowed value is 0 except a flag, stored as value + 1)
+
+// The forced value of a variable, or `dflt` (the shape rule) when unset.
+int tuned(Tune id, int dflt) {
+    const int v = g_tune[id].load(std::memory_order_relaxed);
+    return v == 0 ? dflt : v - 1;
 }
 
 int pad32(int dim) { return (dim + 31) / 32 * 32; }
@@ -153,7 +182,7 @@ int heads_per_wg(int group) { return group % 4 == 0 ? 4 : (group % 2 == 0 ? 2 : 
 enum class Tiled { Forward, Dq };
 int key_tile(Tiled which, int dp, int max_tile, int dim = 0) {
     const int dflt = (which == Tiled::Forward && dp <= 64 && dim % 4 != 0) ? 64 : 32;
-    const int preferred = env_choice("ZT_ATTN_BK", dflt, {32, 64});
+    const int preferred = tuned(kTuneBK, dflt);
     return max_tile >= 64 ? preferred : 32;
 }
 // LDS per workgroup: K and V tiles, row-major with a 4-float pad.
@@ -166,7 +195,7 @@ size_t kv_tile_bytes(int dp, int bk) { return (size_t)2 * bk * (dp + 4) * sizeof
 // 0.76 ms) and, with the register prefetch, when two do (B = 4, T = 2048, 16
 // heads over 8, d = 128: 0.647 -> 0.581 ms; d = 256, B = 2: 0.711 -> 0.588 ms);
 // it loses for MHA (C2 0.057 -> 0.076 ms); the dq kernel loses at every shape tried.
-int fwd_waves(int hw) { return env_choice("ZT_ATTN_FWD_W", hw >= 2 ? 8 : 4, {4, 8}); }
+int fwd_waves(int hw) { return tuned(kTuneFwdW, hw >= 2 ? 8 : 4); }
 
 // Forward kernel name: waves per workgroup, key tile, and for 32-key tiles the
 // register-prefetched variant (ZT_ATTN_FPF=0 turns it off).  Measured on
@@ -175,14 +204,14 @@ int fwd_waves(int hw) { return env_choice("ZT_ATTN_FWD_W", hw >= 2 ? 8 : 4, {4, 
 // sequence of 2048 rows at d = 128 0.30 -> 0.185 ms.
 void fwd_kernel_name(char *name, size_t len, int dim, int dp, int bk, int nw) {
     // The prefetching kernels load 16-byte row chunks unconditionally (dim % 4 == 0).
-    const bool pf = bk == 32 && dim % 4 == 0 && env_choice("ZT_ATTN_FPF", 1, {0, 1}) == 1;
+    const bool pf = bk == 32 && dim % 4 == 0 && tuned(kTuneFPF, 1) == 1;
     if (pf)
         snprintf(name, len, nw == 8 ? "zt_fwd8p_d%d_k32" : "zt_fwdp_d%d_k32", dp);
     else
         snprintf(name, len, nw == 8 ? "zt_fwd8_d%d_k%d" : "zt_fwd_d%d_k%d", dp, bk);
 }
 int dq_waves(int dp) {
-    const int w = env_choice("ZT_ATTN_DQ_W", 4, {4, 8});
+    const int w = tuned(kTuneDqW, 4);
     return dp > 192 ? 4 : w;  // eight-wave dq spills above d = 192
 }
 // bufs: stage buffers (2 in the register-prefetching kernels).
@@ -209,7 +238,7 @@ size_t dkdv_dspd_bytes(int dp, int hs = 2) {
 // Paired tiles (forward rows, dk/dv keys) by default only when the unpaired grid is larger than the CU count.
 int pair_pays(unsigned long long unpaired_blocks, int cus) { return unpaired_blocks > (unsigned long long)cus ? 1 : 0; }
 bool dkdv_dsplit(int dp, size_t lds_limit) {
-    return (dp == 192 || dp == 256) && dkdv_ds_bytes(dp) <= lds_limit && env_choice("ZT_ATTN_DSPLIT", 1, {0, 1}) == 1;
+    return (dp == 192 || dp == 256) && dkdv_ds_bytes(dp) <= lds_limit && tuned(kTuneDSplit, 1) == 1;
 }
 
 int refuse_T(int T) {
@@ -337,8 +366,7 @@ int forward_impl(const float *q, const float *k, const float *v, float *out, int
     // measured on MI355X, C3 1.22 -> 1.13 ms, C5 0.63 -> 0.61 ms, C2 0.082 -> 0.072 ms.
     // Not when the unpaired grid fits the CUs once (one MHA sequence, T 1024,
     // d 64: 0.070 -> 0.064 ms without).
-    a.pair = env_choice("ZT_ATTN_FPAIR",
-                        pair_pays((unsigned long long)a.n_row_tiles * a.n_head_blocks * B, st->cus), {0, 1});
+    a.pair = tuned(kTuneFPair, pair_pays((unsigned long long)a.n_row_tiles * a.n_head_blocks * B, st->cus));
     const unsigned long long blocks =
         (unsigned long long)(a.pair ? (a.n_row_tiles + 1) / 2 : a.n_row_tiles) * a.n_head_blocks * B;
     if (!grid_ok(blocks)) return 1;
@@ -375,7 +403,7 @@ int backward_prepare(const float *q, const float *k, const float *v, const float
     // g = 4, d = 128 and 256: half the Q/dO staging of a 4-way split, twice
     // the workgroups of none).
     const int hs_dflt = group % 2 == 0 ? 2 : 1;
-    int hs = env_choice("ZT_ATTN_HS", hs_dflt, {1, 2, 4});
+    int hs = tuned(kTuneHS, hs_dflt);
     if (group % hs != 0 || (hs == 4 && dp > 128)) hs = hs_dflt;  // 4-way split instantiated up to d = 128
     while (hs > 1 && dkdv_bytes(dp, hs) > st->lds_limit) hs /= 2;
     if (kv_tile_bytes(dp, bk) > st->lds_limit || dkdv_bytes(dp, hs) > st->lds_limit) {
@@ -414,7 +442,7 @@ int backward_prepare(const float *q, const float *k, const float *v, const float
     //    to hide the staging latency with other workgroups; it needs
     //    whole-head rows on 16-byte aligned q/dout;
     //  - otherwise the four-wave register-staged kernel.
-    const bool wide = env_choice("ZT_ATTN_W8", 1, {0, 1}) == 1 && hs == 2 && dp <= 128 &&
+    const bool wide = tuned(kTuneW8, 1) == 1 && hs == 2 && dp <= 128 &&
                       dkdv_bytes(dp, 2, 4) <= st->lds_limit;
     const int keys_per_wg = wide ? 64 : 16 * (4 / hs);
     a->n_key_tiles = (T + keys_per_wg - 1) / keys_per_wg;
@@ -423,8 +451,7 @@ int backward_prepare(const float *q, const float *k, const float *v, const float
     // reading scores 2.01 -> 1.93 ms, C5 1.49 -> 1.43 ms.  Not when the
     // unpaired grid already fits the CUs once: pairing would leave CUs idle
     // (one MHA sequence, T 1024, d 64: 0.131 -> 0.122 ms without).
-    a->pair = env_choice("ZT_ATTN_BPAIR", pair_pays((unsigned long long)a->n_key_tiles * n_kv_heads * B, st->cus),
-                         {0, 1});
+    a->pair = tuned(kTuneBPair, pair_pays((unsigned long long)a->n_key_tiles * n_kv_heads * B, st->cus));
     const unsigned long long blocks_b =
         (unsigned long long)(a->pair ? (a->n_key_tiles + 1) / 2 : a->n_key_tiles) * n_kv_heads * B;
     const bool aligned = ((uintptr_t)q % 16 == 0) && ((uintptr_t)dout % 16 == 0);
@@ -434,7 +461,7 @@ int backward_prepare(const float *q, const float *k, const float *v, const float
     // 0.165 -> 0.137 ms) and for wide heads.
     const bool dma_pays =
         dp >= 160 || (unsigned long long)((a->n_key_tiles + 1) / 2) * n_kv_heads * B <= (unsigned long long)st->cus;
-    const bool dma_want = env_choice("ZT_ATTN_DMA", dma_pays ? 1 : 0, {0, 1}) == 1;
+    const bool dma_want = tuned(kTuneDMA, dma_pays ? 1 : 0) == 1;
     // Eight waves splitting the head's columns in two (two waves per SIMD)
     // where the halves are whole 32-column groups: at d = 192, 256 instead of
     // the four-wave kernels (C5 and the reference entry points); for a group
@@ -445,18 +472,18 @@ int backward_prepare(const float *q, const float *k, const float *v, const float
     // ZT_ATTN_DSPLIT=0 turns it off.
     const bool dsplit = !wide && hs <= 2 && dim == dp && aligned && dkdv_dspd_bytes(dp, hs) <= st->lds_limit &&
                         (dp == 192 || dp == 256 || (hs == 1 && (dp == 64 || dp == 128) && !dma_want)) &&
-                        env_choice("ZT_ATTN_DSPLIT", 1, {0, 1}) == 1;
+                        tuned(kTuneDSplit, 1) == 1;
     const bool dma = !wide && !dsplit && dma_ok && dma_want;
     // A group that cannot be split (MHA, odd groups) on the asynchronously
     // staged kernel: two row parts per workgroup instead, eight waves.
     const bool rsplit = dma && hs == 1 && dp <= 128 && dkdv_dma_bytes(dp, 2) <= st->lds_limit &&
-                        env_choice("ZT_ATTN_RSPLIT", 1, {0, 1}) == 1;
+                        tuned(kTuneRSplit, 1) == 1;
     a->scale = (float)(1.0 / std::sqrt((double)dim));
     a->scale_log2e = (float)(1.4426950408889634 / std::sqrt((double)dim));
     const unsigned long long blocks_a =
         (unsigned long long)(a->pair ? (a->n_row_tiles + 1) / 2 : a->n_row_tiles) * a->n_head_blocks * B;
     if (!grid_ok(blocks_a) || !grid_ok(blocks_b)) return 1;
-    const bool qpf = bk == 32 && env_choice("ZT_ATTN_QPF", 1, {0, 1}) == 1;
+    const bool qpf = bk == 32 && tuned(kTuneQPF, 1) == 1;
     if (saved)
         snprintf(name_dq, 64, "zt_bwd_dql_d%d_k32", dp);
     else if (qpf)
@@ -466,7 +493,7 @@ int backward_prepare(const float *q, const float *k, const float *v, const float
     *threads_dq = 64u * nw_dq;
     // The prefetching kernel loads whole 16-byte chunks unconditionally.
     const bool pf = dim % 4 == 0 && aligned && dkdv_bytes(dp, 2, 4, 16, 2) <= st->lds_limit &&
-                    env_choice("ZT_ATTN_PF", 1, {0, 1}) == 1;
+                    tuned(kTunePF, 1) == 1;
     if (wide)
         snprintf(name_dkdv, 64, pf ? "zt_bwd_dkdv8p_d%d_hs2" : "zt_bwd_dkdv8_d%d_hs2", dp);
     else if (dsplit)
@@ -524,7 +551,7 @@ DecGeom decode_geom(int B, int n_ctx, int n_heads, int n_kv_heads, int dim) {
     // Workgroups to aim for: 512, two per CU of MI355X's 256 (the workspace
     // size must not depend on the device). Measured on MI355X against 1024 / 2048
     // (C4 643 -> 624 us; B = 1, 8192 keys 66 -> 41 us; B = 16, 4096 keys 106 -> 93 us).
-    const long long target = env_choice("ZT_DEC_WGS", 512, {256, 512, 768, 1024, 1536, 2048, 4096, 8192, 16384, 32768});
+    const long long target = tuned(kTuneDecWgs, 512);
     long long per_seq = (target + pairs - 1) / pairs;
     if (per_seq < 1) per_seq = 1;
     long long chunk = (n_ctx + per_seq - 1) / per_seq;
@@ -645,14 +672,15 @@ int zt_attn_bwd_dkdv_train(const float *q, const float *k, const float *v, const
 static int dqds_tile(int B, int T, int n_heads, int dim, int cus) {
     const unsigned long long wgs128 =
         (unsigned long long)(((T + 127) / 128 + 1) / 2) * ((dim + 127) / 128) * B * n_heads;  // row-tile pairs
-    return (dim > 64 && wgs128 >= (unsigned long long)cus) ? 128 : 64;
+    return tuned(kTuneDqdsTile, (dim > 64 && wgs128 >= (unsigned long long)cus) ? 128 : 64);
 }
 
 size_t zt_attn_backward_train_workspace(int B, int T, int n_heads, int n_kv_heads, int dim) {
     if (B < 1 || T < 1 || !zt_attn_dim_ok(dim) || n_heads <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads != 0)
         return 0;
-    const size_t nt = (size_t)(T + 15) / 16;  // dS in 16 x 16 tiles
-    return align256((size_t)B * T * n_heads * sizeof(float)) + (size_t)B * n_heads * nt * nt * 256 * sizeof(float);
+    const int nt = (T + 15) / 16;  // dS in 16 x 16 tiles, the causal ones only
+    return align256((size_t)B * T * n_heads * sizeof(float)) +
+           (size_t)B * n_heads * (size_t)zt_tri_count(nt) * 256 * sizeof(float);
 }
 
 // Shapes whose dk/dv kernel can take the forward's scores instead of
@@ -738,8 +766,7 @@ int zt_attn_backward_train_ws(const float *q, const float *k, const float *v, co
         const int keys = dp <= 128 ? 64 : 32;
         const bool dsplit = dp > 128 && dkdv_dsplit(dp, st->lds_limit);
         a.n_key_tiles = (T + keys - 1) / keys;
-        a.pair = env_choice("ZT_ATTN_BPAIR", pair_pays((unsigned long long)a.n_key_tiles * n_kv_heads * B, st->cus),
-                            {0, 1});
+        a.pair = tuned(kTuneBPair, pair_pays((unsigned long long)a.n_key_tiles * n_kv_heads * B, st->cus));
         const unsigned long long blocks =
             (unsigned long long)(a.pair ? (a.n_key_tiles + 1) / 2 : a.n_key_tiles) * n_kv_heads * B;
         if (!grid_ok(blocks)) return 1;
@@ -1158,7 +1185,7 @@ static int gemm_impl(const char *name, const char *what, const float *a, int lda
     auto tiles = [&](int bt) { return (unsigned long long)((M + bt - 1) / bt) * (unsigned long long)((N + bt - 1) / bt); };
     int bt = 128;
     if (tiles(128) < (unsigned long long)st->cus) bt = tiles(64) >= (unsigned long long)st->cus / 2 ? 64 : 32;
-    bt = env_choice("ZT_GEMM_TILE", bt, {32, 64, 128});
+    bt = tuned(kTuneGemmTile, bt);
     const unsigned long long blocks = tiles(bt);
     if (!grid_ok(blocks)) return 1;
     GemmArgs g{};
@@ -1186,7 +1213,33 @@ int zt_input_grad(float *din, const float *dout, const float *w, int T, int J, i
     return gemm_impl("zt_gemm_nt", "zt_input_grad", dout, J, w, J, din, I, T, I, J, 1, stream);
 }
 
-const char *zt_attn_version(void) { return "zt_attn gfx950 0.1"; }
+int zt_attn_set_tuning(const char *name, int value) {
+    for (int i = 0; name && i < kTuneCount; ++i) {
+        if (strcmp(name, kTuneSpecs[i].name) != 0) continue;
+        if (value == -1) {
+            g_tune[i].store(0, std::memory_order_relaxed);
+            return 0;
+        }
+        for (int j = 0; j < kTuneSpecs[i].n_allowed; ++j) {
+            if (kTuneSpecs[i].allowed[j] == value) {
+                g_tune[i].store(value + 1, std::memory_order_relaxed);
+                return 0;
+            }
+        }
+        fprintf(stderr, "zt_attn: %d is not a value of the tuning variable %s.\n", value, name);
+        return 1;
+    }
+    fprintf(stderr, "zt_attn: %s is not a tuning variable.\n", name ? name : "(null)");
+    return 1;
+}
+
+int zt_attn_get_tuning(const char *name) {
+    for (int i = 0; name && i < kTuneCount; ++i)
+        if (strcmp(name, kTuneSpecs[i].name) == 0) return g_tune[i].load(std::memory_order_relaxed) - 1;
+    return -2;
+}
+
+const char *zt_attn_version(void) { return "zt_attn gfx950 0.2"; }
 
 size_t zt_attn_lds_limit(void) {
     DeviceState *st = device_state();

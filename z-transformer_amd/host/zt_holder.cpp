@@ -3,6 +3,19 @@
 // One deliberate difference: a failed hipMemcpy is DeviceTransferFailed, the
 // error device.zig:134-140 documents for it (its upload/download at :418,:430
 // return DeviceAllocFailed instead).
+//
+// Saved statistics.  device.zig:400-402 requires the forward to have run on the
+// same buffers before the backward, so the holder keeps what its forward
+// formed instead of making the backward rebuild it: a whole-cache forward runs
+// zt_attn_forward_train_ws (log-sum-exp into row_max, 1.0 into row_den, so
+// p = exp(s - row_max) / row_den still holds, and the scores into a workspace
+// the holder owns), and the next backward runs zt_attn_backward_train_ws
+// reading them (row_del receives delta = sum_d out * dout).  The state is
+// dropped by any upload into q, k, v, out or row_max, by a decode-shaped
+// forward_at, and by zt_holder_forget; a backward without a current forward
+// runs the reference pair (zt_attn_backward), which rebuilds the statistics.
+// Without the workspace (its allocation failed, or zt_holder_init_exact) the
+// fast pair is zt_attn_forward_train + zt_attn_backward_train.
 #include <hip/hip_runtime_api.h>
 
 #include <climits>
@@ -56,10 +69,17 @@ int forward_bounds(int c_t, int q_offset, int n_keys, int t) {
     return ZT_OK;
 }
 
+// What the last forward left for the backward.
+enum class Saved { None, Lse, Scores };
+
 struct Attn {
     float *buf[ZT_N_BUFFERS] = {};
     size_t t = 0, n_heads = 0, n_kv_heads = 0, dim = 0;
     int c_t = 0, c_heads = 0, c_kv_heads = 0, c_dim = 0;
+    void *ws = nullptr;  // zt_attn_backward_train_workspace bytes, or null
+    size_t ws_bytes = 0;
+    bool fast = true;    // false: the reference pair only (zt_holder_init_exact)
+    mutable Saved saved = Saved::None;
 
     size_t buffer_bytes(int which) const {
         size_t n = 0;
@@ -74,8 +94,18 @@ struct Attn {
             if (buf[i]) (void)hipFree(buf[i]);
             buf[i] = nullptr;
         }
+        if (ws) (void)hipFree(ws);
+        ws = nullptr;
+        ws_bytes = 0;
     }
 };
+
+// The reference forward's own admission of group_q and max_tile
+// (src/cuda/attn_kernels.cu:858-871): the fast forward ignores both, so it is
+// taken only for arguments the reference entry point would accept too.
+static bool forward_args_ok(int group_q, int max_tile, int dim) {
+    return group_q >= 1 && group_q <= 64 && (size_t)dim * (size_t)group_q <= 1024 && max_tile >= 1;
+}
 
 }  // namespace zt
 
@@ -95,7 +125,7 @@ int zt_forward_bounds(int c_t, int q_offset, int n_keys, int t) {
     return zt::forward_bounds(c_t, q_offset, n_keys, t);
 }
 
-int zt_holder_init(size_t t, size_t n_heads, size_t n_kv_heads, size_t dim, zt_holder **out) {
+static int holder_init(size_t t, size_t n_heads, size_t n_kv_heads, size_t dim, bool fast, zt_holder **out) {
     if (!out) return ZT_CONFIG_REFUSED;
     *out = nullptr;
     int c_t, c_heads, c_kv, c_dim, e;
@@ -125,8 +155,35 @@ int zt_holder_init(size_t t, size_t n_heads, size_t n_kv_heads, size_t dim, zt_h
     }
     h->a.t = t; h->a.n_heads = n_heads; h->a.n_kv_heads = n_kv_heads; h->a.dim = dim;
     h->a.c_t = c_t; h->a.c_heads = c_heads; h->a.c_kv_heads = c_kv; h->a.c_dim = c_dim;
+    h->a.fast = fast;
+    if (fast) {
+        // The score workspace is an optimisation: without it the holder still
+        // runs the saved-statistics pair, so a failed allocation is no error.
+        const size_t wsb = zt_attn_backward_train_workspace(1, c_t, c_heads, c_kv, c_dim);
+        void *p = nullptr;
+        if (wsb != 0 && hipMalloc(&p, wsb) == hipSuccess && p) {
+            h->a.ws = p;
+            h->a.ws_bytes = wsb;
+        } else {
+            (void)hipGetLastError();
+        }
+    }
     *out = h;
     return ZT_OK;
+}
+
+int zt_holder_init(size_t t, size_t n_heads, size_t n_kv_heads, size_t dim, zt_holder **out) {
+    return holder_init(t, n_heads, n_kv_heads, dim, true, out);
+}
+
+int zt_holder_init_exact(size_t t, size_t n_heads, size_t n_kv_heads, size_t dim, zt_holder **out) {
+    return holder_init(t, n_heads, n_kv_heads, dim, false, out);
+}
+
+size_t zt_holder_workspace_bytes(const zt_holder *h) { return h ? h->a.ws_bytes : 0; }
+
+void zt_holder_forget(const zt_holder *h) {
+    if (h) h->a.saved = zt::Saved::None;
 }
 
 void zt_holder_deinit(zt_holder *h) {
@@ -152,6 +209,26 @@ float *zt_holder_buffer(const zt_holder *h, int which) {
 int zt_holder_forward_at(const zt_holder *h, int group_q, int max_tile, int q_offset, int n_keys, int t) {
     const zt::Attn &a = h->a;
     if (int e = zt::forward_bounds(a.c_t, q_offset, n_keys, t)) return e;
+    a.saved = zt::Saved::None;
+    const bool whole = q_offset == 0 && n_keys == a.c_t && t == a.c_t;
+    if (a.fast && whole && zt::forward_args_ok(group_q, max_tile, a.c_dim)) {
+        float *lse = a.buf[ZT_BUF_ROW_MAX];
+        const int rc = a.ws ? zt_attn_forward_train_ws(a.buf[ZT_BUF_Q], a.buf[ZT_BUF_K], a.buf[ZT_BUF_V],
+                                                       a.buf[ZT_BUF_OUT], lse, a.ws, a.ws_bytes, 1, a.c_t, a.c_heads,
+                                                       a.c_kv_heads, a.c_dim, nullptr)
+                            : zt_attn_forward_train(a.buf[ZT_BUF_Q], a.buf[ZT_BUF_K], a.buf[ZT_BUF_V],
+                                                    a.buf[ZT_BUF_OUT], lse, 1, a.c_t, a.c_heads, a.c_kv_heads,
+                                                    a.c_dim, nullptr);
+        if (rc != 0) return ZT_CONFIG_REFUSED;
+        // row_den = 1: with row_max = lse, p = exp(s - row_max) / row_den is the softmax.
+        if (hipMemsetD32Async(a.buf[ZT_BUF_ROW_DEN], 0x3f800000, (size_t)a.c_t * (size_t)a.c_heads, nullptr) !=
+            hipSuccess) {
+            (void)hipGetLastError();
+            return ZT_CONFIG_REFUSED;
+        }
+        a.saved = a.ws ? zt::Saved::Scores : zt::Saved::Lse;
+        return ZT_OK;
+    }
     const int rc = zt_attn_forward(a.buf[ZT_BUF_Q], a.buf[ZT_BUF_K], a.buf[ZT_BUF_V], a.buf[ZT_BUF_OUT], t, a.c_heads,
                                    a.c_kv_heads, a.c_dim, group_q, max_tile, q_offset, n_keys, nullptr);
     return rc != 0 ? ZT_CONFIG_REFUSED : ZT_OK;
@@ -163,6 +240,32 @@ int zt_holder_forward(const zt_holder *h, int group_q, int max_tile) {
 
 int zt_holder_backward(const zt_holder *h, int max_tile) {
     const zt::Attn &a = h->a;
+    if (a.saved != zt::Saved::None && max_tile >= 1) {
+        float *row_del = a.buf[ZT_BUF_ROW_DEL];
+        const size_t per_row = (size_t)a.c_t * (size_t)a.c_heads;
+        int rc;
+        if (a.ws) {
+            rc = zt_attn_backward_train_ws(a.buf[ZT_BUF_Q], a.buf[ZT_BUF_K], a.buf[ZT_BUF_V], a.buf[ZT_BUF_OUT],
+                                           a.buf[ZT_BUF_DOUT], a.buf[ZT_BUF_ROW_MAX], a.buf[ZT_BUF_DQ],
+                                           a.buf[ZT_BUF_DK], a.buf[ZT_BUF_DV], a.ws, a.ws_bytes, 1, a.c_t, a.c_heads,
+                                           a.c_kv_heads, a.c_dim, a.saved == zt::Saved::Scores ? 3 | ZT_WS_SCORES : 3,
+                                           nullptr);
+            // delta sits at the workspace's start; row_del keeps the reference's scratch contract.
+            if (rc == 0 && hipMemcpyAsync(row_del, a.ws, per_row * sizeof(float), hipMemcpyDeviceToDevice, nullptr) !=
+                               hipSuccess) {
+                (void)hipGetLastError();
+                rc = 1;
+            }
+        } else {
+            rc = zt_attn_backward_train(a.buf[ZT_BUF_Q], a.buf[ZT_BUF_K], a.buf[ZT_BUF_V], a.buf[ZT_BUF_OUT],
+                                        a.buf[ZT_BUF_DOUT], a.buf[ZT_BUF_ROW_MAX], a.buf[ZT_BUF_DQ], a.buf[ZT_BUF_DK],
+                                        a.buf[ZT_BUF_DV], row_del, 1, a.c_t, a.c_heads, a.c_kv_heads, a.c_dim,
+                                        nullptr);
+        }
+        // The score tiles now hold dS: a second backward rebuilds them from lse.
+        a.saved = zt::Saved::Lse;
+        return rc != 0 ? ZT_CONFIG_REFUSED : ZT_OK;
+    }
     const int rc = zt_attn_backward(a.buf[ZT_BUF_Q], a.buf[ZT_BUF_K], a.buf[ZT_BUF_V], a.buf[ZT_BUF_DOUT],
                                     a.buf[ZT_BUF_DQ], a.buf[ZT_BUF_DK], a.buf[ZT_BUF_DV], a.buf[ZT_BUF_ROW_MAX],
                                     a.buf[ZT_BUF_ROW_DEN], a.buf[ZT_BUF_ROW_DEL], a.c_t, a.c_heads, a.c_kv_heads,
@@ -175,6 +278,9 @@ int zt_holder_upload(const zt_holder *h, int which, const float *src, size_t n_f
     size_t n = 0;
     if (!zt::mul_ok(n_floats, sizeof(float), &n)) return ZT_SHAPE_TOO_LARGE;
     if (n > h->a.buffer_bytes(which)) return ZT_SHAPE_TOO_LARGE;
+    // New q, k, v, out or lse: the forward's saved state no longer describes them.
+    if (which == ZT_BUF_Q || which == ZT_BUF_K || which == ZT_BUF_V || which == ZT_BUF_OUT || which == ZT_BUF_ROW_MAX)
+        h->a.saved = zt::Saved::None;
     if (hipMemcpy(h->a.buf[which], src, n, hipMemcpyHostToDevice) != hipSuccess) {
         (void)hipGetLastError();
         return ZT_DEVICE_TRANSFER_FAILED;

@@ -25,12 +25,13 @@ ABI_SYMBOLS = [
     "zt_attn_lds_limit", "zt_attn_plan", "zt_attn_forward_train", "zt_attn_backward_train",
     "zt_attn_bwd_dq_train", "zt_attn_bwd_dkdv_train", "zt_attn_plan_train", "zt_calibrate",
     "zt_matmul", "zt_weight_grad", "zt_input_grad", "zt_attn_backward_train_workspace",
-    "zt_attn_backward_train_ws", "zt_attn_forward_train_ws",
+    "zt_attn_backward_train_ws", "zt_attn_forward_train_ws", "zt_attn_set_tuning", "zt_attn_get_tuning",
 ]
 HOLDER_SYMBOLS = [
     "zt_bytes_for", "zt_to_cint", "zt_forward_bounds", "zt_holder_init", "zt_holder_deinit",
     "zt_holder_total_bytes", "zt_holder_buffer", "zt_holder_forward", "zt_holder_forward_at",
-    "zt_holder_backward", "zt_holder_upload", "zt_holder_download",
+    "zt_holder_backward", "zt_holder_upload", "zt_holder_download", "zt_holder_init_exact",
+    "zt_holder_workspace_bytes", "zt_holder_forget",
 ]
 
 # include/zt_holder.h enum zt_error
@@ -89,11 +90,16 @@ def lib():
             "zt_fill_uniform": (I, [P, Z, U64, D, D, P]),
             "zt_attn_version": (ctypes.c_char_p, []),
             "zt_attn_lds_limit": (Z, []),
+            "zt_attn_set_tuning": (I, [ctypes.c_char_p, I]),
+            "zt_attn_get_tuning": (I, [ctypes.c_char_p]),
             "zt_attn_plan": (I, [I, I, I, I, I, I, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, Z]),
             "zt_bytes_for": (I, [I, Z, Z, Z, Z, ctypes.POINTER(Z)]),
             "zt_to_cint": (I, [Z, ctypes.POINTER(I)]),
             "zt_forward_bounds": (I, [I, I, I, I]),
             "zt_holder_init": (I, [Z, Z, Z, Z, ctypes.POINTER(P)]),
+            "zt_holder_init_exact": (I, [Z, Z, Z, Z, ctypes.POINTER(P)]),
+            "zt_holder_workspace_bytes": (Z, [P]),
+            "zt_holder_forget": (None, [P]),
             "zt_holder_deinit": (None, [P]),
             "zt_holder_total_bytes": (Z, [P]),
             "zt_holder_buffer": (P, [P, I]),
@@ -109,6 +115,15 @@ def lib():
             fn.argtypes = args
         _lib = L
     return _lib
+
+
+def set_tuning(name, value):
+    """Force a kernel variant (include/zt_attn.h, zt_attn_set_tuning); -1 restores the shape rule."""
+    _check(lib().zt_attn_set_tuning(name.encode(), int(value)), f"zt_attn_set_tuning({name}, {value})")
+
+
+def get_tuning(name):
+    return lib().zt_attn_get_tuning(name.encode())
 
 
 def _ptr(t):
