@@ -359,6 +359,11 @@ def main():
 
     # ---------------- RMSNorm over rotating buffers ----------------
     norm = {}
+    # The launch floor: back-to-back launches of an empty kernel of the RMSNorm
+    # grids (one 256-thread workgroup per row), timed in the library itself.
+    floor = {"64 x 256 threads": round(zt.launch_floor_us(64, 256), 3),
+             "4096 x 256 threads": round(zt.launch_floor_us(4096, 256), 3)}
+    log(f"launch floor, 64 workgroups: {floor}")
     for rows, cols, sets in ((64, 4096, 256), (4096, 4096, 4)):
         xs = normal(sets * rows * cols, SEEDS["x"]).view(sets, rows * cols)
         ys = torch.empty_like(xs)
@@ -399,13 +404,15 @@ def main():
         nb = (2 * rows * cols + cols) * 4
         gbs = nb / (t_n * 1e-3) / 1e9
         gbs_g = nb / (t_g * 1e-3) / 1e9
-        norm[f"{rows}x{cols}"] = {"us": round(t_n * 1e3, 3), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM, 4),
-                                  "bytes": nb, "rotating_sets": sets,
-                                  "graph_replay": {"us": round(t_g * 1e3, 3), "GB/s": round(gbs_g, 1),
-                                                   "frac_hbm": round(gbs_g / PEAK_HBM, 4)}}
-        log(f"RMSNorm {rows}x{cols}: {t_n * 1e3:.2f} us, {gbs:.0f} GB/s; graph replay {t_g * 1e3:.2f} us, "
+        tag = f"{rows}x{cols}"
+        norm[tag] = {"us": round(t_n * 1e3, 3), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM, 4),
+                     "bytes": nb, "rotating_sets": sets,
+                     "graph_replay": {"us": round(t_g * 1e3, 3), "GB/s": round(gbs_g, 1),
+                                      "frac_hbm": round(gbs_g / PEAK_HBM, 4)}}
+        log(f"RMSNorm {tag}: {t_n * 1e3:.2f} us, {gbs:.0f} GB/s; graph replay {t_g * 1e3:.2f} us, "
             f"{gbs_g:.0f} GB/s")
         del xs, ys
+    norm["launch_floor_us"] = floor
 
     # ---------------- Reference point: a plain 1 GiB device copy ----------------
     # The achievable streaming rate on this box, and the known-size kernel that

@@ -59,7 +59,10 @@ size_t zt_attn_bwd_dkdv_shmem(int dim);
 
 /* Replaces zt_attn_forward, src/cuda/attn_kernels.cu:833-938.
  * out[t] for query rows t in [0, T) at absolute positions q_offset + t, over
- * keys s <= q_offset + t, s < n_keys (k/v hold at least n_keys rows).
+ * keys s <= q_offset + t, s < n_keys (k/v hold at least n_keys rows).  One
+ * query row (T = 1, the reference's decode route, src/decode.zig:462) runs the
+ * decode kernel over the q_offset + 1 visible keys, one chunk per workgroup,
+ * with no workspace.
  * Refusal order: T < 1; width; group; n_heads > 65535; group_q outside
  * [1, 64] or dim*group_q > 1024; q_offset < 0 || n_keys < 1 ||
  * q_offset > n_keys - T; max_tile < 1; device LDS ceiling unreadable; no
@@ -255,6 +258,12 @@ int zt_input_grad(float *din, const float *dout, const float *w, int T, int J, i
 int zt_calibrate(const float *src, size_t src_bytes, float *scratch, size_t scratch_bytes, double *mfma_tflops,
                  double *read_gbs, hipStream_t stream);
 
+/* Launch floor (no reference counterpart): `launches` back-to-back launches of
+ * an empty kernel of `blocks` workgroups x `threads` on `stream`, the average
+ * microseconds per launch (minimum of three timings after a warm-up): what a
+ * latency-bound kernel of that grid cannot go below.  Synchronises the stream. */
+int zt_calibrate_launch(unsigned blocks, unsigned threads, int launches, double *us_per_launch, hipStream_t stream);
+
 /* Seeded synthetic inputs (splitmix64 counter stream + Box-Muller): element i
  * depends only on (seed, i).  normal: mean + sigma*z; uniform: [lo, hi). */
 int zt_fill_normal(float *dst, size_t n, uint64_t seed, double mean, double sigma, hipStream_t stream);
@@ -280,7 +289,9 @@ int zt_attn_plan(int B, int T, int n_heads, int n_kv_heads, int dim, int max_til
  *   ZT_ATTN_BPAIR 0|1 (paired dq / dk/dv tiles), ZT_ATTN_DSPLIT 0|1
  *   (column-split dk/dv), ZT_ATTN_RSPLIT 0|1 (row-split dk/dv), ZT_DEC_WGS
  *   256..32768 (decode workgroup target), ZT_GEMM_TILE 32|64|128 (dense
- *   product tile), ZT_DQDS_TILE 64|128 (dq-from-dS product tile).
+ *   product tile), ZT_DQDS_TILE 64|128 (dq-from-dS product tile), ZT_ROW_G
+ *   1|2|4|8 and ZT_ROW_W 4|8 (query heads and waves per workgroup of the
+ *   one-row forward, T = 1).
  * Returns 0, or 1 (reason on stderr) for an unknown name or value.  The
  * process environment is never read.  Not synchronised with launches in
  * flight on other threads: set before launching. */

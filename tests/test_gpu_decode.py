@@ -69,6 +69,34 @@ def test_decode_through_the_reference_entry_point(gpu, zt, oracle):
     assert max_abs(out, ref) <= FWD_TOL
 
 
+@pytest.mark.parametrize("env", [{}, {"ZT_ROW_W": 4}, {"ZT_ROW_W": 8, "ZT_ROW_G": 2}, {"ZT_ROW_W": 4, "ZT_ROW_G": 2},
+                                 {"ZT_ROW_G": 4}, {"ZT_ROW_G": 8}])
+@pytest.mark.parametrize("B,H,Hkv,D,q_offset,n_keys,kv_rows", [
+    (1, 32, 8, 128, 2999, 3000, 3000),   # the reference seam: the last position sees every key
+    (1, 32, 8, 128, 1234, 3000, 3000),   # a query mid-cache sees only the first q_offset + 1 keys
+    (3, 16, 2, 256, 99, 100, 160),       # batched over a larger preallocated cache
+    (1, 6, 3, 34, 40, 41, 41), (2, 8, 8, 64, 0, 1, 5), (1, 4, 1, 96, 77, 78, 78),
+    (70, 8, 2, 80, 19, 20, 20),          # more than one launch of 64 sequences
+    (1, 16, 2, 250, 500, 600, 600), (2, 10, 5, 160, 63, 64, 64),
+])
+def test_one_row_forward_takes_the_decode_kernel(gpu, zt, oracle, tune, env, B, H, Hkv, D, q_offset, n_keys,
+                                                kv_rows):
+    """zt_attn_forward(_batched) with T = 1 runs the decode kernel with one chunk
+    per (sequence, kv head, head sub-group) and no workspace: every head
+    sub-group size and both wave counts, any width, a query anywhere in the
+    cache, caches longer than n_keys."""
+    tune(env)
+    assert zt.plan(B, 1, H, Hkv, D)[0].startswith(("zt_dec_", "zt_dec8_"))
+    q = dev_normal(gpu, zt, B * H * D, SEED_Q)
+    kc = dev_normal(gpu, zt, B * kv_rows * Hkv * D, SEED_KC)
+    vc = dev_normal(gpu, zt, B * kv_rows * Hkv * D, SEED_VC)
+    out = gpu.full((B * H * D,), float("nan"), device="cuda", dtype=gpu.float32)
+    zt.forward(q, kc, vc, out, 1, H, Hkv, D, q_offset=q_offset, n_keys=n_keys, B=B, kv_rows=kv_rows)
+    gpu.cuda.synchronize()
+    ref = oracle.attn_step(host(q), host(kc), host(vc), [q_offset + 1] * B, B, kv_rows, H, Hkv, D)
+    assert max_abs(host(out), ref) <= FWD_TOL
+
+
 def test_decode_over_a_filling_cache(gpu, zt, oracle):
     # src/decode_test.zig:222-330: every position of a filling cache agrees.
     n_ctx, H, Hkv, D = 48, 4, 2, 32

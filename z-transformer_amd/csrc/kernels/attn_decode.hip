@@ -20,6 +20,18 @@
 // Per-chunk (max, denominator, accumulator) partials go to a caller-provided
 // workspace and zt_dec_combine merges them; with one chunk per sequence the
 // workgroup writes the output itself and no combine runs.
+//
+// NW waves per workgroup take a chunk's steps in turn: four when the grid
+// fills the device, eight (zt_dec8_*, one or two query heads per workgroup)
+// when it cannot -- a single sequence decoded through zt_attn_forward with
+// T = 1 has only as many workgroups as (kv head, head sub-group) pairs, and
+// then each wave's dependent chain per step (partial dots, butterfly, running
+// max, exp, the p broadcast) bounds the rate, so two chains per SIMD instead
+// of one nearly halve the time.  Measured on MI355X (one sequence of 8192 keys,
+// 32 / 8 heads, d = 128, one query head per workgroup): four waves 237 us,
+// eight 143 us; loads two or three steps ahead instead of one gained at most
+// 8 % at four waves and nothing at eight, and sixteen waves with half the
+// loads per step (to stay within 128 registers) 150 us.
 #include "common.h"
 #include "args.h"
 
@@ -59,7 +71,7 @@ DEVI float wave_sum(float v) {
     return v;
 }
 
-template <int DP, int G>
+template <int DP, int G, int NW>
 __device__ __forceinline__ void decode_body(const DecArgs &a) {
     constexpr int LPR = DP / 4;        // lanes per cache row
     constexpr int RPI = 64 / LPR;      // rows per load instruction
@@ -67,9 +79,9 @@ __device__ __forceinline__ void decode_body(const DecArgs &a) {
     constexpr int KS = NI * RPI;       // keys per step
     constexpr int V0 = NI * G;         // partial dots per lane
     constexpr int CNT = V0 >= LPR ? V0 / LPR : 1;  // complete scores per lane
-    __shared__ float Pl[4][KS * G];
-    __shared__ float Wm[4][G], Wl[4][G];
-    __shared__ f4 Wacc[4][G][LPR];
+    __shared__ float Pl[NW][KS * G];
+    __shared__ float Wm[NW][G], Wl[NW][G];
+    __shared__ f4 Wacc[NW][G][LPR];
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int rg = lane / LPR, sub = lane % LPR;
@@ -137,15 +149,17 @@ __device__ __forceinline__ void decode_body(const DecArgs &a) {
     if (w < nsteps) load_step(w, kn, vn);
 
     // Which (row i, head gi) each of this lane's complete scores belongs to.
+    // With fewer partial dots than lanes per row, LPR / V0 lanes hold each complete score.
+    constexpr int SHARE = V0 >= LPR ? 1 : LPR / V0;
     int jidx[CNT];
 #pragma unroll
-    for (int cc = 0; cc < CNT; ++cc) jidx[cc] = (V0 >= LPR) ? sub * CNT + cc : sub / (LPR / V0);
-    const bool counted = (V0 >= LPR) || (sub % (LPR / (V0 < LPR ? V0 : LPR))) == 0;
+    for (int cc = 0; cc < CNT; ++cc) jidx[cc] = (V0 >= LPR) ? sub * CNT + cc : sub / SHARE;
+    const bool counted = sub % SHARE == 0;
 
-    for (int st = w; st < nsteps; st += 4) {
+    for (int st = w; st < nsteps; st += NW) {
 #pragma unroll
         for (int i = 0; i < NI; ++i) { kx[i] = kn[i]; vx[i] = vn[i]; }
-        if (st + 4 < nsteps) load_step(st + 4, kn, vn);
+        if (st + NW < nsteps) load_step(st + NW, kn, vn);
         const int kbase = key0 + st * KS;
 
         float part[V0];
@@ -203,7 +217,7 @@ __device__ __forceinline__ void decode_body(const DecArgs &a) {
         __builtin_amdgcn_wave_barrier();
     }
 
-    // Fold the row groups of this wave, then the four waves of the workgroup.
+    // Fold the row groups of this wave, then the NW waves of the workgroup.
 #pragma unroll
     for (int gi = 0; gi < G; ++gi) {
 #pragma unroll
@@ -218,13 +232,13 @@ __device__ __forceinline__ void decode_body(const DecArgs &a) {
         if (rg == 0) Wacc[w][gi][sub] = acc[gi];
     }
     __syncthreads();
-    for (int e = tid; e < G * LPR; e += 256) {
+    for (int e = tid; e < G * LPR; e += 64 * NW) {
         const int gi = e / LPR, sb = e % LPR;
         float M = -INFINITY;
-        for (int ww = 0; ww < 4; ++ww) M = fmaxf(M, Wm[ww][gi]);
+        for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, Wm[ww][gi]);
         float L = 0.f;
         f4 A = zero4();
-        for (int ww = 0; ww < 4; ++ww) {
+        for (int ww = 0; ww < NW; ++ww) {
             const float f = Wm[ww][gi] == -INFINITY ? 0.f : fast_exp2(Wm[ww][gi] - M);
             L += Wl[ww][gi] * f;
             A += Wacc[ww][gi][sb] * f;
@@ -278,9 +292,14 @@ extern "C" __global__ void __launch_bounds__(256) zt_dec_combine(DecArgs a) {
 
 #define ZT_DEC(DP, G)                                                                              \
     extern "C" __global__ void __launch_bounds__(256) zt_dec_d##DP##_g##G(DecArgs a) {           \
-        decode_body<DP, G>(a);                                                                     \
+        decode_body<DP, G, 4>(a);                                                                  \
     }
-#define ZT_DEC_ALL(DP) ZT_DEC(DP, 1) ZT_DEC(DP, 2) ZT_DEC(DP, 4) ZT_DEC(DP, 8)
+// Eight waves for one or two query heads per workgroup (more would spill).
+#define ZT_DEC8(DP, G)                                                                             \
+    extern "C" __global__ void __launch_bounds__(512) zt_dec8_d##DP##_g##G(DecArgs a) {          \
+        decode_body<DP, G, 8>(a);                                                                  \
+    }
+#define ZT_DEC_ALL(DP) ZT_DEC(DP, 1) ZT_DEC(DP, 2) ZT_DEC(DP, 4) ZT_DEC(DP, 8) ZT_DEC8(DP, 1) ZT_DEC8(DP, 2)
 ZT_DEC_ALL(32)
 ZT_DEC_ALL(64)
 ZT_DEC_ALL(128)

@@ -8,6 +8,8 @@
 // zt_cal_read: a grid-stride streaming read of a large buffer in 16-byte
 // nontemporal loads, the access pattern of the decode kernel, reduced to one
 // value per thread so the loads cannot be dropped.
+// zt_cal_empty: does nothing; back-to-back launches of it measure what a
+// launch alone costs on the device (the floor of a latency-bound kernel).
 #include "common.h"
 #include "args.h"
 
@@ -29,3 +31,5 @@ extern "C" __global__ void __launch_bounds__(256) zt_cal_read(CalArgs a) {
         acc += __builtin_nontemporal_load(x + i);
     a.out[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = acc.x + acc.y + acc.z + acc.w;
 }
+
+extern "C" __global__ void __launch_bounds__(1024) zt_cal_empty(CalArgs a) { (void)a; }

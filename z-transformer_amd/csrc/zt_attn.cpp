@@ -135,7 +135,7 @@ int launch(DeviceState *st, const char *name, unsigned blocks, const Args &args,
 // array of atomics: the launchers read it without a lock.
 enum Tune {
     kTuneBK, kTuneFwdW, kTuneFPF, kTuneFPair, kTuneQPF, kTuneDqW, kTuneHS, kTuneW8, kTunePF, kTuneDMA, kTuneBPair,
-    kTuneDSplit, kTuneRSplit, kTuneDecWgs, kTuneGemmTile, kTuneDqdsTile, kTuneCount
+    kTuneDSplit, kTuneRSplit, kTuneDecWgs, kTuneGemmTile, kTuneDqdsTile, kTuneRowG, kTuneRowW, kTuneCount
 };
 struct TuneSpec {
     const char *name;
@@ -159,6 +159,8 @@ const TuneSpec kTuneSpecs[kTuneCount] = {
     {"ZT_DEC_WGS", {256, 512, 768, 1024, 1536, 2048, 4096, 8192, 16384, 32768}, 10},
     {"ZT_GEMM_TILE", {32, 64, 128}, 3},
     {"ZT_DQDS_TILE", {64, 128}, 2},
+    {"ZT_ROW_G", {1, 2, 4, 8}, 4},
+    {"ZT_ROW_W", {4, 8}, 2},
 };
 std::atomic<int> g_tune[kTuneCount] = {};  // 0 = unset (no allowed value is 0 except a flag, stored as value + 1)
 
@@ -281,8 +283,10 @@ DeviceState *require_device() {
     return st;
 }
 
-bool grid_ok(unsigned long long blocks) {
-    if (blocks == 0 || blocks * kThreads > 0xFFFFFFFFull) {
+// The launch's total work-items (workgroups x threads per workgroup) must fit
+// HIP's 32-bit grid.
+bool grid_ok(unsigned long long blocks, unsigned threads = kThreads) {
+    if (blocks == 0 || blocks * threads > 0xFFFFFFFFull) {
         fprintf(stderr, "zt_attn: the launch would need %llu workgroups, beyond the 2^32 work-item grid.\n", blocks);
         return false;
     }
@@ -316,6 +320,58 @@ static bool rows_aligned(int dim, std::initializer_list<const void *> ptrs) {
     return true;
 }
 
+// One query row per sequence (T = 1: a decode step through the reference entry
+// point, src/decode.zig:462, whose query at position q_offset sees the first
+// n_vis = q_offset + 1 keys): the decode kernel with the whole visible prefix in
+// one chunk per (sequence, kv head, head sub-group), so each workgroup writes
+// `out` itself and no workspace is needed.  Measured on MI355X (C4's 64
+// sequences of 8192 keys, 32 / 8 heads, d = 128, one call per sequence): the
+// forward kernel took 665 us per call, 15 of every 16 rows of its MFMA tiles
+// idle; the decode kernel with four query heads per workgroup (8 workgroups)
+// 319 us, with one (32 workgroups, each kv head's rows read four times, the
+// repeats from cache) 237 us, and with eight waves per workgroup 143 us.
+// Without a workspace the key axis cannot be split, so a single sequence has
+// only H / G workgroups: where they cannot fill the device, G = 1 and eight
+// waves.
+// The one-row forward's head sub-group G, waves per workgroup and kernel name.
+void one_row_plan(const DeviceState *st, int B, int n_heads, int n_kv_heads, int dim, int *G_out, int *nw_out,
+                  char *name, size_t len) {
+    const int group = n_heads / n_kv_heads;
+    const int dp = dim <= 32 ? 32 : dim <= 64 ? 64 : dim <= 128 ? 128 : 256;
+    const int g_fill = group % 8 == 0 ? 8 : group % 4 == 0 ? 4 : group % 2 == 0 ? 2 : 1;
+    const bool few = (unsigned long long)B * n_kv_heads * (group / g_fill) < (unsigned long long)st->cus;
+    int G = tuned(kTuneRowG, few ? 1 : g_fill);
+    if (group % G != 0) G = 1;
+    int nw = tuned(kTuneRowW, few ? 8 : 4);
+    if (G > 2) nw = 4;  // eight waves instantiated for one or two heads per workgroup
+    snprintf(name, len, nw == 8 ? "zt_dec8_d%d_g%d" : "zt_dec_d%d_g%d", dp, G);
+    *G_out = G;
+    *nw_out = nw;
+}
+
+int forward_one_row(DeviceState *st, const float *q, const float *k, const float *v, float *out, int B, int n_heads,
+                    int n_kv_heads, int dim, int n_vis, int kv_rows, hipStream_t stream) {
+    int G = 0, nw = 0;
+    char name[64];
+    one_row_plan(st, B, n_heads, n_kv_heads, dim, &G, &nw, name, sizeof name);
+    const int n_gsub = n_heads / n_kv_heads / G;
+    DecArgs a{};
+    a.q = q; a.kc = k; a.vc = v; a.out = out;
+    a.part_acc = nullptr; a.part_ml = nullptr;  // one chunk: never touched
+    a.n_ctx = kv_rows; a.H = n_heads; a.Hkv = n_kv_heads; a.dim = dim;
+    a.chunk = n_vis; a.n_chunks = 1; a.n_gsub = n_gsub;
+    a.scale_log2e = (float)(1.4426950408889634 / std::sqrt((double)dim));
+    for (int b0 = 0; b0 < B; b0 += ZT_DEC_MAXB) {
+        a.b_base = b0;
+        a.nb = B - b0 < ZT_DEC_MAXB ? B - b0 : ZT_DEC_MAXB;
+        for (int i = 0; i < a.nb; ++i) a.n_keys[i] = n_vis;
+        const unsigned long long blocks = (unsigned long long)a.nb * n_kv_heads * n_gsub;
+        if (!grid_ok(blocks, 64u * nw)) return 1;
+        if (launch(st, name, (unsigned)blocks, a, stream, 64u * nw)) return 1;
+    }
+    return 0;
+}
+
 int forward_impl(const float *q, const float *k, const float *v, float *out, int B, int T, int n_heads,
                  int n_kv_heads, int dim, int group_q, int max_tile, int q_offset, int n_keys, int kv_rows,
                  hipStream_t stream, float *lse = nullptr, float *s_out = nullptr) {
@@ -338,6 +394,14 @@ int forward_impl(const float *q, const float *k, const float *v, float *out, int
     }
     DeviceState *st = require_device();
     if (!st) return 1;
+    if (T == 1 && !lse && !s_out) {
+        if (!q || !k || !v || !out) {
+            fprintf(stderr, "zt_attn: a null tensor pointer is not launchable.\n");
+            return 1;
+        }
+        if (!rows_aligned(dim, {q, k, v, out})) return 1;
+        return forward_one_row(st, q, k, v, out, B, n_heads, n_kv_heads, dim, q_offset + 1, kv_rows, stream);
+    }
     const int dp = pad32(dim);
     int bk = key_tile(Tiled::Forward, dp, max_tile, dim);
     if (fwd_tile_bytes(dp, bk) > st->lds_limit) bk = 32;
@@ -369,7 +433,7 @@ int forward_impl(const float *q, const float *k, const float *v, float *out, int
     a.pair = tuned(kTuneFPair, pair_pays((unsigned long long)a.n_row_tiles * a.n_head_blocks * B, st->cus));
     const unsigned long long blocks =
         (unsigned long long)(a.pair ? (a.n_row_tiles + 1) / 2 : a.n_row_tiles) * a.n_head_blocks * B;
-    if (!grid_ok(blocks)) return 1;
+    if (!grid_ok(blocks, 64u * nw)) return 1;
     char name[64];
     fwd_kernel_name(name, sizeof name, dim, dp, bk, nw);
     if (s_out && dp <= 128 && strncmp(name, "zt_fwd8p_d", 10) == 0)
@@ -482,7 +546,6 @@ int backward_prepare(const float *q, const float *k, const float *v, const float
     a->scale_log2e = (float)(1.4426950408889634 / std::sqrt((double)dim));
     const unsigned long long blocks_a =
         (unsigned long long)(a->pair ? (a->n_row_tiles + 1) / 2 : a->n_row_tiles) * a->n_head_blocks * B;
-    if (!grid_ok(blocks_a) || !grid_ok(blocks_b)) return 1;
     const bool qpf = bk == 32 && tuned(kTuneQPF, 1) == 1;
     if (saved)
         snprintf(name_dq, 64, "zt_bwd_dql_d%d_k32", dp);
@@ -503,6 +566,7 @@ int backward_prepare(const float *q, const float *k, const float *v, const float
     else
         snprintf(name_dkdv, 64, dma ? "zt_bwd_dkdv_dma_d%d_hs%d" : "zt_bwd_dkdv_d%d_hs%d", dp, hs);
     *threads_dkdv = wide || dsplit || rsplit ? 512 : kThreads;
+    if (!grid_ok(blocks_a, *threads_dq) || !grid_ok(blocks_b, *threads_dkdv)) return 1;
     *blocks_dq = (unsigned)blocks_a;
     *blocks_dkdv = (unsigned)blocks_b;
     *st_out = st;
@@ -769,9 +833,9 @@ int zt_attn_backward_train_ws(const float *q, const float *k, const float *v, co
         a.pair = tuned(kTuneBPair, pair_pays((unsigned long long)a.n_key_tiles * n_kv_heads * B, st->cus));
         const unsigned long long blocks =
             (unsigned long long)(a.pair ? (a.n_key_tiles + 1) / 2 : a.n_key_tiles) * n_kv_heads * B;
-        if (!grid_ok(blocks)) return 1;
-        blocks_b = (unsigned)blocks;
         threads_b = dp <= 128 || dsplit ? 512 : 256;
+        if (!grid_ok(blocks, threads_b)) return 1;
+        blocks_b = (unsigned)blocks;
         snprintf(name_b, sizeof name_b,
                  dp <= 128 ? "zt_bwd_dkdv8s_d%d_hs2" : dsplit ? "zt_bwd_dkdv8sd_d%d_hs2" : "zt_bwd_dkdv_dmas_d%d_hs2",
                  dp);
@@ -1081,7 +1145,12 @@ int zt_attn_plan(int B, int T, int n_heads, int n_kv_heads, int dim, int max_til
     const int dp = pad32(dim);
     int bk = key_tile(Tiled::Forward, dp, max_tile, dim);
     if (fwd_tile_bytes(dp, bk) > st->lds_limit) bk = 32;
-    fwd_kernel_name(fwd, len, dim, dp, bk, fwd_waves(heads_per_wg(n_heads / n_kv_heads)));
+    if (T == 1) {  // one query row: the decode kernel
+        int G = 0, nw = 0;
+        one_row_plan(st, B, n_heads, n_kv_heads, dim, &G, &nw, fwd, len);
+    } else {
+        fwd_kernel_name(fwd, len, dim, dp, bk, fwd_waves(heads_per_wg(n_heads / n_kv_heads)));
+    }
     BwdArgs a;
     DeviceState *st2 = nullptr;
     unsigned ba = 0, bb = 0, ta = 0, tb = 0;
@@ -1102,6 +1171,9 @@ int zt_attn_plan_train(int B, int T, int n_heads, int n_kv_heads, int dim, char 
     if (zt_attn_plan(B, T, n_heads, n_kv_heads, dim, 64, fwd, dq, dkdv, len)) return 1;
     DeviceState *st = device_state();
     if (!st) return 1;
+    if (T == 1)  // the training forward keeps lse, so one row still takes the forward kernel
+        fwd_kernel_name(fwd, len, dim, pad32(dim), key_tile(Tiled::Forward, pad32(dim), 64, dim),
+                        fwd_waves(heads_per_wg(n_heads / n_kv_heads)));
     snprintf(dq, len, "zt_gemm_dqds_%d", dqds_tile(B, T, n_heads, dim, st->cus));
     if (scores_path(dim, n_heads, n_kv_heads, st->lds_limit)) {
         const int dp = pad32(dim);
@@ -1159,6 +1231,39 @@ int zt_calibrate(const float *src, size_t src_bytes, float *scratch, size_t scra
     const double flop = 2.0 * a.iters * 2048.0 * 4.0 * mfma_blocks;
     *mfma_tflops = flop / (best_mfma * 1e-3) / 1e12;
     *read_gbs = (double)a.n4 * 16.0 / (best_read * 1e-3) / 1e9;
+    return 0;
+}
+
+int zt_calibrate_launch(unsigned blocks, unsigned threads, int launches, double *us_per_launch, hipStream_t stream) {
+    DeviceState *st = require_device();
+    if (!st) return 1;
+    if (!us_per_launch || blocks == 0 || threads == 0 || threads > 1024 || threads % 64 != 0 || launches < 1) {
+        fprintf(stderr, "zt_calibrate_launch: %u workgroups of %u threads, %d launches is not a probe.\n", blocks,
+                threads, launches);
+        return 1;
+    }
+    hipEvent_t e0, e1;
+    if (hipEventCreate(&e0) != hipSuccess) return 1;
+    if (hipEventCreate(&e1) != hipSuccess) {
+        (void)hipEventDestroy(e0);
+        return 1;
+    }
+    CalArgs a{};
+    int rc = 0;
+    float best = 1e30f;
+    for (int rep = 0; rep < 4 && rc == 0; ++rep) {  // the first warms up; min over the rest
+        float ms = 0.f;
+        rc |= hipEventRecord(e0, stream) != hipSuccess;
+        for (int i = 0; i < launches && rc == 0; ++i) rc |= launch(st, "zt_cal_empty", blocks, a, stream, threads);
+        rc |= hipEventRecord(e1, stream) != hipSuccess;
+        rc |= hipEventSynchronize(e1) != hipSuccess;
+        rc |= hipEventElapsedTime(&ms, e0, e1) != hipSuccess;
+        if (rep > 0 && ms < best) best = ms;
+    }
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    if (rc) return 1;
+    *us_per_launch = best * 1e3 / launches;
     return 0;
 }
 

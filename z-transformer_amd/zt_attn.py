@@ -26,6 +26,7 @@ ABI_SYMBOLS = [
     "zt_attn_bwd_dq_train", "zt_attn_bwd_dkdv_train", "zt_attn_plan_train", "zt_calibrate",
     "zt_matmul", "zt_weight_grad", "zt_input_grad", "zt_attn_backward_train_workspace",
     "zt_attn_backward_train_ws", "zt_attn_forward_train_ws", "zt_attn_set_tuning", "zt_attn_get_tuning",
+    "zt_calibrate_launch",
 ]
 HOLDER_SYMBOLS = [
     "zt_bytes_for", "zt_to_cint", "zt_forward_bounds", "zt_holder_init", "zt_holder_deinit",
@@ -82,6 +83,7 @@ def lib():
             "zt_weight_grad": (I, [P, P, P, I, I, I, P]),
             "zt_input_grad": (I, [P, P, P, I, I, I, P]),
             "zt_calibrate": (I, [P, Z, P, Z, P, P, P]),
+            "zt_calibrate_launch": (I, [ctypes.c_uint, ctypes.c_uint, I, P, P]),
             "zt_rope_forward": (I, [P, P, I, I, I, D, I, P]),
             "zt_rope_backward": (I, [P, P, I, I, I, D, I, P]),
             "zt_rope_qk_forward": (I, [P, P, P, P, I, I, I, I, I, I, D, P]),
@@ -340,6 +342,14 @@ def calibrate(src, scratch, stream=None):
     _check(lib().zt_calibrate(_ptr(src), src.numel() * 4, _ptr(scratch), scratch.numel() * 4, ctypes.addressof(tf),
                               ctypes.addressof(gb), _stream(stream)), "zt_calibrate")
     return tf.value, gb.value
+
+
+def launch_floor_us(blocks, threads, launches=256, stream=None):
+    """Average microseconds per back-to-back launch of an empty kernel of this grid."""
+    us = ctypes.c_double(0.0)
+    _check(lib().zt_calibrate_launch(blocks, threads, launches, ctypes.addressof(us), _stream(stream)),
+           "zt_calibrate_launch")
+    return us.value
 
 
 def fill_normal(t, seed, mean=0.0, sigma=1.0, stream=None):
