@@ -125,6 +125,22 @@ int zt_attn_decode(const float *q, const float *k_cache, const float *v_cache, f
                    const int *n_keys, int B, int n_ctx, int n_heads, int n_kv_heads, int dim,
                    void *workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* zt_attn_decode without a workspace.  No reference counterpart: it is for
+ * callers that cannot allocate (code under graph capture, tight serving loops,
+ * harnesses that forbid allocation).  The chunk partials go to a scratch array
+ * of ZT_NOALLOC_SCRATCH_BYTES = 16 MiB that is part of the library's device
+ * image, one copy per GPU, held until the process ends; the call allocates
+ * nothing (no hipMalloc, no allocating library routine).  Same arguments,
+ * semantics and refusals as zt_attn_decode, plus a refusal when the split's
+ * partials exceed the scratch (every shape at the default split fits; only a
+ * wider split forced with ZT_DEC_WGS can exceed it).  No part of the scratch
+ * needs to start at zero: the combine reads only partials the same call wrote.
+ * Every call on one GPU shares that GPU's scratch, so calls that overlap on
+ * one GPU (concurrent streams, threads) race: serialise them. */
+int zt_attn_decode_noalloc(const float *q, const float *k_cache, const float *v_cache, float *out,
+                           const int *n_keys, int B, int n_ctx, int n_heads, int n_kv_heads, int dim,
+                           hipStream_t stream);
+
 /* One decode step with the KV cache resident on the device (no counterpart:
  * the reference re-uploads the whole prefix every step, src/decode.zig:435-437).
  * For each sequence b: RoPE (src/rope.zig:21-55, theta e.g. 500000) rotates

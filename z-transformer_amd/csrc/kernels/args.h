@@ -54,6 +54,8 @@ struct BwdArgs {
 };
 
 #define ZT_MAX_DIM 256  // the widest head the library admits
+// Bytes of the fixed per-device scratch of zt_attn_decode_noalloc (noalloc.hip).
+#define ZT_NOALLOC_SCRATCH_BYTES (16u << 20)
 #define ZT_DEC_MAXB 64  // sequences per decode launch (n_keys travels in the arguments)
 
 struct DecArgs {

@@ -35,6 +35,7 @@ extern const unsigned char zt_co_dec[], zt_co_dec_end[];
 extern const unsigned char zt_co_misc[], zt_co_misc_end[];
 extern const unsigned char zt_co_cal[], zt_co_cal_end[];
 extern const unsigned char zt_co_gemm[], zt_co_gemm_end[];
+int zt_noalloc_scratch_address(void **ptr);  // noalloc.hip
 }
 
 namespace {
@@ -49,6 +50,7 @@ struct DeviceState {
     size_t lds_limit = 0;
     int cus = 0;
     hipModule_t mods[6] = {};
+    float *scratch = nullptr;  // this device's address of noalloc.hip's scratch (null: unavailable)
     std::mutex mu;
     std::unordered_map<std::string, hipFunction_t> fns;
 };
@@ -69,6 +71,10 @@ void load_device(DeviceState &st, int dev) {
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 1;
     st.cus = cus;
     st.lds_limit = (size_t)lds;
+    // The no-allocation decode's scratch: its address on this device, asked
+    // once while the device is current (each device holds its own copy).
+    void *scratch = nullptr;
+    if (zt_noalloc_scratch_address(&scratch) == 0) st.scratch = static_cast<float *>(scratch);
     st.ok = true;
 }
 
@@ -886,9 +892,9 @@ size_t zt_attn_decode_workspace(int B, int n_ctx, int n_heads, int n_kv_heads, i
     return (size_t)B * n_heads * g.n_chunks * ((size_t)dim + 2) * sizeof(float);
 }
 
-int zt_attn_decode(const float *q, const float *k_cache, const float *v_cache, float *out, const int *n_keys,
-                   int B, int n_ctx, int n_heads, int n_kv_heads, int dim, void *workspace,
-                   size_t workspace_bytes, hipStream_t stream) {
+// The decode's checks up to its workspace, shared by zt_attn_decode and
+// zt_attn_decode_noalloc: 0 when the shape is launchable.
+static int decode_check(const int *n_keys, int B, int n_ctx, int n_heads, int n_kv_heads, int dim) {
     if (B < 1 || n_ctx < 1) {
         fprintf(stderr, "zt_attn: decode over %d sequences of %d cached rows is not launchable.\n", B, n_ctx);
         return 1;
@@ -905,6 +911,20 @@ int zt_attn_decode(const float *q, const float *k_cache, const float *v_cache, f
             return 1;
         }
     }
+    return 0;
+}
+
+// Launches the decode (and, with more than one chunk per sequence, the
+// combine) with the chunk partials at `part` (only read or written when
+// there is more than one chunk).
+static int decode_launch(DeviceState *st, const float *q, const float *k_cache, const float *v_cache, float *out,
+                         const int *n_keys, int B, int n_ctx, int n_heads, int n_kv_heads, int dim, float *part,
+                         hipStream_t stream);
+
+int zt_attn_decode(const float *q, const float *k_cache, const float *v_cache, float *out, const int *n_keys,
+                   int B, int n_ctx, int n_heads, int n_kv_heads, int dim, void *workspace,
+                   size_t workspace_bytes, hipStream_t stream) {
+    if (decode_check(n_keys, B, n_ctx, n_heads, n_kv_heads, dim)) return 1;
     const size_t need = zt_attn_decode_workspace(B, n_ctx, n_heads, n_kv_heads, dim);
     if (!workspace || workspace_bytes < need) {
         fprintf(stderr, "zt_attn: decode workspace of %zu bytes is short of the %zu needed.\n", workspace_bytes,
@@ -919,10 +939,45 @@ int zt_attn_decode(const float *q, const float *k_cache, const float *v_cache, f
     if (!rows_aligned(dim, {q, k_cache, v_cache, out})) return 1;
     DeviceState *st = require_device();
     if (!st) return 1;
+    return decode_launch(st, q, k_cache, v_cache, out, n_keys, B, n_ctx, n_heads, n_kv_heads, dim,
+                         static_cast<float *>(workspace), stream);
+}
+
+int zt_attn_decode_noalloc(const float *q, const float *k_cache, const float *v_cache, float *out, const int *n_keys,
+                           int B, int n_ctx, int n_heads, int n_kv_heads, int dim, hipStream_t stream) {
+    if (decode_check(n_keys, B, n_ctx, n_heads, n_kv_heads, dim)) return 1;
+    // The partials are needed only when a sequence's keys are split into chunks.
+    const DecGeom g = decode_geom(B, n_ctx, n_heads, n_kv_heads, dim);
+    const size_t need = g.n_chunks > 1 ? zt_attn_decode_workspace(B, n_ctx, n_heads, n_kv_heads, dim) : 0;
+    if (need > ZT_NOALLOC_SCRATCH_BYTES) {
+        fprintf(stderr,
+                "zt_attn: decode_noalloc of %d sequences x %d heads in %d key chunks needs %zu bytes of partials,\n"
+                "       beyond the library's fixed %u-byte scratch. Use zt_attn_decode with a workspace.\n",
+                B, n_heads, g.n_chunks, need, ZT_NOALLOC_SCRATCH_BYTES);
+        return 1;
+    }
+    if (!q || !k_cache || !v_cache || !out) {
+        fprintf(stderr, "zt_attn: a null tensor pointer is not launchable.\n");
+        return 1;
+    }
+    if (!rows_aligned(dim, {q, k_cache, v_cache, out})) return 1;
+    DeviceState *st = require_device();
+    if (!st) return 1;
+    if (!st->scratch) {
+        fprintf(stderr, "zt_attn: decode_noalloc's scratch has no address on this device.\n");
+        return 1;
+    }
+    return decode_launch(st, q, k_cache, v_cache, out, n_keys, B, n_ctx, n_heads, n_kv_heads, dim, st->scratch,
+                         stream);
+}
+
+static int decode_launch(DeviceState *st, const float *q, const float *k_cache, const float *v_cache, float *out,
+                         const int *n_keys, int B, int n_ctx, int n_heads, int n_kv_heads, int dim, float *part,
+                         hipStream_t stream) {
     const DecGeom g = decode_geom(B, n_ctx, n_heads, n_kv_heads, dim);
     DecArgs a{};
     a.q = q; a.kc = k_cache; a.vc = v_cache; a.out = out;
-    a.part_acc = static_cast<float *>(workspace);
+    a.part_acc = part;
     a.part_ml = a.part_acc + (size_t)B * n_heads * g.n_chunks * dim;
     a.n_ctx = n_ctx; a.H = n_heads; a.Hkv = n_kv_heads; a.dim = dim;
     a.chunk = g.chunk; a.n_chunks = g.n_chunks; a.n_gsub = g.n_gsub;

@@ -26,7 +26,7 @@ ABI_SYMBOLS = [
     "zt_attn_bwd_dq_train", "zt_attn_bwd_dkdv_train", "zt_attn_plan_train", "zt_calibrate",
     "zt_matmul", "zt_weight_grad", "zt_input_grad", "zt_attn_backward_train_workspace",
     "zt_attn_backward_train_ws", "zt_attn_forward_train_ws", "zt_attn_set_tuning", "zt_attn_get_tuning",
-    "zt_calibrate_launch",
+    "zt_calibrate_launch", "zt_attn_decode_noalloc",
 ]
 HOLDER_SYMBOLS = [
     "zt_bytes_for", "zt_to_cint", "zt_forward_bounds", "zt_holder_init", "zt_holder_deinit",
@@ -68,6 +68,7 @@ def lib():
             "zt_attn_bwd_dkdv": (I, [P] * 9 + [I] * 5 + [P]),
             "zt_attn_decode_workspace": (Z, [I, I, I, I, I]),
             "zt_attn_decode": (I, [P, P, P, P, P, I, I, I, I, I, P, Z, P]),
+            "zt_attn_decode_noalloc": (I, [P, P, P, P, P, I, I, I, I, I, P]),
             "zt_attn_decode_step_workspace": (Z, [I, I, I, I, I]),
             "zt_attn_decode_step": (I, [P] * 7 + [I] * 5 + [D, P, Z, P]),
             "zt_rmsnorm_forward": (I, [P, P, P, I, I, D, P]),
