@@ -250,3 +250,4 @@ def test_train_paired_tiles_and_128_products_at_small_shapes(gpu, zt, oracle, th
     assert rel_err(dk, rk) <= BWD_REL
     assert rel_err(dv, rv) <= BWD_REL
 
+

@@ -48,7 +48,7 @@ __device__ __forceinline__ void bwd_dq_tile(const BwdArgs &a, const int tile) {
     const int hb = rem % a.n_head_blocks, b = rem / a.n_head_blocks;
     const int group = a.H / a.Hkv;
     const int h = hb * a.HW + (w % a.HW);
-    const int kvh = h / group;
+    const int kvh = ZT_PLANT == 12 ? 0 : h / group;
     const int wg_row0 = tile * 16 * RB;
     const int row0 = wg_row0 + 16 * (w / a.HW);
     const bool vec4 = (a.dim & 3) == 0;
@@ -60,7 +60,8 @@ __device__ __forceinline__ void bwd_dq_tile(const BwdArgs &a, const int tile) {
     const int my_row = row0 + l16;
     const bool row_ok = my_row < a.T;
     float qr[DQ], dor[DQ];
-    load_row_seg<DQ>(qr, a.q + qoff + (size_t)my_row * qld, grp * DQ, a.dim, vec4, row_ok, a.scale_log2e);
+    load_row_seg<DQ>(qr, a.q + qoff + (size_t)my_row * qld, grp * DQ, a.dim, vec4, row_ok,
+                     ZT_PLANT == 14 ? kLog2e : a.scale_log2e);
     load_row_seg<DQ>(dor, a.dout + qoff + (size_t)my_row * qld, grp * DQ, a.dim, vec4, row_ok, 1.f);
 
     f4 a0[NT], a1[NT];
@@ -184,7 +185,7 @@ __device__ __forceinline__ void bwd_dq_tile(const BwdArgs &a, const int tile) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int key = k0 + 16 * j + 4 * grp + r;
-                    if (key > my_row || key >= a.T) s[j][r] = -INFINITY;
+                    if ((ZT_PLANT != 11 && key > my_row) || key >= a.T) s[j][r] = -INFINITY;
                 }
             }
         }
@@ -231,11 +232,11 @@ __device__ __forceinline__ void bwd_dq_tile(const BwdArgs &a, const int tile) {
 
     const float l = sum4grp(lsum);
     const float delta = sum4grp(dlsum) / l;
-    const float f = a.scale / l;
+    const float f = (ZT_PLANT == 14 ? 1.f : a.scale) / l;
     if (row_ok) {
         float *dqrow = a.dq + qoff + (size_t)my_row * qld;
 #pragma unroll
-        for (int i = 0; i < NT; ++i) a1[i] = a1[i] - delta * a0[i];
+        for (int i = 0; i < NT; ++i) a1[i] = ZT_PLANT == 13 ? a0[i] : a1[i] - delta * a0[i];
 #pragma unroll
         for (int r = 0; r < 4; ++r) store_run<NT>(dqrow, 4 * grp + r, a.dim, vec4, a1, r, f);
         if (grp == 0) {
@@ -266,7 +267,7 @@ __device__ __forceinline__ void bwd_dq_lse_tile(const BwdArgs &a, const int tile
     const int hb = rem % a.n_head_blocks, b = rem / a.n_head_blocks;
     const int group = a.H / a.Hkv;
     const int h = hb * a.HW + (w % a.HW);
-    const int kvh = h / group;
+    const int kvh = ZT_PLANT == 12 ? 0 : h / group;
     const int wg_row0 = tile * 16 * RB;
     const int row0 = wg_row0 + 16 * (w / a.HW);
     const bool vec4 = (a.dim & 3) == 0;
@@ -278,7 +279,8 @@ __device__ __forceinline__ void bwd_dq_lse_tile(const BwdArgs &a, const int tile
     const int my_row = row0 + l16;
     const bool row_ok = my_row < a.T;
     float qr[DQ], dor[DQ];
-    load_row_seg<DQ>(qr, a.q + qoff + (size_t)my_row * qld, grp * DQ, a.dim, vec4, row_ok, a.scale_log2e);
+    load_row_seg<DQ>(qr, a.q + qoff + (size_t)my_row * qld, grp * DQ, a.dim, vec4, row_ok,
+                     ZT_PLANT == 14 ? kLog2e : a.scale_log2e);
     load_row_seg<DQ>(dor, a.dout + qoff + (size_t)my_row * qld, grp * DQ, a.dim, vec4, row_ok, 1.f);
     float delta, lse2;
     {
@@ -399,8 +401,8 @@ __device__ __forceinline__ void bwd_dq_lse_tile(const BwdArgs &a, const int tile
             for (int r = 0; r < 4; ++r) {
                 const int key = k0 + 16 * j + 4 * grp + r;
                 const float e = fast_exp2(s[j][r] - lse2);
-                const float p = (key <= my_row) ? e : 0.f;
-                s[j][r] = p * (dp[j][r] - delta);
+                const float p = (ZT_PLANT == 11 ? key < a.T : key <= my_row) ? e : 0.f;
+                s[j][r] = ZT_PLANT == 13 ? p : p * (dp[j][r] - delta);
             }
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
@@ -418,7 +420,7 @@ __device__ __forceinline__ void bwd_dq_lse_tile(const BwdArgs &a, const int tile
     if (row_ok) {
         float *dqrow = a.dq + qoff + (size_t)my_row * qld;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) store_run<NT>(dqrow, 4 * grp + r, a.dim, vec4, acc, r, a.scale);
+        for (int r = 0; r < 4; ++r) store_run<NT>(dqrow, 4 * grp + r, a.dim, vec4, acc, r, ZT_PLANT == 14 ? 1.f : a.scale);
     }
 }
 
@@ -431,10 +433,10 @@ template <int DP, int HS, int KW, bool PF = false, int NU = 1, bool SIN = false,
 __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile, const bool up) {
     static_assert(!SIN || PF, "the scores are prefetched with the stage's rows");
     static_assert(DS == 1 || (PF && DS == 2 && (DP / 32) % 2 == 0), "d-split: prefetching, whole 32-column halves");
-    constexpr int LW = DP + 4, DQ = DP / 4, NT = DP / 16, NTH = 64 * KW * HS * DS;
+    constexpr int LW = DP + 4, NTH = 64 * KW * HS * DS;
     constexpr int DPW = DP / DS, DQW = DPW / 4, NTW = DPW / 16;  // a wave's columns
     constexpr int BQ = 16 * NU;  // query rows per stage: NU sub-tiles of 16
-    // Per head-split part: Q rows, dO rows, and (m2, 1/l, delta) per row.
+    // Per head-split part: Q rows, dO rows, and (m2, delta, 1/l) per row.
     // With the register prefetch (PF) two such stage buffers: stage s reads one
     // while the prefetched rows of stage s + 1 are written to the other at its
     // end, one barrier per stage (C3, scores read: 1.83 -> 1.80 ms; forming S
@@ -461,14 +463,15 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
     const bool vec4 = (a.dim & 3) == 0;
     const size_t qld = (size_t)a.H * a.dim, kld = (size_t)a.Hkv * a.dim;
     const size_t kvoff = (size_t)b * a.T * kld + (size_t)kvh * a.dim;
+    const size_t kvrd = ZT_PLANT == 12 ? (size_t)b * a.T * kld : kvoff;  // where K and V are read
 
     const int my_key = s0 + l16;
     const bool key_ok = my_key < a.T;
     float kr[SIN ? 1 : DQW], vr[DQW];  // with the forward's scores K is not needed
     if constexpr (!SIN)
-        load_row_seg<DQW>(kr, a.k + kvoff + (size_t)my_key * kld + dh * DPW, grp * DQW, a.dim - dh * DPW, vec4, key_ok,
-                          a.scale_log2e);
-    load_row_seg<DQW>(vr, a.v + kvoff + (size_t)my_key * kld + dh * DPW, grp * DQW, a.dim - dh * DPW, vec4, key_ok,
+        load_row_seg<DQW>(kr, a.k + kvrd + (size_t)my_key * kld + dh * DPW, grp * DQW, a.dim - dh * DPW, vec4, key_ok,
+                          ZT_PLANT == 14 ? kLog2e : a.scale_log2e);
+    load_row_seg<DQW>(vr, a.v + kvrd + (size_t)my_key * kld + dh * DPW, grp * DQW, a.dim - dh * DPW, vec4, key_ok,
                       1.f);
 
     f4 dka[NTW], dva[NTW];
@@ -505,7 +508,7 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
     f4 pf[NPF];
     float pm2 = 0.f, pil = 0.f, pde = 0.f;
     bool prow = false;                      // the statistics' row is below T
-    f4 sn[SIN ? NU : 1], sc[SIN ? NU : 1];  // scores of the next / this stage (SIN)
+    f4 sn[SIN ? NU : 1];  // the score tiles of the next stage to run (SIN)
     auto fetch_piece = [&](int n, int stg) {
         const int hi = stg % hpp, t0 = tile_row(stg);
         const int e = tid + n * NTH;
@@ -515,16 +518,19 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
                             (size_t)(kvh * group + part * hpp + hi) * a.dim;
         pf[n] = *reinterpret_cast<const f4 *>(base + (r * (int)qld + c));
     };
-    auto fetch_aux = [&](int stg) {
+    // The stage's row statistics, one row per lane of wave 0 (the wave that stores them).
+    auto fetch_stats = [&](int stg) {
+        if (w != 0) return;  // wave-uniform
         const int hi = stg % hpp, t0 = tile_row(stg);
-        {
-            const int part = (lane / BQ) % HS, r = lane % BQ;
-            prow = t0 + r < a.T;
-            const size_t o = ((size_t)b * a.T + min(t0 + r, a.T - 1)) * a.H + kvh * group + part * hpp + hi;
-            pm2 = (a.lse ? a.lse : a.row_max)[o];
-            pil = (a.lse ? a.row_del : a.row_den)[o];  // unused with lse
-            pde = a.row_del[o];
-        }
+        const int part = (lane / BQ) % HS, r = lane % BQ;
+        prow = t0 + r < a.T;
+        const size_t o = ((size_t)b * a.T + min(t0 + r, a.T - 1)) * a.H + kvh * group + part * hpp + hi;
+        pm2 = (a.lse ? a.lse : a.row_max)[o];
+        pil = (a.lse ? a.row_del : a.row_den)[o];  // unused with lse
+        pde = a.row_del[o];
+    };
+    auto fetch_scores = [&](int stg) {
+        const int hi = stg % hpp, t0 = tile_row(stg);
         if constexpr (SIN) {
             // This wave's score tiles of the stage (lane order, as dS is stored).
             // A tile with no visible pair (past T, above the diagonal or past
@@ -537,7 +543,13 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
                 sn[u] = __builtin_nontemporal_load(
                     reinterpret_cast<const f4 *>(a.ds_out + (hblk + zt_tri_index(tb, min(sb, tb))) * 256) + lane);
             }
+        } else {
+            (void)hi; (void)t0;
         }
+    };
+    auto fetch_aux = [&](int stg) {
+        fetch_stats(stg);
+        fetch_scores(stg);
     };
     auto fetch = [&](int stg) {
         fetch_aux(stg);
@@ -554,22 +566,29 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
         }
         if (tid < HS * BQ) {  // rows past T: m2 = 0, 1/l = 0, delta = 0
             St[off + tid * 4 + 0] = prow ? pm2 * kLog2e : 0.f;
-            St[off + tid * 4 + 1] = prow ? (a.lse ? 1.f : 1.f / pil) : 0.f;
-            St[off + tid * 4 + 2] = prow ? pde : 0.f;
+            St[off + tid * 4 + 1] = prow ? pde : 0.f;
+            St[off + tid * 4 + 2] = prow ? (a.lse ? 1.f : 1.f / pil) : 0.f;
         }
     };
     if constexpr (PF) fetch(0);
 
-    // One stage's products for this wave, from the staged rows.
-    const float *qs = Qs + hs * BQ * LW, *ds = Ds + hs * BQ * LW, *st = St + hs * BQ * 4;
-    // nx: the stage whose rows the prefetch loads meanwhile (PF).
-    auto work = [&](int stg, int nx) {
+    // A stage's staged rows and statistics for this wave's part: with the
+    // register prefetch (PF) stage stg sits in buffer stg & 1.
+    auto stage_off = [&](int stg) { return PF ? (stg & 1) * STAGE_F : 0; };
+    // Wave-uniform: stage stg holds a visible (query, key) pair for this wave.
+    auto visible = [&](int stg) {
+        const int t0 = tile_row(stg);
+        return !(t0 + BQ - 1 < s0 || s0 >= a.T);
+    };
+
+    // The first half of a visible stage's products: dP (and S again without
+    // the forward's scores), then P and dS = P (dP - delta) into p and dsv,
+    // and dS stored for the dq product.  The prefetch of stage nx goes out
+    // between the products (PF).
+    auto front = [&](int stg, int nx, f4 (&p)[NU], f4 (&dsv)[NU]) {
         const int hi = stg % hpp, t0 = tile_row(stg);
-        if (t0 + BQ - 1 < s0 || s0 >= a.T) {  // wave-uniform: no visible pair
-            if constexpr (PF) fetch(nx);
-            if constexpr (DS > 1) __syncthreads();  // the partial-dP exchange's barrier, met by every wave
-            return;
-        }
+        const float *qs = Qs + stage_off(stg) + hs * BQ * LW, *ds = Ds + stage_off(stg) + hs * BQ * LW;
+        const float *st = St + stage_off(stg) + hs * BQ * 4;
         // The prefetch pieces go out between the first products' groups.
         constexpr int NI = DQW / 4;
         auto fetch_after = [&](int i) {
@@ -582,11 +601,20 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
 
         // Sub-tile u holds query rows t0 + 16 u + [0, 16).  This lane's four
         // rows' statistics per sub-tile are read ahead of the MFMAs.
+        // Per row (m2, delta, 1/l); with the forward's scores 1/l is 1 and not read.
         f4 stv[NU][4];
 #pragma unroll
         for (int u = 0; u < NU; ++u)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) stv[u][r] = *reinterpret_cast<const f4 *>(st + (16 * u + 4 * grp + r) * 4);
+            for (int r = 0; r < 4; ++r) {
+                const float *sr = st + (16 * u + 4 * grp + r) * 4;
+                if constexpr (SIN) {
+                    const f2 x = *reinterpret_cast<const f2 *>(sr);
+                    stv[u][r] = f4{x.x, x.y, 1.f, 0.f};
+                } else {
+                    stv[u][r] = *reinterpret_cast<const f4 *>(sr);
+                }
+            }
         f4 s[NU], dp[NU];
 #pragma unroll
         for (int u = 0; u < NU; ++u) { s[u] = zero4(); dp[u] = zero4(); }
@@ -599,7 +627,7 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
             if (DS == 1 && hs == 1) __builtin_amdgcn_s_setprio(2);
             f4 dp2[NU];
 #pragma unroll
-            for (int u = 0; u < NU; ++u) { s[u] = sc[u]; dp2[u] = zero4(); }
+            for (int u = 0; u < NU; ++u) { s[u] = sn[u]; dp2[u] = zero4(); }
             // dO operands read one group ahead of their products.
             const float *dsw = ds + dh * DPW + grp * DQW;
             f4 dxn[NU];
@@ -672,15 +700,14 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
         }
         // s[u][r] = S[t = t0 + 16 u + 4 grp + r][key = s0 + l16]
         // With the forward's scores (log-sum-exp statistics) 1/l is 1.
-        f4 p[NU], dsv[NU];
         if (t0 >= s0 + 15 && t0 + BQ <= a.T) {  // wave-uniform: every pair of the stage is visible
 #pragma unroll
             for (int u = 0; u < NU; ++u)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     p[u][r] = SIN ? fast_exp2(s[u][r] - stv[u][r].x)
-                                  : fast_exp2(s[u][r] - stv[u][r].x) * stv[u][r].y;
-                    dsv[u][r] = p[u][r] * (dp[u][r] - stv[u][r].z);
+                                  : fast_exp2(s[u][r] - stv[u][r].x) * stv[u][r].z;
+                    dsv[u][r] = ZT_PLANT == 13 ? p[u][r] : p[u][r] * (dp[u][r] - stv[u][r].y);
                 }
         } else {
 #pragma unroll
@@ -688,11 +715,11 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int t = t0 + 16 * u + 4 * grp + r;
-                    const bool vis = (t < a.T) && (t >= my_key);
+                    const bool vis = (t < a.T) && (ZT_PLANT == 11 || t >= my_key);
                     const float e = SIN ? fast_exp2(s[u][r] - stv[u][r].x)
-                                        : fast_exp2(s[u][r] - stv[u][r].x) * stv[u][r].y;
+                                        : fast_exp2(s[u][r] - stv[u][r].x) * stv[u][r].z;
                     p[u][r] = vis ? e : 0.f;
-                    dsv[u][r] = p[u][r] * (dp[u][r] - stv[u][r].z);
+                    dsv[u][r] = ZT_PLANT == 13 ? p[u][r] : p[u][r] * (dp[u][r] - stv[u][r].y);
                 }
         }
         // dS for a dq product outside this kernel, one 16 x 16 tile per (u) in lane
@@ -709,6 +736,12 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
                 __builtin_nontemporal_store(dsv[u], reinterpret_cast<f4 *>(a.ds_out + tile * 256) + lane);
             }
         }
+    };
+
+    // The second half: dV^T += dO^T P and dK^T += Q^T dS from the stage's rows.
+    auto back = [&](int stg, const f4 (&p)[NU], const f4 (&dsv)[NU]) {
+        const int t0 = tile_row(stg);
+        const float *qs = Qs + stage_off(stg) + hs * BQ * LW, *ds = Ds + stage_off(stg) + hs * BQ * LW;
 #pragma unroll
         for (int u = 0; u < NU; ++u) {
             if (t0 + 16 * u + 15 < s0) continue;  // wave-uniform: this sub-tile is wholly masked
@@ -727,19 +760,24 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
         }
     };
 
+    // One whole stage: the first half, then the second.
+    auto work = [&](int stg, int nx) {
+        if (!visible(stg)) {
+            if constexpr (PF) fetch(nx);
+            if constexpr (DS > 1) __syncthreads();  // the partial-dP exchange's barrier, met by every wave
+            return;
+        }
+        f4 p[NU], dsv[NU];
+        front(stg, nx, p, dsv);
+        back(stg, p, dsv);
+    };
+
     if constexpr (PF) {
         put(0);
         __syncthreads();
     }
     for (int stg = 0; stg < n_stage; ++stg) {
-        if constexpr (PF) {
-            const int off = (stg & 1) * STAGE_F;
-            qs = Qs + off + hs * BQ * LW; ds = Ds + off + hs * BQ * LW; st = St + off + hs * BQ * 4;
-            if constexpr (SIN) {
-#pragma unroll
-                for (int u = 0; u < NU; ++u) sc[u] = sn[u];
-            }
-        } else {
+        if constexpr (!PF) {
             __syncthreads();
             const int hi = stg % hpp, t0 = tile_row(stg);
             // Stage Q, dO rows [t0, t0+16) for every part's head.
@@ -761,8 +799,8 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
                     de = a.row_del[o];
                 }
                 St[(part * BQ + r) * 4 + 0] = m2;
-                St[(part * BQ + r) * 4 + 1] = il;
-                St[(part * BQ + r) * 4 + 2] = de;
+                St[(part * BQ + r) * 4 + 1] = de;
+                St[(part * BQ + r) * 4 + 2] = il;
             }
             __syncthreads();
         }
@@ -797,7 +835,7 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
         float *dvrow = a.dv + kvoff + (size_t)my_key * kld + dh * DPW;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            store_run<NTW>(dkrow, 4 * grp + r, a.dim - dh * DPW, vec4, dka, r, a.scale);
+            store_run<NTW>(dkrow, 4 * grp + r, a.dim - dh * DPW, vec4, dka, r, ZT_PLANT == 14 ? 1.f : a.scale);
             store_run<NTW>(dvrow, 4 * grp + r, a.dim - dh * DPW, vec4, dva, r, 1.f);
         }
     }
@@ -1154,6 +1192,7 @@ __device__ __forceinline__ void bwd_dkdv_dma_body(const BwdArgs &a) {
     ZT_BWD_DQ(DP, 32) ZT_BWD_DQ(DP, 64) ZT_BWD_DQ_PF(DP) ZT_BWD_DQ_LSE(DP) ZT_BWD_DKDV(DP, 1) ZT_BWD_DKDV(DP, 2) ZT_BWD_DKDV8(DP)    \
     ZT_BWD_DKDV_DMA(DP, 1) ZT_BWD_DKDV_DMA(DP, 2)
 
+#if ZT_PLANT == 0
 ZT_BWD_ALL(32)
 ZT_BWD_ALL(64)
 ZT_BWD_ALL(96)
@@ -1207,6 +1246,10 @@ ZT_BWD_DKDV8PD(192) ZT_BWD_DKDV8PD(256)
         bwd_dkdv_body<DP, 1, 4, true, 1, false, 2>(a);                                             \
     }
 ZT_BWD_DKDV8PD1(64) ZT_BWD_DKDV8PD1(128)
+#else
+// A planted-defect build (test-only): the kernels of the negative-control shape, d = 32.
+ZT_BWD_DQ_PF(32) ZT_BWD_DQ_LSE(32) ZT_BWD_DKDV8(32)
+#endif
 
 // delta[row] = sum_d o[row, d] * dout[row, d] over the B*T*H rows of dim
 // floats (the row statistic the dk/dv kernel needs, autograd.zig:774-797 as

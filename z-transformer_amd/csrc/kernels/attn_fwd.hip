@@ -39,7 +39,7 @@ __device__ __forceinline__ void attn_fwd_tile(const FwdArgs &a, const int tile) 
     const int hb = rem % a.n_head_blocks, b = rem / a.n_head_blocks;
     const int group = a.H / a.Hkv;
     const int h = hb * a.HW + (w % a.HW);
-    const int kvh = h / group;
+    const int kvh = ZT_PLANT == 2 ? 0 : h / group;
     const int wg_row0 = tile * 16 * RB;
     const int row0 = wg_row0 + 16 * (w / a.HW);
     const bool vec4 = (a.dim & 3) == 0;
@@ -50,7 +50,8 @@ __device__ __forceinline__ void attn_fwd_tile(const FwdArgs &a, const int tile) 
 
     const int my_row = row0 + l16;
     float qr[DQ];
-    load_row_seg<DQ>(qr, qb + (size_t)my_row * qld, grp * DQ, a.dim, vec4, my_row < a.T, a.scale_log2e);
+    load_row_seg<DQ>(qr, qb + (size_t)my_row * qld, grp * DQ, a.dim, vec4, my_row < a.T,
+                     ZT_PLANT == 4 ? kLog2e : a.scale_log2e);
 
     f4 o[NT];
 #pragma unroll
@@ -152,7 +153,7 @@ __device__ __forceinline__ void attn_fwd_tile(const FwdArgs &a, const int tile) 
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int key = k0 + 16 * j + 4 * grp + r;
-                    if (key > qpos || key >= a.n_keys) s[j][r] = -INFINITY;
+                    if ((ZT_PLANT != 1 && key > qpos) || key >= a.n_keys) s[j][r] = -INFINITY;
                 }
             }
         }
@@ -172,9 +173,9 @@ __device__ __forceinline__ void attn_fwd_tile(const FwdArgs &a, const int tile) 
                 s[j][r] = fast_exp2(s[j][r] - mnew);
                 ps += s[j][r];
             }
-        lsum = lsum * corr + ps;
+        lsum = ZT_PLANT == 3 ? lsum + ps : lsum * corr + ps;
 #pragma unroll
-        for (int i = 0; i < NT; ++i) o[i] *= corr;
+        for (int i = 0; i < NT; ++i) o[i] *= ZT_PLANT == 3 ? 1.f : corr;
 
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
@@ -229,6 +230,7 @@ __device__ __forceinline__ void attn_fwd_body(const FwdArgs &a) {
         attn_fwd_body<DP, 32, 8, true>(a);                                                         \
     }
 
+#if ZT_PLANT == 0
 ZT_FWD(32, 32) ZT_FWD(32, 64)
 ZT_FWD(64, 32) ZT_FWD(64, 64)
 ZT_FWD(96, 32) ZT_FWD(96, 64)
@@ -246,3 +248,7 @@ ZT_FWD_PF(160) ZT_FWD_PF(192) ZT_FWD_PF(224) ZT_FWD_PF(256)
         attn_fwd_body<DP, 32, 8, true>(a);                                                         \
     }
 ZT_FWD_PFS(32) ZT_FWD_PFS(64) ZT_FWD_PFS(96) ZT_FWD_PFS(128)
+#else
+// A planted-defect build (test-only): the kernels of the negative-control shape, d = 32.
+ZT_FWD_PF(32)
+#endif

@@ -28,6 +28,27 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+// Planted defects.  ZT_PLANT selects one of the defects below for the
+// test-only code objects that the negative-control tests load (built by
+// tests/planted/build.py, each into its own test library); libzt_attn.so is
+// built without it, so every `if constexpr (ZT_PLANT == n)` folds away and
+// its kernels carry no trace of them.  Each is a defect a real kernel of
+// this kind can ship with:
+//   1  forward: causal mask dropped (a query sees the later keys of its tile)
+//   2  forward: every query head reads kv head 0 (GQA collapsed)
+//   3  forward: the online softmax's running-max rescale skipped
+//   4  forward: the 1/sqrt(d) scale dropped
+//   11 backward: causal mask dropped in the dq and dk/dv kernels
+//   12 backward: K and V read from kv head 0 for every kv group
+//   13 backward: the softmax Jacobian dropped (dS = P, so dv stays right)
+//   14 backward: the 1/sqrt(d) scale dropped (scores, dq and dk)
+//   21 RMSNorm: the first weight element moved by 1e-3
+//   22 RMSNorm: the mean of x instead of the mean of its squares
+//   23 RMSNorm: the weight read from x (the wrong tensor at the right index)
+#ifndef ZT_PLANT
+#define ZT_PLANT 0
+#endif
+
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef float f2 __attribute__((ext_vector_type(2)));
 

@@ -58,10 +58,14 @@ __device__ __forceinline__ void rms_vec(const NormArgs &a) {
         // x is read once and y written once: nontemporal, so neither displaces
         // the gain row every workgroup rereads.
         xv[i] = c < n4 ? __builtin_nontemporal_load(reinterpret_cast<const f4 *>(xr) + c) : zero4();
-        ss += (double)xv[i].x * (double)xv[i].x;
-        ss += (double)xv[i].y * (double)xv[i].y;
-        ss += (double)xv[i].z * (double)xv[i].z;
-        ss += (double)xv[i].w * (double)xv[i].w;
+        if constexpr (ZT_PLANT == 22) {
+            ss += (double)xv[i].x + (double)xv[i].y + (double)xv[i].z + (double)xv[i].w;
+        } else {
+            ss += (double)xv[i].x * (double)xv[i].x;
+            ss += (double)xv[i].y * (double)xv[i].y;
+            ss += (double)xv[i].z * (double)xv[i].z;
+            ss += (double)xv[i].w * (double)xv[i].w;
+        }
     }
     const double tot = block_sum_d(ss, red);
     const float rms = (float)sqrt(tot / (double)a.cols + a.eps);
@@ -69,7 +73,8 @@ __device__ __forceinline__ void rms_vec(const NormArgs &a) {
     for (int i = 0; i < NV; ++i) {
         const int c = threadIdx.x + NTH * i;
         if (c < n4) {
-            const f4 wv = reinterpret_cast<const f4 *>(a.w)[c];
+            f4 wv = reinterpret_cast<const f4 *>(ZT_PLANT == 23 ? xr : a.w)[c];
+            if (ZT_PLANT == 21 && c == 0) wv.x += 1e-3f;
             f4 yv;
             yv.x = xv[i].x / rms * wv.x;
             yv.y = xv[i].y / rms * wv.y;

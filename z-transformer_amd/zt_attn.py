@@ -48,76 +48,83 @@ class ZtRefused(RuntimeError):
 
 
 def lib():
+    """The library built in-tree (z-transformer_amd/_build/libzt_attn.so), bound once."""
     global _lib
     if _lib is None:
         if not os.path.exists(LIB_PATH):
             raise FileNotFoundError(
                 f"{LIB_PATH} is not built; run `python z-transformer_amd/build.py` (or __graft_entry__.build())")
-        L = ctypes.CDLL(LIB_PATH)
-        P, I, Z, D, U64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t, ctypes.c_double, ctypes.c_uint64
-        sig = {
-            "zt_attn_dim_ok": (I, [I]),
-            "zt_attn_forward_shmem": (Z, [I, I, I]),
-            "zt_attn_bwd_dq_shmem": (Z, [I, I]),
-            "zt_attn_bwd_dkdv_shmem": (Z, [I]),
-            "zt_attn_forward": (I, [P, P, P, P, I, I, I, I, I, I, I, I, P]),
-            "zt_attn_backward": (I, [P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, P]),
-            "zt_attn_forward_batched": (I, [P, P, P, P, I, I, I, I, I, I, I, I, I, I, P]),
-            "zt_attn_backward_batched": (I, [P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, P]),
-            "zt_attn_bwd_dq": (I, [P] * 8 + [I] * 6 + [P]),
-            "zt_attn_bwd_dkdv": (I, [P] * 9 + [I] * 5 + [P]),
-            "zt_attn_decode_workspace": (Z, [I, I, I, I, I]),
-            "zt_attn_decode": (I, [P, P, P, P, P, I, I, I, I, I, P, Z, P]),
-            "zt_attn_decode_noalloc": (I, [P, P, P, P, P, I, I, I, I, I, P]),
-            "zt_attn_decode_step_workspace": (Z, [I, I, I, I, I]),
-            "zt_attn_decode_step": (I, [P] * 7 + [I] * 5 + [D, P, Z, P]),
-            "zt_rmsnorm_forward": (I, [P, P, P, I, I, D, P]),
-            "zt_attn_forward_train": (I, [P] * 5 + [I] * 5 + [P]),
-            "zt_attn_backward_train": (I, [P] * 10 + [I] * 5 + [P]),
-            "zt_attn_bwd_dq_train": (I, [P] * 8 + [I] * 5 + [P]),
-            "zt_attn_bwd_dkdv_train": (I, [P] * 9 + [I] * 5 + [P]),
-            "zt_attn_plan_train": (I, [I] * 5 + [P, P, P, Z]),
-            "zt_attn_backward_train_workspace": (Z, [I] * 5),
-            "zt_attn_backward_train_ws": (I, [P] * 10 + [Z] + [I] * 6 + [P]),
-            "zt_attn_forward_train_ws": (I, [P] * 6 + [Z] + [I] * 5 + [P]),
-            "zt_matmul": (I, [P, P, P, I, I, I, P]),
-            "zt_weight_grad": (I, [P, P, P, I, I, I, P]),
-            "zt_input_grad": (I, [P, P, P, I, I, I, P]),
-            "zt_calibrate": (I, [P, Z, P, Z, P, P, P]),
-            "zt_calibrate_launch": (I, [ctypes.c_uint, ctypes.c_uint, I, P, P]),
-            "zt_rope_forward": (I, [P, P, I, I, I, D, I, P]),
-            "zt_rope_backward": (I, [P, P, I, I, I, D, I, P]),
-            "zt_rope_qk_forward": (I, [P, P, P, P, I, I, I, I, I, I, D, P]),
-            "zt_rope_qk_backward": (I, [P, P, P, P, I, I, I, I, I, I, D, P]),
-            "zt_fill_normal": (I, [P, Z, U64, D, D, P]),
-            "zt_fill_uniform": (I, [P, Z, U64, D, D, P]),
-            "zt_attn_version": (ctypes.c_char_p, []),
-            "zt_attn_lds_limit": (Z, []),
-            "zt_attn_set_tuning": (I, [ctypes.c_char_p, I]),
-            "zt_attn_get_tuning": (I, [ctypes.c_char_p]),
-            "zt_attn_plan": (I, [I, I, I, I, I, I, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, Z]),
-            "zt_bytes_for": (I, [I, Z, Z, Z, Z, ctypes.POINTER(Z)]),
-            "zt_to_cint": (I, [Z, ctypes.POINTER(I)]),
-            "zt_forward_bounds": (I, [I, I, I, I]),
-            "zt_holder_init": (I, [Z, Z, Z, Z, ctypes.POINTER(P)]),
-            "zt_holder_init_exact": (I, [Z, Z, Z, Z, ctypes.POINTER(P)]),
-            "zt_holder_workspace_bytes": (Z, [P]),
-            "zt_holder_forget": (None, [P]),
-            "zt_holder_deinit": (None, [P]),
-            "zt_holder_total_bytes": (Z, [P]),
-            "zt_holder_buffer": (P, [P, I]),
-            "zt_holder_forward": (I, [P, I, I]),
-            "zt_holder_forward_at": (I, [P, I, I, I, I, I]),
-            "zt_holder_backward": (I, [P, I]),
-            "zt_holder_upload": (I, [P, I, P, Z]),
-            "zt_holder_download": (I, [P, P, I, Z]),
-        }
-        for name, (res, args) in sig.items():
-            fn = getattr(L, name)
-            fn.restype = res
-            fn.argtypes = args
-        _lib = L
+        _lib = load_library(LIB_PATH)
     return _lib
+
+
+def load_library(path):
+    """Another build of the library (the tests' planted-defect builds) with the
+    same C ABI, bound like lib() and kept separate from it."""
+    L = ctypes.CDLL(path, mode=os.RTLD_LOCAL)
+    P, I, Z, D, U64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t, ctypes.c_double, ctypes.c_uint64
+    sig = {
+        "zt_attn_dim_ok": (I, [I]),
+        "zt_attn_forward_shmem": (Z, [I, I, I]),
+        "zt_attn_bwd_dq_shmem": (Z, [I, I]),
+        "zt_attn_bwd_dkdv_shmem": (Z, [I]),
+        "zt_attn_forward": (I, [P, P, P, P, I, I, I, I, I, I, I, I, P]),
+        "zt_attn_backward": (I, [P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, P]),
+        "zt_attn_forward_batched": (I, [P, P, P, P, I, I, I, I, I, I, I, I, I, I, P]),
+        "zt_attn_backward_batched": (I, [P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, P]),
+        "zt_attn_bwd_dq": (I, [P] * 8 + [I] * 6 + [P]),
+        "zt_attn_bwd_dkdv": (I, [P] * 9 + [I] * 5 + [P]),
+        "zt_attn_decode_workspace": (Z, [I, I, I, I, I]),
+        "zt_attn_decode": (I, [P, P, P, P, P, I, I, I, I, I, P, Z, P]),
+        "zt_attn_decode_noalloc": (I, [P, P, P, P, P, I, I, I, I, I, P]),
+        "zt_attn_decode_step_workspace": (Z, [I, I, I, I, I]),
+        "zt_attn_decode_step": (I, [P] * 7 + [I] * 5 + [D, P, Z, P]),
+        "zt_rmsnorm_forward": (I, [P, P, P, I, I, D, P]),
+        "zt_attn_forward_train": (I, [P] * 5 + [I] * 5 + [P]),
+        "zt_attn_backward_train": (I, [P] * 10 + [I] * 5 + [P]),
+        "zt_attn_bwd_dq_train": (I, [P] * 8 + [I] * 5 + [P]),
+        "zt_attn_bwd_dkdv_train": (I, [P] * 9 + [I] * 5 + [P]),
+        "zt_attn_plan_train": (I, [I] * 5 + [P, P, P, Z]),
+        "zt_attn_backward_train_workspace": (Z, [I] * 5),
+        "zt_attn_backward_train_ws": (I, [P] * 10 + [Z] + [I] * 6 + [P]),
+        "zt_attn_forward_train_ws": (I, [P] * 6 + [Z] + [I] * 5 + [P]),
+        "zt_matmul": (I, [P, P, P, I, I, I, P]),
+        "zt_weight_grad": (I, [P, P, P, I, I, I, P]),
+        "zt_input_grad": (I, [P, P, P, I, I, I, P]),
+        "zt_calibrate": (I, [P, Z, P, Z, P, P, P]),
+        "zt_calibrate_launch": (I, [ctypes.c_uint, ctypes.c_uint, I, P, P]),
+        "zt_rope_forward": (I, [P, P, I, I, I, D, I, P]),
+        "zt_rope_backward": (I, [P, P, I, I, I, D, I, P]),
+        "zt_rope_qk_forward": (I, [P, P, P, P, I, I, I, I, I, I, D, P]),
+        "zt_rope_qk_backward": (I, [P, P, P, P, I, I, I, I, I, I, D, P]),
+        "zt_fill_normal": (I, [P, Z, U64, D, D, P]),
+        "zt_fill_uniform": (I, [P, Z, U64, D, D, P]),
+        "zt_attn_version": (ctypes.c_char_p, []),
+        "zt_attn_lds_limit": (Z, []),
+        "zt_attn_set_tuning": (I, [ctypes.c_char_p, I]),
+        "zt_attn_get_tuning": (I, [ctypes.c_char_p]),
+        "zt_attn_plan": (I, [I, I, I, I, I, I, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, Z]),
+        "zt_bytes_for": (I, [I, Z, Z, Z, Z, ctypes.POINTER(Z)]),
+        "zt_to_cint": (I, [Z, ctypes.POINTER(I)]),
+        "zt_forward_bounds": (I, [I, I, I, I]),
+        "zt_holder_init": (I, [Z, Z, Z, Z, ctypes.POINTER(P)]),
+        "zt_holder_init_exact": (I, [Z, Z, Z, Z, ctypes.POINTER(P)]),
+        "zt_holder_workspace_bytes": (Z, [P]),
+        "zt_holder_forget": (None, [P]),
+        "zt_holder_deinit": (None, [P]),
+        "zt_holder_total_bytes": (Z, [P]),
+        "zt_holder_buffer": (P, [P, I]),
+        "zt_holder_forward": (I, [P, I, I]),
+        "zt_holder_forward_at": (I, [P, I, I, I, I, I]),
+        "zt_holder_backward": (I, [P, I]),
+        "zt_holder_upload": (I, [P, I, P, Z]),
+        "zt_holder_download": (I, [P, P, I, Z]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    return L
 
 
 def set_tuning(name, value):
