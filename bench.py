@@ -353,9 +353,15 @@ def main():
                    M, K, N, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
         t_mm = event_time(torch, lambda: zt.lib().zt_matmul(*args_mm), 10)
         tf = 2.0 * M * K * N / (t_mm * 1e-3) / 1e12
-        mm[tag] = {"us": round(t_mm * 1e3, 2), "TFLOP/s": round(tf, 2), "frac_mfma_f32": round(tf / PEAK_MFMA_F32, 4)}
-        log(f"matmul {tag}: {t_mm * 1e3:.1f} us, {tf:.2f} TFLOP/s")
+        kname = zt.gemm_kernel(M, K, N)
+        mm[tag] = {"us": round(t_mm * 1e3, 2), "TFLOP/s": round(tf, 2), "frac_mfma_f32": round(tf / PEAK_MFMA_F32, 4),
+                   "kernel": kname}
+        log(f"matmul {tag}: {t_mm * 1e3:.1f} us, {tf:.2f} TFLOP/s ({kname})")
         del a, b, c
+    # The model shapes sit near the launch floor: empty kernels of the w_down
+    # split-K grid (128 workgroups of 16 waves), back to back.
+    mm["launch_floor_us"] = {"128 x 1024 threads": round(zt.launch_floor_us(128, 1024), 3)}
+    log(f"matmul launch floor: {mm['launch_floor_us']}")
 
     # ---------------- RMSNorm over rotating buffers ----------------
     norm = {}

@@ -264,6 +264,12 @@ int zt_matmul(const float *a, const float *b, float *out, int M, int K, int N, h
 int zt_weight_grad(float *w, const float *input, const float *dout, int T, int I, int J, hipStream_t stream);
 /* src/autograd.zig:999-1022 (inputGrad): din[T,I] += dout[T,J] w[I,J]^T. */
 int zt_input_grad(float *din, const float *dout, const float *w, int T, int J, int I, hipStream_t stream);
+/* The kernel zt_matmul launches for an M x K x N product on the current device
+ * ("zt_gemm_nn_<tile>" slab kernel or "zt_gemm_nn_sk<tile>" split-K kernel;
+ * the two gradients take the same choice for the same output shape and
+ * reduction length), into name[len].  0, or 1 if there is no usable device,
+ * the shape is empty or name is too short.  No reference counterpart. */
+int zt_matmul_plan(int M, int K, int N, char *name, int len);
 
 /* Roofline calibration (no reference counterpart): the FP32 MFMA rate this
  * device sustains (two interleaved v_mfma_f32_16x16x4_f32 chains per wave,
@@ -305,7 +311,9 @@ int zt_attn_plan(int B, int T, int n_heads, int n_kv_heads, int dim, int max_til
  *   ZT_ATTN_BPAIR 0|1 (paired dq / dk/dv tiles), ZT_ATTN_DSPLIT 0|1
  *   (column-split dk/dv), ZT_ATTN_RSPLIT 0|1 (row-split dk/dv), ZT_DEC_WGS
  *   256..32768 (decode workgroup target), ZT_GEMM_TILE 32|64|128 (dense
- *   product tile), ZT_DQDS_TILE 64|128 (dq-from-dS product tile), ZT_ROW_G
+ *   product slab tile), ZT_GEMM_SK 0|4|8|16 (dense product split-K waves, 0 =
+ *   the slab kernels), ZT_GEMM_SK_TILE 16|32 (split-K tile), ZT_DQDS_TILE
+ *   64|128 (dq-from-dS product tile), ZT_ROW_G
  *   1|2|4|8 and ZT_ROW_W 4|8 (query heads and waves per workgroup of the
  *   one-row forward, T = 1).
  * Returns 0, or 1 (reason on stderr) for an unknown name or value.  The

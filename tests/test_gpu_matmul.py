@@ -132,3 +132,46 @@ def test_every_tile_size_passes_the_gate(gpu, zt, tune, tile, M, K, N):
     assert _divergence(host(out).reshape(M, N), exact, abs_sum) < (K - 1) * EPS32
     for g in (wg, ig):
         assert _divergence(host(g).reshape(M, N), c0.astype(np.float64) + exact, abs_sum, c0) < K * EPS32
+
+
+@pytest.mark.parametrize("split,tile", [("4", "16"), ("8", "32"), ("16", "16"), ("16", "32")])
+@pytest.mark.parametrize("M,K,N", [(200, 70, 150), (33, 129, 65), (256, 512, 128), (5, 3, 7), (64, 1000, 48)])
+def test_every_split_k_variant_passes_the_gate(gpu, zt, tune, split, tile, M, K, N):
+    """The split-K kernels (forced through ZT_GEMM_SK / ZT_GEMM_SK_TILE), for
+    all three products, on ragged shapes: K not a multiple of 16, fewer
+    16-deep blocks than waves, and more than two blocks per wave."""
+    tune({"ZT_GEMM_SK": split, "ZT_GEMM_SK_TILE": tile})
+    rng = np.random.default_rng(M * K + N + int(split))
+    a = rng.uniform(-1, 1, (M, K)).astype(np.float32)
+    b = rng.uniform(-1, 1, (K, N)).astype(np.float32)
+    a64, b64 = a.astype(np.float64), b.astype(np.float64)
+    out = gpu.full((M * N,), float("nan"), device="cuda")
+    zt.matmul(_dev(gpu, a), _dev(gpu, b), out, M, K, N)
+    c0 = rng.uniform(-1, 1, (M, N)).astype(np.float32)
+    wg = _dev(gpu, c0)
+    zt.weight_grad(wg, _dev(gpu, np.ascontiguousarray(a.T)), _dev(gpu, b), K, M, N)
+    ig = _dev(gpu, c0)
+    zt.input_grad(ig, _dev(gpu, a), _dev(gpu, np.ascontiguousarray(b.T)), M, K, N)
+    gpu.cuda.synchronize()
+    exact, abs_sum = a64 @ b64, np.abs(a64) @ np.abs(b64)
+    assert _divergence(host(out).reshape(M, N), exact, abs_sum) < max(K - 1, 1) * EPS32
+    for g in (wg, ig):
+        assert _divergence(host(g).reshape(M, N), c0.astype(np.float64) + exact, abs_sum, c0) < K * EPS32
+
+
+def test_split_k_is_deterministic_and_chosen_for_the_model_shapes(gpu, zt):
+    """The model's products take the split-K kernel by the shape rule, and two
+    runs agree bit for bit (the partial tiles are summed in wave order)."""
+    for M, K, N in ((256, 512, 128), (256, 128, 512), (256, 128, 456)):
+        rng = np.random.default_rng(M + K + N)
+        a = _dev(gpu, rng.uniform(-1, 1, (M, K)))
+        b = _dev(gpu, rng.uniform(-1, 1, (K, N)))
+        outs = []
+        for _ in range(2):
+            out = gpu.full((M * N,), float("nan"), device="cuda")
+            zt.matmul(a, b, out, M, K, N)
+            gpu.cuda.synchronize()
+            outs.append(host(out).view(np.uint32))
+        assert np.array_equal(outs[0], outs[1])
+    assert zt.gemm_kernel(256, 512, 128) == "zt_gemm_nn_sk16"
+    assert zt.gemm_kernel(4096, 4096, 4096) == "zt_gemm_nn_128"

@@ -4,8 +4,9 @@
 //   zt_gemm_nt: C += A B^T    src/autograd.zig:999-1022 (inputGrad: d input += dout w^T)
 // All matrices row-major f32.  op(A) is M x K, op(B) is K x N, C is M x N.
 //
-// A workgroup of 4 waves computes a BT x BT tile of C (BT = 128, or 64 / 32
-// when the product is too small to fill the device with 128-tiles), each wave
+// Slab kernels: a workgroup of 4 waves computes a BT x BT tile of C (BT = 128,
+// or 64 / 32 when the product is too small to fill the device with 128-tiles;
+// products smaller still take the split-K kernels further down), each wave
 // a quarter as TW x TW tiles of 16 x 16 (TW = BT / 32): up to 16 independent
 // accumulation chains of v_mfma_f32_16x16x4_f32.  Each 32-deep k slab of both operands is copied to
 // LDS in the orientation it has in memory, with 16-byte loads and stores:
@@ -191,6 +192,104 @@ DEVI void gemm_body(const GemmArgs &g) {
         }
 }
 
+// Split-K variant for products too small to fill the device with slab tiles
+// (the model's own: 256 x 512 x 128 and the like).  There the slab kernels'
+// serial walk over K, a global-load round trip and two barriers per 32-deep
+// slab on a handful of workgroups, sets the time, not the MFMAs.
+//
+// A workgroup of NW waves (NW = blockDim.x / 64: 4, 8 or 16) owns a
+// 16 TW x 16 TW tile of C.  The waves split K into 16-deep blocks taken
+// round-robin (wave w: blocks w, w + NW, ...); each wave loads its blocks'
+// operands straight from global memory into MFMA operand registers (no LDS
+// staging, no barrier), the next block's loads issued before the current
+// block's MFMAs.  Lane group grp holds k = 16 kb + 4 grp + c at k-step c, as
+// the slab kernels do.  The NW partial tiles are then summed through LDS in
+// wave order: the result does not depend on timing, and needs neither atomics
+// nor a workspace.
+constexpr int SK_MAXW = 16;
+
+// MFMA operand of index r (this lane's row of op(X)) at k .. k+3 (this lane's
+// k-steps), zero past rmax / kmax.  KC: X stored index-major, k contiguous.
+template <bool KC>
+DEVI f4 sk_operand(const float *base, int ld, int r, int rmax, int k, int kmax, bool vec) {
+    f4 x = zero4();
+    if (r >= rmax) return x;
+    if constexpr (KC) {
+        x = load4(base + (size_t)r * ld + k, kmax - k, vec);
+    } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            if (k + c < kmax) x[c] = base[(size_t)(k + c) * ld + r];
+    }
+    return x;
+}
+
+template <int TW, bool A_KC, bool B_KC>
+DEVI void gemm_sk_body(const GemmArgs &g) {
+    constexpr int E = TW * TW * 256;  // floats of the workgroup's tile
+    __shared__ __attribute__((aligned(16))) float red[SK_MAXW * E];
+    const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, grp = lane >> 4;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6), nw = (int)(blockDim.x >> 6);
+    const int tiles_n = (g.N + 16 * TW - 1) / (16 * TW);
+    const int m0 = (int)(blockIdx.x / tiles_n) * 16 * TW, n0 = (int)(blockIdx.x % tiles_n) * 16 * TW;
+    const int nkb = (g.K + 15) >> 4;
+
+    f4 acc[TW][TW];
+#pragma unroll
+    for (int i = 0; i < TW; ++i)
+#pragma unroll
+        for (int j = 0; j < TW; ++j) acc[i][j] = zero4();
+
+    auto load = [&](f4 (&a)[TW], f4 (&b)[TW], int kb) {
+        const int k = 16 * kb + 4 * grp;
+#pragma unroll
+        for (int t = 0; t < TW; ++t) {
+            a[t] = sk_operand<A_KC>(g.a, g.lda, m0 + 16 * t + l16, g.M, k, g.K, g.vec_a);
+            b[t] = sk_operand<B_KC>(g.b, g.ldb, n0 + 16 * t + l16, g.N, k, g.K, g.vec_b);
+        }
+    };
+    auto mma = [&](const f4 (&a)[TW], const f4 (&b)[TW]) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int i = 0; i < TW; ++i)
+#pragma unroll
+                for (int j = 0; j < TW; ++j) acc[i][j] = mfma16(a[i][c], b[j][c], acc[i][j]);
+    };
+
+    // Two register sets: the block after next loads while a block computes.
+    f4 a0[TW], b0[TW], a1[TW], b1[TW];
+    if (w < nkb) load(a0, b0, w);
+    for (int kb = w; kb < nkb; kb += 2 * nw) {  // wave-uniform
+        if (kb + nw < nkb) load(a1, b1, kb + nw);
+        mma(a0, b0);
+        if (kb + nw >= nkb) break;
+        if (kb + 2 * nw < nkb) load(a0, b0, kb + 2 * nw);
+        mma(a1, b1);
+    }
+
+    // acc[i][j][r] = partial C[m0 + 16 i + 4 grp + r][n0 + 16 j + l16], stored
+    // at ((i TW + j) 4 + r) 64 + lane of the wave's slot.
+    float *const mine = red + w * E;
+#pragma unroll
+    for (int i = 0; i < TW; ++i)
+#pragma unroll
+        for (int j = 0; j < TW; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) mine[((i * TW + j) * 4 + r) * 64 + lane] = acc[i][j][r];
+    __syncthreads();
+    for (int e = tid; e < E; e += (int)blockDim.x) {
+        float s = red[e];
+        for (int ww = 1; ww < nw; ++ww) s += red[ww * E + e];
+        const int ln = e & 63, r = (e >> 6) & 3, ij = e >> 8;
+        const int m = m0 + 16 * (ij / TW) + 4 * (ln >> 4) + r, n = n0 + 16 * (ij % TW) + (ln & 15);
+        if (m < g.M && n < g.N) {
+            float *p = g.c + (size_t)m * g.ldc + n;
+            *p = g.accumulate ? *p + s : s;
+        }
+    }
+}
+
 // dq from a stored dS (the training backward's workspace path):
 //   dq[b, t, h, :] = scale * sum_{s <= t} dS[b, h, t, s] k[b, s, h / group, :]
 // A GEMM per (sequence, head): A = dS, B = k rows (index-contiguous: the head
@@ -354,6 +453,15 @@ DEVI void dq_ds_body(const DqDsArgs &g) {
 ZT_GEMM(128)
 ZT_GEMM(64)
 ZT_GEMM(32)
+
+// Split-K kernels: zt_gemm_<op>_sk<16 TW>, 64 NW threads (NW = 4, 8 or 16).
+#define ZT_GEMM_SK(TW, BT)                                                                               \
+    extern "C" __global__ void __launch_bounds__(1024) zt_gemm_nn_sk##BT(GemmArgs g) { gemm_sk_body<TW, true, false>(g); } \
+    extern "C" __global__ void __launch_bounds__(1024) zt_gemm_tn_sk##BT(GemmArgs g) { gemm_sk_body<TW, false, false>(g); } \
+    extern "C" __global__ void __launch_bounds__(1024) zt_gemm_nt_sk##BT(GemmArgs g) { gemm_sk_body<TW, true, true>(g); }
+
+ZT_GEMM_SK(1, 16)
+ZT_GEMM_SK(2, 32)
 
 extern "C" __global__ void __launch_bounds__(256) zt_gemm_dqds_128(DqDsArgs g) { dq_ds_body<128>(g); }
 extern "C" __global__ void __launch_bounds__(256) zt_gemm_dqds_64(DqDsArgs g) { dq_ds_body<64>(g); }

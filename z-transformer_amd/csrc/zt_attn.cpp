@@ -141,7 +141,8 @@ int launch(DeviceState *st, const char *name, unsigned blocks, const Args &args,
 // array of atomics: the launchers read it without a lock.
 enum Tune {
     kTuneBK, kTuneFwdW, kTuneFPF, kTuneFPair, kTuneQPF, kTuneDqW, kTuneHS, kTuneW8, kTunePF, kTuneDMA, kTuneBPair,
-    kTuneDSplit, kTuneRSplit, kTuneDecWgs, kTuneGemmTile, kTuneDqdsTile, kTuneRowG, kTuneRowW, kTuneCount
+    kTuneDSplit, kTuneRSplit, kTuneDecWgs, kTuneGemmTile, kTuneGemmSk, kTuneGemmSkTile, kTuneDqdsTile, kTuneRowG,
+    kTuneRowW, kTuneCount
 };
 struct TuneSpec {
     const char *name;
@@ -164,6 +165,8 @@ const TuneSpec kTuneSpecs[kTuneCount] = {
     {"ZT_ATTN_RSPLIT", {0, 1}, 2},
     {"ZT_DEC_WGS", {256, 512, 768, 1024, 1536, 2048, 4096, 8192, 16384, 32768}, 10},
     {"ZT_GEMM_TILE", {32, 64, 128}, 3},
+    {"ZT_GEMM_SK", {0, 4, 8, 16}, 4},
+    {"ZT_GEMM_SK_TILE", {16, 32}, 2},
     {"ZT_DQDS_TILE", {64, 128}, 2},
     {"ZT_ROW_G", {1, 2, 4, 8}, 4},
     {"ZT_ROW_W", {4, 8}, 2},
@@ -1322,6 +1325,45 @@ int zt_calibrate_launch(unsigned blocks, unsigned threads, int launches, double 
     return 0;
 }
 
+// The dense-product kernel for an M x N x K product: slab tile *bt (128, 64
+// or 32) with *sk = 0, or split-K tile *bt (16 or 32) with *sk waves.
+static void gemm_choose(int M, int N, int K, int n_cus, int *bt_out, int *sk_out) {
+    // The largest slab tile whose grid gives every CU a 128-tile, two 64-tiles
+    // or 1.5 32-tiles (one 64-tile per CU leaves one wave per SIMD: 1024 x
+    // 1024 x 4096 takes 119 us on 64-tiles, 104 us on 32-tiles; 640 x 1024 x
+    // 640, 400 32-tiles, 17.4 us against 20.7 us split).  Below that the
+    // split-K kernel, with enough waves that each walks at most two 16-deep
+    // blocks of K (4 to 16): on 32-tiles when they still give every CU one
+    // (512 x 4096 x 512: 39 us, against 49 us on 16-tiles and 60 us on slab
+    // 32-tiles), else on 16-tiles (the model's own products, 256 x 512 x 128
+    // and the like: 4.1 us, against 6.5 us on 32-tiles and 8.1 us on slabs).
+    auto tiles = [&](int t) { return (unsigned long long)((M + t - 1) / t) * (unsigned long long)((N + t - 1) / t); };
+    const unsigned long long cus = (unsigned long long)n_cus;
+    int bt = 128, sk = 0;
+    if (tiles(128) < cus) {
+        if (tiles(64) >= 2 * cus) {
+            bt = 64;
+        } else if (2 * tiles(32) >= 3 * cus) {
+            bt = 32;
+        } else {
+            bt = tiles(32) >= cus ? 32 : 16;
+            const int blocks_k = (K + 15) / 16;
+            sk = blocks_k <= 8 ? 4 : blocks_k <= 16 ? 8 : 16;
+        }
+    }
+    // A forced slab tile (ZT_GEMM_TILE) takes the slab kernel unless the
+    // split is forced too; a forced split (ZT_GEMM_SK > 0) its own tile.
+    if (tuned(kTuneGemmTile, 0) != 0 && tuned(kTuneGemmSk, -1) == -1) sk = 0;
+    sk = tuned(kTuneGemmSk, sk);
+    if (sk) {
+        bt = tuned(kTuneGemmSkTile, bt == 32 ? 32 : 16);
+    } else {
+        bt = tuned(kTuneGemmTile, bt == 16 ? 32 : bt);
+    }
+    *bt_out = bt;
+    *sk_out = sk;
+}
+
 // C (+)= op(A) op(B) with the kernel variant `name` (see gemm.hip).
 static int gemm_impl(const char *name, const char *what, const float *a, int lda, const float *b, int ldb, float *c,
                      int ldc, int M, int N, int K, int accumulate, hipStream_t stream) {
@@ -1339,15 +1381,12 @@ static int gemm_impl(const char *name, const char *what, const float *a, int lda
         fprintf(stderr, "%s: no usable gfx950 device or code object.\n", what);
         return 1;
     }
-    // The largest workgroup tile whose grid still gives every CU a workgroup
-    // (the model's own products, 256 x 128 x 512 and the like, would leave
-    // most of the device idle with 128-tiles).
-    auto tiles = [&](int bt) { return (unsigned long long)((M + bt - 1) / bt) * (unsigned long long)((N + bt - 1) / bt); };
-    int bt = 128;
-    if (tiles(128) < (unsigned long long)st->cus) bt = tiles(64) >= (unsigned long long)st->cus / 2 ? 64 : 32;
-    bt = tuned(kTuneGemmTile, bt);
+    int bt = 0, sk = 0;
+    gemm_choose(M, N, K, st->cus, &bt, &sk);
+    auto tiles = [&](int t) { return (unsigned long long)((M + t - 1) / t) * (unsigned long long)((N + t - 1) / t); };
     const unsigned long long blocks = tiles(bt);
-    if (!grid_ok(blocks)) return 1;
+    const unsigned threads = sk ? 64u * (unsigned)sk : kThreads;
+    if (!grid_ok(blocks, threads)) return 1;
     GemmArgs g{};
     g.a = a; g.b = b; g.c = c;
     g.M = M; g.N = N; g.K = K;
@@ -1357,8 +1396,8 @@ static int gemm_impl(const char *name, const char *what, const float *a, int lda
     g.vec_b = ldb % 4 == 0 && (uintptr_t)b % 16 == 0;
     g.vec_c = ldc % 4 == 0 && (uintptr_t)c % 16 == 0;
     char kname[32];
-    snprintf(kname, sizeof kname, "%s_%d", name, bt);
-    return launch(st, kname, (unsigned)blocks, g, stream);
+    snprintf(kname, sizeof kname, sk ? "%s_sk%d" : "%s_%d", name, bt);
+    return launch(st, kname, (unsigned)blocks, g, stream, threads);
 }
 
 int zt_matmul(const float *a, const float *b, float *out, int M, int K, int N, hipStream_t stream) {
@@ -1371,6 +1410,15 @@ int zt_weight_grad(float *w, const float *input, const float *dout, int T, int I
 
 int zt_input_grad(float *din, const float *dout, const float *w, int T, int J, int I, hipStream_t stream) {
     return gemm_impl("zt_gemm_nt", "zt_input_grad", dout, J, w, J, din, I, T, I, J, 1, stream);
+}
+
+int zt_matmul_plan(int M, int K, int N, char *name, int len) {
+    DeviceState *st = device_state();
+    if (!st || !name || len < 1 || M < 1 || N < 1 || K < 0) return 1;
+    int bt = 0, sk = 0;
+    gemm_choose(M, N, K, st->cus, &bt, &sk);
+    const int n = sk ? snprintf(name, (size_t)len, "zt_gemm_nn_sk%d", bt) : snprintf(name, (size_t)len, "zt_gemm_nn_%d", bt);
+    return n < 0 || n >= len;
 }
 
 int zt_attn_set_tuning(const char *name, int value) {

@@ -26,7 +26,7 @@ ABI_SYMBOLS = [
     "zt_attn_bwd_dq_train", "zt_attn_bwd_dkdv_train", "zt_attn_plan_train", "zt_calibrate",
     "zt_matmul", "zt_weight_grad", "zt_input_grad", "zt_attn_backward_train_workspace",
     "zt_attn_backward_train_ws", "zt_attn_forward_train_ws", "zt_attn_set_tuning", "zt_attn_get_tuning",
-    "zt_calibrate_launch", "zt_attn_decode_noalloc",
+    "zt_calibrate_launch", "zt_attn_decode_noalloc", "zt_matmul_plan",
 ]
 HOLDER_SYMBOLS = [
     "zt_bytes_for", "zt_to_cint", "zt_forward_bounds", "zt_holder_init", "zt_holder_deinit",
@@ -91,6 +91,7 @@ def load_library(path):
         "zt_matmul": (I, [P, P, P, I, I, I, P]),
         "zt_weight_grad": (I, [P, P, P, I, I, I, P]),
         "zt_input_grad": (I, [P, P, P, I, I, I, P]),
+        "zt_matmul_plan": (I, [I, I, I, P, I]),
         "zt_calibrate": (I, [P, Z, P, Z, P, P, P]),
         "zt_calibrate_launch": (I, [ctypes.c_uint, ctypes.c_uint, I, P, P]),
         "zt_rope_forward": (I, [P, P, I, I, I, D, I, P]),
@@ -329,6 +330,13 @@ def matmul(a, b, out, M, K, N, stream=None):
     if a.numel() != M * K or b.numel() != K * N or out.numel() != M * N:
         raise DimensionMismatch(f"{M}x{K} @ {K}x{N} into {out.numel()} elements")
     _check(lib().zt_matmul(_ptr(a), _ptr(b), _ptr(out), M, K, N, _stream(stream)), "zt_matmul")
+
+
+def gemm_kernel(M, K, N):
+    """The kernel zt_matmul launches for an M x K x N product."""
+    buf = ctypes.create_string_buffer(64)
+    _check(lib().zt_matmul_plan(M, K, N, buf, 64), "zt_matmul_plan")
+    return buf.value.decode()
 
 
 def weight_grad(w, inp, dout, T, I, J, stream=None):
