@@ -15,11 +15,15 @@
  *     only at the caller's next synchronising call);
  *   - return 1 = refused, with the reason on stderr; never exit();
  *   - outputs (out, dq, dk, dv) are assigned, never accumulated into.
- * One difference: inputs must be finite.  The kernels remove a masked
- * (query, key) pair with a zero weight instead of skipping its product, so an
- * inf or NaN in the K or V (or Q, dout) row of a later position can reach the
- * results of earlier rows that share its 16- or 32-row tile through 0 * inf,
- * where the reference's loops never read a masked key (src/attention.zig:117-147).
+ * One difference, for non-finite inputs only.  The reference's loops never
+ * read a masked key (src/attention.zig:117-147); here a masked pair's score is
+ * replaced by -inf (so a non-finite K row never reaches an earlier query) but
+ * its product with V is kept with weight 0, so an inf or NaN in V row s can
+ * turn column d of up to 80 earlier rows (those sharing its staged key tile)
+ * into NaN through 0 * inf, and in the backward their dq rows.  Rows before
+ * that window, the other columns and the other KV heads are bit-identical to
+ * a finite run; rows the reference reaches get what it gives; K/V rows at or
+ * past n_keys are never read (a cache need not be cleared).
  * Layout: dense row-major f32 (src/tensor.zig:3-54): q/out/dout/dq are
  * [T, n_heads*dim], k/v/dk/dv are [T, n_kv_heads*dim]; query head h reads kv
  * head h / (n_heads / n_kv_heads) (src/attention.zig:111-112).
