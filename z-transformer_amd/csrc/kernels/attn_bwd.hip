@@ -632,12 +632,10 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
 #pragma unroll
         for (int u = 0; u < NU; ++u) { s[u] = zero4(); dp[u] = zero4(); }
         if constexpr (SIN) {
-            // Scores from the forward; dP alone as two interleaved chains.  The
-            // two waves of a SIMD (head halves 0 and 1) run in step and the
-            // hardware favours the first, whose dV/dK products then starve the
-            // second's softmax; the second goes first through dP instead
-            // (C3: 1.80 -> 1.78 ms; the kernel that forms S again loses with it).
-            if (DS == 1 && hs == 1) __builtin_amdgcn_s_setprio(2);
+            // Scores from the forward; dP alone as two interleaved chains.  (Raising
+            // the second head half's wave priority through dP, so that the two
+            // waves of a SIMD leave it at different times, once gained 1%; with
+            // the dP column blocks of lane groups 1 and 2 swapped it costs 0.9%.)
             f4 dp2[NU];
 #pragma unroll
             for (int u = 0; u < NU; ++u) { s[u] = sn[u]; dp2[u] = zero4(); }
@@ -666,7 +664,6 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
             }
 #pragma unroll
             for (int u = 0; u < NU; ++u) dp[u] += dp2[u];
-            __builtin_amdgcn_s_setprio(0);
             if constexpr (DS > 1) {
                 float *xch = smem + MAIN_F;
 #pragma unroll
