@@ -459,12 +459,14 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
     // 64 banks) apart.  With grp itself the reads of rows l16 and l16 - 8 of
     // groups 0 and 1 meet in one bank: a probe of the bank-conflict counter
     // on gfx950 shows 3.8 conflict cycles per read, and none with the swap
-    // (C3 dk/dv 1.776 -> 1.762 ms).  Needs DP % 128 == 0.  The dV / dK reads
+    // (C3 dk/dv 1.776 -> 1.762 ms).  Needs DP % 128 == 0; only where the
+    // scores are read (the kernel that forms S again reads Q and dO this way
+    // too, and measured 2.268 -> 2.281 ms with the swap).  The dV / dK reads
     // (a lane per 16-byte chunk of rows 4 grp + kk) keep 3.8: no ownership of
     // chunks free of per-step address arithmetic removes them under every
     // lane grouping the probe admits, and an XOR-swizzled layout that does
     // cost more in registers and VALU than it saved (1.78 -> 1.81 ms).
-    constexpr bool PERM = DS == 1 && DP % 128 == 0;
+    constexpr bool PERM = SIN && DS == 1 && DP % 128 == 0;
     const int cbk = PERM ? ((grp & 1) << 1) | (grp >> 1) : grp;
     const int per_tile = a.Hkv * a.B;
     const int rem = (int)blockIdx.x % per_tile;
