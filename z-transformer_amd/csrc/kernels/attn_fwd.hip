@@ -162,20 +162,33 @@ __device__ __forceinline__ void attn_fwd_tile(const FwdArgs &a, const int tile) 
         for (int j = 0; j < NJ; ++j)
             mt = fmaxf(mt, fmaxf(fmaxf(s[j][0], s[j][1]), fmaxf(s[j][2], s[j][3])));
         mt = max4grp(mt);
-        const float mnew = fmaxf(m, mt);  // finite: key 0 is visible to every row
-        const float corr = fast_exp2(m - mnew);
-        m = mnew;
+        // Lazy rescaling: a row's exponent base m moves only when the row meets
+        // a tile maximum more than 8 (log2 units) above it, so between moves
+        // every exp2 stays at most 2^8 and the running sum and O need no
+        // rescaling (C3 training forward 1.114 -> 1.099 ms, C5 0.587 -> 0.577 ms;
+        // the rescale's 32 multiplies per tile ran beside no MFMA).  The first tile always moves it (m
+        // starts at -inf; key 0 is visible to every row, so mt is finite
+        // there); the result is the eager rescaling's up to rounding.  Decided
+        // per row (the four lanes of a row agree), not per wave: a row's
+        // arithmetic then depends on no other row, and the branch is skipped
+        // when no row of the wave moves.
+        if (ZT_PLANT == 3 || mt > m + 8.f) {
+            const float mnew = fmaxf(m, mt);
+            const float corr = fast_exp2(m - mnew);
+            m = mnew;
+            lsum = ZT_PLANT == 3 ? lsum : lsum * corr;
+#pragma unroll
+            for (int i = 0; i < NT; ++i) o[i] *= ZT_PLANT == 3 ? 1.f : corr;
+        }
         float ps = 0.f;
 #pragma unroll
         for (int j = 0; j < NJ; ++j)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                s[j][r] = fast_exp2(s[j][r] - mnew);
+                s[j][r] = fast_exp2(s[j][r] - m);
                 ps += s[j][r];
             }
-        lsum = ZT_PLANT == 3 ? lsum + ps : lsum * corr + ps;
-#pragma unroll
-        for (int i = 0; i < NT; ++i) o[i] *= ZT_PLANT == 3 ? 1.f : corr;
+        lsum += ps;
 
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
