@@ -81,10 +81,25 @@ __device__ __forceinline__ void bwd_dq_tile(const BwdArgs &a, const int tile) {
     // T load key T - 1 (masked, P = 0) and columns past dim the row's last
     // chunk (met by Q's and dO's zero columns, or landing in dq columns never
     // stored).  Otherwise guarded loads, all at the top of the tile.
+    // VEC: a thread's byte offsets within a tile's rows are fixed for the
+    // kernel (rows tid / CPR + j RPN, its column): a piece is one load from the
+    // tile's base plus the offset clamped (one min) to key T - 1, as in the
+    // forward (d <= 128: C3 dq kernels 2.045 -> 2.035 ms; at d = 256 the
+    // statistics-building one spills more and loses, 1.28 -> 1.32 ms).
+    constexpr int RPN = NTH / CPR;
+    constexpr int NOFF = DP <= 128 && (BK * CPR) % NTH == 0 && BK % RPN == 0 ? BK / RPN : 1;
+    unsigned voff[NOFF];
+    const unsigned coff = (unsigned)min((tid % CPR) * 4, a.dim - 4) * 4u;
+#pragma unroll
+    for (int j = 0; j < NOFF; ++j) voff[j] = (unsigned)((tid / CPR + j * RPN) * (int)kld) * 4u + coff;
     auto fetch_piece = [&](int n, int k0) {
         const int e = tid + n * NTH;
         const int arr = e / (BK * CPR), r = (e / CPR) % BK, c = (e % CPR) * 4;
-        if constexpr (VEC) {
+        if constexpr (VEC && NOFF > 1) {
+            const unsigned last = (unsigned)((a.T - 1 - k0) * (int)kld) * 4u + coff;  // key T - 1
+            const unsigned off = min(voff[(n * RPN % BK) / RPN], last);
+            pf[n] = *reinterpret_cast<const f4 *>(reinterpret_cast<const char *>((arr ? vb : kb) + (size_t)k0 * kld) + off);
+        } else if constexpr (VEC) {
             pf[n] = *reinterpret_cast<const f4 *>((arr ? vb : kb) + (size_t)k0 * kld +
                                                   (min(r, a.T - 1 - k0) * (int)kld + min(c, a.dim - 4)));
         } else {
@@ -322,10 +337,25 @@ __device__ __forceinline__ void bwd_dq_lse_tile(const BwdArgs &a, const int tile
     // T load key T - 1 (masked, P = 0) and columns past dim the row's last
     // chunk (met by Q's and dO's zero columns, or landing in dq columns never
     // stored).  Otherwise guarded loads, all at the top of the tile.
+    // VEC: a thread's byte offsets within a tile's rows are fixed for the
+    // kernel (rows tid / CPR + j RPN, its column): a piece is one load from the
+    // tile's base plus the offset clamped (one min) to key T - 1, as in the
+    // forward (d <= 128: C3 dq kernels 2.045 -> 2.035 ms; at d = 256 the
+    // statistics-building one spills more and loses, 1.28 -> 1.32 ms).
+    constexpr int RPN = NTH / CPR;
+    constexpr int NOFF = DP <= 128 && (BK * CPR) % NTH == 0 && BK % RPN == 0 ? BK / RPN : 1;
+    unsigned voff[NOFF];
+    const unsigned coff = (unsigned)min((tid % CPR) * 4, a.dim - 4) * 4u;
+#pragma unroll
+    for (int j = 0; j < NOFF; ++j) voff[j] = (unsigned)((tid / CPR + j * RPN) * (int)kld) * 4u + coff;
     auto fetch_piece = [&](int n, int k0) {
         const int e = tid + n * NTH;
         const int arr = e / (BK * CPR), r = (e / CPR) % BK, c = (e % CPR) * 4;
-        if constexpr (VEC) {
+        if constexpr (VEC && NOFF > 1) {
+            const unsigned last = (unsigned)((a.T - 1 - k0) * (int)kld) * 4u + coff;  // key T - 1
+            const unsigned off = min(voff[(n * RPN % BK) / RPN], last);
+            pf[n] = *reinterpret_cast<const f4 *>(reinterpret_cast<const char *>((arr ? vb : kb) + (size_t)k0 * kld) + off);
+        } else if constexpr (VEC) {
             pf[n] = *reinterpret_cast<const f4 *>((arr ? vb : kb) + (size_t)k0 * kld +
                                                   (min(r, a.T - 1 - k0) * (int)kld + min(c, a.dim - 4)));
         } else {
