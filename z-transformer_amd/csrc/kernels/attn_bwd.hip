@@ -96,7 +96,8 @@ __device__ __forceinline__ void bwd_dq_tile(const BwdArgs &a, const int tile) {
         const int e = tid + n * NTH;
         const int arr = e / (BK * CPR), r = (e / CPR) % BK, c = (e % CPR) * 4;
         if constexpr (VEC && NOFF > 1) {
-            const unsigned last = (unsigned)((a.T - 1 - k0) * (int)kld) * 4u + coff;  // key T - 1
+            // Key T - 1, counted within the tile (no 32-bit overflow however long T is).
+            const unsigned last = (unsigned)(min(a.T - 1 - k0, BK - 1) * (int)kld) * 4u + coff;
             const unsigned off = min(voff[(n * RPN % BK) / RPN], last);
             pf[n] = *reinterpret_cast<const f4 *>(reinterpret_cast<const char *>((arr ? vb : kb) + (size_t)k0 * kld) + off);
         } else if constexpr (VEC) {
@@ -352,7 +353,8 @@ __device__ __forceinline__ void bwd_dq_lse_tile(const BwdArgs &a, const int tile
         const int e = tid + n * NTH;
         const int arr = e / (BK * CPR), r = (e / CPR) % BK, c = (e % CPR) * 4;
         if constexpr (VEC && NOFF > 1) {
-            const unsigned last = (unsigned)((a.T - 1 - k0) * (int)kld) * 4u + coff;  // key T - 1
+            // Key T - 1, counted within the tile (no 32-bit overflow however long T is).
+            const unsigned last = (unsigned)(min(a.T - 1 - k0, BK - 1) * (int)kld) * 4u + coff;
             const unsigned off = min(voff[(n * RPN % BK) / RPN], last);
             pf[n] = *reinterpret_cast<const f4 *>(reinterpret_cast<const char *>((arr ? vb : kb) + (size_t)k0 * kld) + off);
         } else if constexpr (VEC) {
@@ -585,7 +587,8 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
         const float *base = (arr ? a.dout : a.q) + ((size_t)b * a.T + t0) * qld +
                             (size_t)(kvh * group + part * hpp + hi) * a.dim;
         if constexpr (NOFF > 1) {
-            const unsigned last = (unsigned)((a.T - 1 - t0) * (int)qld) * 4u + coff;  // row T - 1
+            // Row T - 1, counted within the stage (no 32-bit overflow however long T is).
+            const unsigned last = (unsigned)(min(a.T - 1 - t0, BQ - 1) * (int)qld) * 4u + coff;
             const unsigned off = min(voff[(n * RPN % BQ) / RPN], last);
             pf[n] = *reinterpret_cast<const f4 *>(reinterpret_cast<const char *>(base) + off);
         } else {

@@ -88,7 +88,8 @@ __device__ __forceinline__ void attn_fwd_tile(const FwdArgs &a, const int tile) 
         const int e = tid + n * NTH;
         const int arr = e / (BK * CPR);
         if constexpr (NOFF > 1) {
-            const unsigned last = (unsigned)((a.n_keys - 1 - k0) * (int)kld) * 4u + coff;  // key n_keys - 1
+            // Key n_keys - 1, counted within the tile (no 32-bit overflow however many keys).
+            const unsigned last = (unsigned)(min(a.n_keys - 1 - k0, BK - 1) * (int)kld) * 4u + coff;
             const unsigned off = min(voff[(n * RPN % BK) / RPN], last);
             pf[n] = *reinterpret_cast<const f4 *>(reinterpret_cast<const char *>((arr ? vb : kb) + (size_t)k0 * kld) + off);
         } else {
