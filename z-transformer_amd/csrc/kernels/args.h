@@ -27,7 +27,10 @@ struct FwdArgs {
 // its (sequence, head) block of zt_tri_count(nt) tiles, nt = ceil(T / 16).
 // constexpr: callable from the host launcher and from device code.
 constexpr long long zt_tri_count(int nt) { return (long long)nt * (nt + 1) / 2; }
-constexpr long long zt_tri_index(int tb, int sb) { return (long long)tb * (tb + 1) / 2 + sb; }
+// Unsigned product: no sign fix-up for the halving (tb >= 0).
+constexpr long long zt_tri_index(int tb, int sb) {
+    return (long long)(((unsigned long long)(unsigned)tb * (unsigned)(tb + 1)) >> 1) + sb;
+}
 
 struct BwdArgs {
     const float *q, *k, *v, *dout;       // q/dout [B,T,H*dim]; k/v [B,T,Hkv*dim]

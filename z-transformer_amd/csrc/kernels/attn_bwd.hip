@@ -545,10 +545,14 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
     // time in either phase and read the same Q/dO rows from L2.
     const int n_t = (a.T - wg_s0 + BQ - 1) / BQ;
     const int n_stage = hpp * n_t;
-    auto tile_row = [&](int stg) {
-        const int ri = stg / hpp;
-        return wg_s0 + (up ? ri : n_t - 1 - ri) * BQ;
-    };
+    // A stage's head hi and first row t0, kept by the stage loop as it steps
+    // (no division per stage).
+    struct StageAt { int hi, t0; };
+    auto stage_at = [&](int hi, int ri) { return StageAt{hi, wg_s0 + (up ? ri : n_t - 1 - ri) * BQ}; };
+    // Tile blocks of this workgroup's (sequence, head part) in the triangular dS layout.
+    const int nt16 = (a.T + 15) >> 4;
+    const size_t tri_cnt = (size_t)zt_tri_count(nt16);
+    const size_t hblk0 = ((size_t)b * a.H + kvh * group + hs * hpp) * tri_cnt;
 
     // Register prefetch (PF): thread tid holds float4 chunks e = tid + n * NTH
     // of the stage's HS x {Q, dO} x BQ x DP block, each lane of every wave
@@ -580,10 +584,13 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
     const unsigned coff = (unsigned)min((tid % CPR) * 4, a.dim - 4) * 4u;
 #pragma unroll
     for (int j = 0; j < NOFF; ++j) voff[j] = (unsigned)((tid / CPR + j * RPN) * (int)qld) * 4u + coff;
-    auto fetch_piece = [&](int n, int stg) {
-        const int hi = stg % hpp, t0 = tile_row(stg);
+    auto fetch_piece = [&](int n, const StageAt x) {
+        const int hi = x.hi, t0 = x.t0;
         const int e = tid + n * NTH;
-        const int part = e / (2 * BQ * CPR), arr = (e / (BQ * CPR)) & 1;
+        // With whole (part, array) blocks per piece, the piece's block follows
+        // from n alone (tid < NTH): the base stays in scalar registers.
+        const int eb = NOFF > 1 ? n * NTH : e;
+        const int part = eb / (2 * BQ * CPR), arr = (eb / (BQ * CPR)) & 1;
         const float *base = (arr ? a.dout : a.q) + ((size_t)b * a.T + t0) * qld +
                             (size_t)(kvh * group + part * hpp + hi) * a.dim;
         if constexpr (NOFF > 1) {
@@ -597,9 +604,9 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
         }
     };
     // The stage's row statistics, one row per lane of wave 0 (the wave that stores them).
-    auto fetch_stats = [&](int stg) {
+    auto fetch_stats = [&](const StageAt x) {
         if (w != 0) return;  // wave-uniform
-        const int hi = stg % hpp, t0 = tile_row(stg);
+        const int hi = x.hi, t0 = x.t0;
         const int part = (lane / BQ) % HS, r = lane % BQ;
         prow = t0 + r < a.T;
         const size_t o = ((size_t)b * a.T + min(t0 + r, a.T - 1)) * a.H + kvh * group + part * hpp + hi;
@@ -607,14 +614,14 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
         pil = (a.lse ? a.row_del : a.row_den)[o];  // unused with lse
         pde = a.row_del[o];
     };
-    auto fetch_scores = [&](int stg) {
-        const int hi = stg % hpp, t0 = tile_row(stg);
+    auto fetch_scores = [&](const StageAt x) {
+        const int hi = x.hi, t0 = x.t0;
         if constexpr (SIN) {
             // This wave's score tiles of the stage (lane order, as dS is stored).
             // A tile with no visible pair (past T, above the diagonal or past
             // the last key) loads an in-bounds tile whose values the mask drops.
-            const int nt = (a.T + 15) >> 4, sb = min(s0, a.T - 1) >> 4;
-            const size_t hblk = ((size_t)b * a.H + kvh * group + hs * hpp + hi) * zt_tri_count(nt);
+            const int sb = min(s0, a.T - 1) >> 4;
+            const size_t hblk = hblk0 + (size_t)hi * tri_cnt;
 #pragma unroll
             for (int u = 0; u < NU; ++u) {
                 const int tb = min(t0 + 16 * u, a.T - 1) >> 4;
@@ -625,14 +632,14 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
             (void)hi; (void)t0;
         }
     };
-    auto fetch_aux = [&](int stg) {
-        fetch_stats(stg);
-        fetch_scores(stg);
+    auto fetch_aux = [&](const StageAt x) {
+        fetch_stats(x);
+        fetch_scores(x);
     };
-    auto fetch = [&](int stg) {
-        fetch_aux(stg);
+    auto fetch = [&](const StageAt x) {
+        fetch_aux(x);
 #pragma unroll
-        for (int n = 0; n < NPF; ++n) fetch_piece(n, stg);
+        for (int n = 0; n < NPF; ++n) fetch_piece(n, x);
     };
     auto put = [&](int off) {
 #pragma unroll
@@ -648,23 +655,20 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
             St[off + tid * 4 + 2] = prow ? (a.lse ? 1.f : 1.f / pil) : 0.f;
         }
     };
-    if constexpr (PF) fetch(0);
+    if constexpr (PF) fetch(stage_at(0, 0));
 
     // A stage's staged rows and statistics for this wave's part: with the
     // register prefetch (PF) stage stg sits in buffer stg & 1.
     auto stage_off = [&](int stg) { return PF ? (stg & 1) * STAGE_F : 0; };
     // Wave-uniform: stage stg holds a visible (query, key) pair for this wave.
-    auto visible = [&](int stg) {
-        const int t0 = tile_row(stg);
-        return !(t0 + BQ - 1 < s0 || s0 >= a.T);
-    };
+    auto visible = [&](const StageAt x) { return !(x.t0 + BQ - 1 < s0 || s0 >= a.T); };
 
     // The first half of a visible stage's products: dP (and S again without
     // the forward's scores), then P and dS = P (dP - delta) into p and dsv,
     // and dS stored for the dq product.  The prefetch of stage nx goes out
     // between the products (PF).
-    auto front = [&](int stg, int nx, f4 (&p)[NU], f4 (&dsv)[NU]) {
-        const int hi = stg % hpp, t0 = tile_row(stg);
+    auto front = [&](int stg, const StageAt cur, const StageAt nx, f4 (&p)[NU], f4 (&dsv)[NU]) {
+        const int hi = cur.hi, t0 = cur.t0;
         const float *qs = Qs + stage_off(stg) + hs * BQ * LW, *ds = Ds + stage_off(stg) + hs * BQ * LW;
         const float *st = St + stage_off(stg) + hs * BQ * 4;
         // The prefetch pieces go out between the first products' groups.
@@ -801,21 +805,20 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
         // order; nontemporal, so the 1 GB stream does not evict the Q/dO rows
         // the other workgroups are about to reread.
         if (a.ds_out && dh == 0) {  // d-split: the partners hold the same dS; one stores it
-            const int hh = kvh * group + hs * hpp + hi;
-            const int nt = (a.T + 15) >> 4;
+            const size_t hblk = hblk0 + (size_t)hi * tri_cnt;
 #pragma unroll
             for (int u = 0; u < NU; ++u) {
                 // wave-uniform: a sub-tile past the last row or above the diagonal has no slot
                 if (t0 + 16 * u >= a.T || t0 + 16 * u + 15 < s0) continue;
-                const size_t tile = ((size_t)b * a.H + hh) * zt_tri_count(nt) + zt_tri_index((t0 >> 4) + u, s0 >> 4);
+                const size_t tile = hblk + zt_tri_index((t0 >> 4) + u, s0 >> 4);
                 __builtin_nontemporal_store(dsv[u], reinterpret_cast<f4 *>(a.ds_out + tile * 256) + lane);
             }
         }
     };
 
     // The second half: dV^T += dO^T P and dK^T += Q^T dS from the stage's rows.
-    auto back = [&](int stg, const f4 (&p)[NU], const f4 (&dsv)[NU]) {
-        const int t0 = tile_row(stg);
+    auto back = [&](int stg, const StageAt cur, const f4 (&p)[NU], const f4 (&dsv)[NU]) {
+        const int t0 = cur.t0;
         const float *qs = Qs + stage_off(stg) + hs * BQ * LW, *ds = Ds + stage_off(stg) + hs * BQ * LW;
 #pragma unroll
         for (int u = 0; u < NU; ++u) {
@@ -836,25 +839,29 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
     };
 
     // One whole stage: the first half, then the second.
-    auto work = [&](int stg, int nx) {
-        if (!visible(stg)) {
+    auto work = [&](int stg, const StageAt cur, const StageAt nx) {
+        if (!visible(cur)) {
             if constexpr (PF) fetch(nx);
             if constexpr (DS > 1) __syncthreads();  // the partial-dP exchange's barrier, met by every wave
             return;
         }
         f4 p[NU], dsv[NU];
-        front(stg, nx, p, dsv);
-        back(stg, p, dsv);
+        front(stg, cur, nx, p, dsv);
+        back(stg, cur, p, dsv);
     };
 
     if constexpr (PF) {
         put(0);
         __syncthreads();
     }
+    int shi = 0, sri = 0;  // the next stage's head and row tile
     for (int stg = 0; stg < n_stage; ++stg) {
+        const StageAt cur = stage_at(shi, sri);
+        if (stg + 1 < n_stage && ++shi == hpp) { shi = 0; ++sri; }  // the last stage fetches its own rows again, unused
+        const StageAt nx = stage_at(shi, sri);
         if constexpr (!PF) {
             __syncthreads();
-            const int hi = stg % hpp, t0 = tile_row(stg);
+            const int hi = cur.hi, t0 = cur.t0;
             // Stage Q, dO rows [t0, t0+16) for every part's head.
             const int nvalid = min(BQ, a.T - t0);
             for (int part = 0; part < HS; ++part) {
@@ -879,7 +886,7 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
             }
             __syncthreads();
         }
-        work(stg, min(stg + 1, n_stage - 1));  // the last stage fetches its own rows again, unused
+        work(stg, cur, nx);
         if constexpr (PF) {
             if (stg + 1 < n_stage) put(((stg + 1) & 1) * STAGE_F);
             __syncthreads();
