@@ -545,14 +545,26 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
     // time in either phase and read the same Q/dO rows from L2.
     const int n_t = (a.T - wg_s0 + BQ - 1) / BQ;
     const int n_stage = hpp * n_t;
-    // A stage's head hi and first row t0, kept by the stage loop as it steps
-    // (no division per stage).
-    struct StageAt { int hi, t0; };
-    auto stage_at = [&](int hi, int ri) { return StageAt{hi, wg_s0 + (up ? ri : n_t - 1 - ri) * BQ}; };
     // Tile blocks of this workgroup's (sequence, head part) in the triangular dS layout.
     const int nt16 = (a.T + 15) >> 4;
     const size_t tri_cnt = (size_t)zt_tri_count(nt16);
     const size_t hblk0 = ((size_t)b * a.H + kvh * group + hs * hpp) * tri_cnt;
+    // A stage: head hi and first row t0, kept by the stage loop as it steps (no
+    // division per stage), and the addresses its fetches and stores derive
+    // from, formed once per stage in scalar registers.
+    struct StageAt {
+        int hi, t0;
+        size_t roff;    // element offset of row t0, head hi of part 0 (q and dout alike)
+        unsigned last;  // byte offset within the stage of its last row below T
+        size_t sblk;    // first tile of head hi's dS block (this wave's part)
+    };
+    auto stage_at = [&](int hi, int ri) {
+        const int t0 = wg_s0 + (up ? ri : n_t - 1 - ri) * BQ;
+        // The offset of the last row is counted within the stage: no 32-bit overflow however long T is.
+        return StageAt{hi, t0, ((size_t)b * a.T + t0) * qld + (size_t)(kvh * group + hi) * a.dim,
+                       (unsigned)(min(a.T - 1 - t0, BQ - 1) * (int)qld) * 4u, hblk0 + (size_t)hi * tri_cnt};
+    };
+    const size_t part_off = (size_t)hpp * a.dim;  // from one part's head to the next part's
 
     // Register prefetch (PF): thread tid holds float4 chunks e = tid + n * NTH
     // of the stage's HS x {Q, dO} x BQ x DP block, each lane of every wave
@@ -591,12 +603,10 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
         // from n alone (tid < NTH): the base stays in scalar registers.
         const int eb = NOFF > 1 ? n * NTH : e;
         const int part = eb / (2 * BQ * CPR), arr = (eb / (BQ * CPR)) & 1;
-        const float *base = (arr ? a.dout : a.q) + ((size_t)b * a.T + t0) * qld +
-                            (size_t)(kvh * group + part * hpp + hi) * a.dim;
+        const float *base = (arr ? a.dout : a.q) + x.roff + part * part_off;
+        (void)hi;
         if constexpr (NOFF > 1) {
-            // Row T - 1, counted within the stage (no 32-bit overflow however long T is).
-            const unsigned last = (unsigned)(min(a.T - 1 - t0, BQ - 1) * (int)qld) * 4u + coff;
-            const unsigned off = min(voff[(n * RPN % BQ) / RPN], last);
+            const unsigned off = min(voff[(n * RPN % BQ) / RPN], x.last + coff);  // row T - 1 at most
             pf[n] = *reinterpret_cast<const f4 *>(reinterpret_cast<const char *>(base) + off);
         } else {
             const int r = min((e / CPR) % BQ, a.T - 1 - t0), c = min((e % CPR) * 4, a.dim - 4);
@@ -621,16 +631,14 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
             // A tile with no visible pair (past T, above the diagonal or past
             // the last key) loads an in-bounds tile whose values the mask drops.
             const int sb = min(s0, a.T - 1) >> 4;
-            const size_t hblk = hblk0 + (size_t)hi * tri_cnt;
 #pragma unroll
             for (int u = 0; u < NU; ++u) {
                 const int tb = min(t0 + 16 * u, a.T - 1) >> 4;
                 sn[u] = __builtin_nontemporal_load(
-                    reinterpret_cast<const f4 *>(a.ds_out + (hblk + zt_tri_index(tb, min(sb, tb))) * 256) + lane);
+                    reinterpret_cast<const f4 *>(a.ds_out + (x.sblk + zt_tri_index(tb, min(sb, tb))) * 256) + lane);
             }
-        } else {
-            (void)hi; (void)t0;
         }
+        (void)hi; (void)t0;
     };
     auto fetch_aux = [&](const StageAt x) {
         fetch_stats(x);
@@ -668,7 +676,7 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
     // and dS stored for the dq product.  The prefetch of stage nx goes out
     // between the products (PF).
     auto front = [&](int stg, const StageAt cur, const StageAt nx, f4 (&p)[NU], f4 (&dsv)[NU]) {
-        const int hi = cur.hi, t0 = cur.t0;
+        const int t0 = cur.t0;
         const float *qs = Qs + stage_off(stg) + hs * BQ * LW, *ds = Ds + stage_off(stg) + hs * BQ * LW;
         const float *st = St + stage_off(stg) + hs * BQ * 4;
         // The prefetch pieces go out between the first products' groups.
@@ -805,12 +813,11 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
         // order; nontemporal, so the 1 GB stream does not evict the Q/dO rows
         // the other workgroups are about to reread.
         if (a.ds_out && dh == 0) {  // d-split: the partners hold the same dS; one stores it
-            const size_t hblk = hblk0 + (size_t)hi * tri_cnt;
 #pragma unroll
             for (int u = 0; u < NU; ++u) {
                 // wave-uniform: a sub-tile past the last row or above the diagonal has no slot
                 if (t0 + 16 * u >= a.T || t0 + 16 * u + 15 < s0) continue;
-                const size_t tile = hblk + zt_tri_index((t0 >> 4) + u, s0 >> 4);
+                const size_t tile = cur.sblk + zt_tri_index((t0 >> 4) + u, s0 >> 4);
                 __builtin_nontemporal_store(dsv[u], reinterpret_cast<f4 *>(a.ds_out + tile * 256) + lane);
             }
         }
@@ -855,10 +862,11 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
         __syncthreads();
     }
     int shi = 0, sri = 0;  // the next stage's head and row tile
+    StageAt cur = stage_at(0, 0);
     for (int stg = 0; stg < n_stage; ++stg) {
-        const StageAt cur = stage_at(shi, sri);
-        if (stg + 1 < n_stage && ++shi == hpp) { shi = 0; ++sri; }  // the last stage fetches its own rows again, unused
-        const StageAt nx = stage_at(shi, sri);
+        // The last stage fetches its own rows again, unused.
+        if (stg + 1 < n_stage && ++shi == hpp) { shi = 0; ++sri; }
+        const StageAt nx = stg + 1 < n_stage ? stage_at(shi, sri) : cur;
         if constexpr (!PF) {
             __syncthreads();
             const int hi = cur.hi, t0 = cur.t0;
@@ -887,6 +895,7 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
             __syncthreads();
         }
         work(stg, cur, nx);
+        cur = nx;
         if constexpr (PF) {
             if (stg + 1 < n_stage) put(((stg + 1) & 1) * STAGE_F);
             __syncthreads();
