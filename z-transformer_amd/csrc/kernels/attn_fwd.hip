@@ -86,7 +86,9 @@ __device__ __forceinline__ void attn_fwd_tile(const FwdArgs &a, const int tile) 
     for (int j = 0; j < NOFF; ++j) voff[j] = (unsigned)((tid / CPR + j * RPN) * (int)kld) * 4u + coff;
     auto fetch_piece = [&](int n, int k0) {
         const int e = tid + n * NTH;
-        const int arr = e / (BK * CPR);
+        // With whole arrays per piece, the piece's array follows from n alone
+        // (tid < NTH): the base stays in scalar registers.
+        const int arr = (NOFF > 1 ? n * NTH : e) / (BK * CPR);
         if constexpr (NOFF > 1) {
             // Key n_keys - 1, counted within the tile (no 32-bit overflow however many keys).
             const unsigned last = (unsigned)(min(a.n_keys - 1 - k0, BK - 1) * (int)kld) * 4u + coff;
@@ -178,11 +180,12 @@ __device__ __forceinline__ void attn_fwd_tile(const FwdArgs &a, const int tile) 
                 }
             }
         }
-        float mt = -INFINITY;
+        float sv[4 * NJ];
 #pragma unroll
         for (int j = 0; j < NJ; ++j)
-            mt = fmaxf(mt, fmaxf(fmaxf(s[j][0], s[j][1]), fmaxf(s[j][2], s[j][3])));
-        mt = max4grp(mt);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sv[4 * j + r] = s[j][r];
+        const float mt = max4grp(vmax_n(sv));
         // Lazy rescaling: a row's exponent base m moves only when the row meets
         // a tile maximum more than 8 (log2 units) above it, so between moves
         // every exp2 stays at most 2^8 and the running sum and O need no
@@ -201,14 +204,13 @@ __device__ __forceinline__ void attn_fwd_tile(const FwdArgs &a, const int tile) 
 #pragma unroll
             for (int i = 0; i < NT; ++i) o[i] *= ZT_PLANT == 3 ? 1.f : corr;
         }
-        float ps = 0.f;
 #pragma unroll
         for (int j = 0; j < NJ; ++j)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                s[j][r] = fast_exp2(s[j][r] - m);
-                ps += s[j][r];
-            }
+            for (int r = 0; r < 4; ++r) s[j][r] = fast_exp2(s[j][r] - m);
+        float ps = s[0][0];  // = 0 + s[0][0]: the weights are >= +0
+#pragma unroll
+        for (int i = 1; i < 4 * NJ; ++i) ps += s[i / 4][i % 4];
         lsum += ps;
 
 #pragma unroll

@@ -86,11 +86,38 @@ DEVI void pair32(float v, float &a, float &b) {
     b = __uint_as_float(r[1]);
 }
 
+// Maxima on v_max_f32 / v_max3_f32 as they stand.  fmaxf first quiets every
+// operand the compiler cannot show to be quiet, one more v_max_f32 x, x, x per
+// MFMA result or lane-swapped copy; the operands here are those and never
+// signalling NaNs, for which the two agree (a quiet NaN operand yields the
+// other operand, in the hardware's IEEE mode as in fmaxf).
+DEVI float vmax(float a, float b) {
+    float r;
+    asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+DEVI float vmax3(float a, float b, float c) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+// Maximum of the N values x[0..N).
+template <int N>
+DEVI float vmax_n(const float (&x)[N]) {
+    static_assert(N >= 2, "two values at least");
+    float m = vmax(x[0], x[1]);
+    int i = 2;
+#pragma unroll
+    for (; i + 1 < N; i += 2) m = vmax3(m, x[i], x[i + 1]);
+    if (i < N) m = vmax(m, x[i]);
+    return m;
+}
+
 DEVI float max4grp(float v) {  // max over the four lane groups sharing l16
     float a, b;
     pair16(v, a, b);
-    pair32(fmaxf(a, b), a, b);
-    return fmaxf(a, b);
+    pair32(vmax(a, b), a, b);
+    return vmax(a, b);
 }
 // Sum over the four lane groups sharing l16 (each step adds one pair, and a
 // two-operand f32 add does not depend on operand order, so all four agree).
