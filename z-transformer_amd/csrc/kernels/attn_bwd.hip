@@ -481,7 +481,8 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
     constexpr int LW = DP + 4, NTH = 64 * KW * HS * DS;
     constexpr int DPW = DP / DS, DQW = DPW / 4, NTW = DPW / 16;  // a wave's columns
     constexpr int BQ = 16 * NU;  // query rows per stage: NU sub-tiles of 16
-    // Per head-split part: Q rows, dO rows, and (m2, delta, 1/l) per row.
+    // Per head-split part: Q rows, dO rows, and the rows' m2, -delta and 1/l
+    // (BQ floats each, so that a lane reads its four rows' values as one float4).
     // With the register prefetch (PF) two such stage buffers: stage s reads one
     // while the prefetched rows of stage s + 1 are written to the other at its
     // end, one barrier per stage (C3, scores read: 1.83 -> 1.80 ms; forming S
@@ -634,8 +635,9 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
 #pragma unroll
             for (int u = 0; u < NU; ++u) {
                 const int tb = min(t0 + 16 * u, a.T - 1) >> 4;
-                sn[u] = __builtin_nontemporal_load(
-                    reinterpret_cast<const f4 *>(a.ds_out + (x.sblk + zt_tri_index(tb, min(sb, tb))) * 256) + lane);
+                sn[u] = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(
+                    reinterpret_cast<const char *>(a.ds_out + (x.sblk + zt_tri_index(tb, min(sb, tb))) * 256) +
+                    lane * 16u));
             }
         }
         (void)hi; (void)t0;
@@ -658,9 +660,10 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
             *reinterpret_cast<f4 *>((arr ? Ds : Qs) + off + (part * BQ + r) * LW + c) = pf[n];
         }
         if (tid < HS * BQ) {  // rows past T: m2 = 0, 1/l = 0, delta = 0
-            St[off + tid * 4 + 0] = prow ? pm2 * kLog2e : 0.f;
-            St[off + tid * 4 + 1] = prow ? pde : 0.f;
-            St[off + tid * 4 + 2] = prow ? (a.lse ? 1.f : 1.f / pil) : 0.f;
+            float *sr = St + off + (tid / BQ) * 4 * BQ + tid % BQ;
+            sr[0] = prow ? pm2 * kLog2e : 0.f;
+            sr[BQ] = prow ? -pde : 0.f;
+            sr[2 * BQ] = prow ? (a.lse ? 1.f : 1.f / pil) : 0.f;
         }
     };
     if constexpr (PF) fetch(stage_at(0, 0));
@@ -678,41 +681,39 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
     auto front = [&](int stg, const StageAt cur, const StageAt nx, f4 (&p)[NU], f4 (&dsv)[NU]) {
         const int t0 = cur.t0;
         const float *qs = Qs + stage_off(stg) + hs * BQ * LW, *ds = Ds + stage_off(stg) + hs * BQ * LW;
-        const float *st = St + stage_off(stg) + hs * BQ * 4;
-        // The prefetch pieces go out between the first products' groups.
+        const float *st = St + stage_off(stg) + hs * 4 * BQ;
+        // The prefetch pieces go out between the first products' groups (the
+        // next stage's scores after this stage's have been used).
         constexpr int NI = DQW / 4;
         auto fetch_after = [&](int i) {
             if constexpr (PF) {
-                if (i == 0) fetch_aux(nx);
+                if (i == 0) fetch_stats(nx);
 #pragma unroll
                 for (int n = i * NPF / NI; n < (i + 1) * NPF / NI; ++n) fetch_piece(n, nx);
             }
         };
 
-        // Sub-tile u holds query rows t0 + 16 u + [0, 16).  This lane's four
-        // rows' statistics per sub-tile are read ahead of the MFMAs.
-        // Per row (m2, delta, 1/l); with the forward's scores 1/l is 1 and not read.
-        f4 stv[NU][4];
+        // Sub-tile u holds query rows t0 + 16 u + [0, 16); this lane's four
+        // rows 4 grp + r: m2 and 1/l (read ahead of the MFMAs), and -delta as
+        // the dP accumulator's start, so that the products leave dP - delta
+        // (d-split: in one of the two partial sums).  With the forward's scores
+        // 1/l is 1 and not read.
+        f4 m2v[NU], ilv[NU], s[NU], dp[NU];
 #pragma unroll
-        for (int u = 0; u < NU; ++u)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float *sr = st + (16 * u + 4 * grp + r) * 4;
-                if constexpr (SIN) {
-                    const f2 x = *reinterpret_cast<const f2 *>(sr);
-                    stv[u][r] = f4{x.x, x.y, 1.f, 0.f};
-                } else {
-                    stv[u][r] = *reinterpret_cast<const f4 *>(sr);
-                }
-            }
-        f4 s[NU], dp[NU];
-#pragma unroll
-        for (int u = 0; u < NU; ++u) { s[u] = zero4(); dp[u] = zero4(); }
+        for (int u = 0; u < NU; ++u) {
+            m2v[u] = *reinterpret_cast<const f4 *>(st + 16 * u + 4 * grp);
+            ilv[u] = SIN ? f4{1.f, 1.f, 1.f, 1.f} : *reinterpret_cast<const f4 *>(st + 2 * BQ + 16 * u + 4 * grp);
+            dp[u] = DS == 1 || dh == 0 ? *reinterpret_cast<const f4 *>(st + BQ + 16 * u + 4 * grp) : zero4();
+            s[u] = zero4();
+        }
         if constexpr (SIN) {
-            // Scores from the forward; dP alone as two interleaved chains.  (Raising
-            // the second head half's wave priority through dP, so that the two
-            // waves of a SIMD leave it at different times, once gained 1%; with
-            // the dP column blocks of lane groups 1 and 2 swapped it costs 0.9%.)
+            // Scores from the forward; dP alone, as one chain per sub-tile with
+            // the sub-tiles' products interleaved (NU >= 2), else as two chains
+            // summed.  (Raising the second head half's wave priority through dP,
+            // so that the two waves of a SIMD leave it at different times, once
+            // gained 1%; with the dP column blocks of lane groups 1 and 2 swapped
+            // it costs 0.9%.)
+            constexpr bool TWO = NU < 2;
             f4 dp2[NU];
 #pragma unroll
             for (int u = 0; u < NU; ++u) { s[u] = sn[u]; dp2[u] = zero4(); }
@@ -730,17 +731,26 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
                     if (kk + 4 < DQW) dxn[u] = *reinterpret_cast<const f4 *>(dsw + (16 * u + l16) * LW + kk + 4);
                 }
                 __builtin_amdgcn_sched_barrier(0);  // keeps the reads ahead of this group's products
+                if constexpr (TWO) {
 #pragma unroll
-                for (int u = 0; u < NU; ++u) {
-                    dp[u] = mfma16(dx[u].x, vr[kk + 0], dp[u]);
-                    dp2[u] = mfma16(dx[u].y, vr[kk + 1], dp2[u]);
-                    dp[u] = mfma16(dx[u].z, vr[kk + 2], dp[u]);
-                    dp2[u] = mfma16(dx[u].w, vr[kk + 3], dp2[u]);
+                    for (int u = 0; u < NU; ++u) {
+                        dp[u] = mfma16(dx[u].x, vr[kk + 0], dp[u]);
+                        dp2[u] = mfma16(dx[u].y, vr[kk + 1], dp2[u]);
+                        dp[u] = mfma16(dx[u].z, vr[kk + 2], dp[u]);
+                        dp2[u] = mfma16(dx[u].w, vr[kk + 3], dp2[u]);
+                    }
+                } else {
+#pragma unroll
+                    for (int c = 0; c < 4; ++c)
+#pragma unroll
+                        for (int u = 0; u < NU; ++u) dp[u] = mfma16(dx[u][c], vr[kk + c], dp[u]);
                 }
                 fetch_after(kk / 4);
             }
+            if constexpr (TWO) {
 #pragma unroll
-            for (int u = 0; u < NU; ++u) dp[u] += dp2[u];
+                for (int u = 0; u < NU; ++u) dp[u] += dp2[u];
+            }
             if constexpr (DS > 1) {
                 float *xch = smem + MAIN_F;
 #pragma unroll
@@ -785,16 +795,15 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
                 }
             }
         }
-        // s[u][r] = S[t = t0 + 16 u + 4 grp + r][key = s0 + l16]
+        // s[u][r] = S[t = t0 + 16 u + 4 grp + r][key = s0 + l16], dp[u][r] = dP - delta there.
         // With the forward's scores (log-sum-exp statistics) 1/l is 1.
         if (t0 >= s0 + 15 && t0 + BQ <= a.T) {  // wave-uniform: every pair of the stage is visible
 #pragma unroll
             for (int u = 0; u < NU; ++u)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    p[u][r] = SIN ? fast_exp2(s[u][r] - stv[u][r].x)
-                                  : fast_exp2(s[u][r] - stv[u][r].x) * stv[u][r].z;
-                    dsv[u][r] = ZT_PLANT == 13 ? p[u][r] : p[u][r] * (dp[u][r] - stv[u][r].y);
+                    p[u][r] = SIN ? fast_exp2(s[u][r] - m2v[u][r]) : fast_exp2(s[u][r] - m2v[u][r]) * ilv[u][r];
+                    dsv[u][r] = ZT_PLANT == 13 ? p[u][r] : p[u][r] * dp[u][r];
                 }
         } else {
 #pragma unroll
@@ -803,12 +812,12 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
                 for (int r = 0; r < 4; ++r) {
                     const int t = t0 + 16 * u + 4 * grp + r;
                     const bool vis = (t < a.T) && (ZT_PLANT == 11 || t >= my_key);
-                    const float e = SIN ? fast_exp2(s[u][r] - stv[u][r].x)
-                                        : fast_exp2(s[u][r] - stv[u][r].x) * stv[u][r].z;
+                    const float e = SIN ? fast_exp2(s[u][r] - m2v[u][r]) : fast_exp2(s[u][r] - m2v[u][r]) * ilv[u][r];
                     p[u][r] = vis ? e : 0.f;
-                    dsv[u][r] = ZT_PLANT == 13 ? p[u][r] : p[u][r] * (dp[u][r] - stv[u][r].y);
+                    dsv[u][r] = ZT_PLANT == 13 ? p[u][r] : p[u][r] * dp[u][r];
                 }
         }
+        if constexpr (PF) fetch_scores(nx);  // this stage's scores are used: the next stage's go out
         // dS for a dq product outside this kernel, one 16 x 16 tile per (u) in lane
         // order; nontemporal, so the 1 GB stream does not evict the Q/dO rows
         // the other workgroups are about to reread.
@@ -818,7 +827,9 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
                 // wave-uniform: a sub-tile past the last row or above the diagonal has no slot
                 if (t0 + 16 * u >= a.T || t0 + 16 * u + 15 < s0) continue;
                 const size_t tile = cur.sblk + zt_tri_index((t0 >> 4) + u, s0 >> 4);
-                __builtin_nontemporal_store(dsv[u], reinterpret_cast<f4 *>(a.ds_out + tile * 256) + lane);
+                // Scalar tile base plus the lane's 32-bit byte offset.
+                __builtin_nontemporal_store(
+                    dsv[u], reinterpret_cast<f4 *>(reinterpret_cast<char *>(a.ds_out + tile * 256) + lane * 16u));
             }
         }
     };
@@ -886,11 +897,12 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
                     const size_t o = ((size_t)b * a.T + t) * a.H + hh;
                     m2 = (a.lse ? a.lse[o] : a.row_max[o]) * kLog2e;
                     il = a.lse ? 1.f : 1.f / a.row_den[o];
-                    de = a.row_del[o];
+                    de = -a.row_del[o];
                 }
-                St[(part * BQ + r) * 4 + 0] = m2;
-                St[(part * BQ + r) * 4 + 1] = de;
-                St[(part * BQ + r) * 4 + 2] = il;
+                // Per part: m2, -delta and 1/l, each BQ rows long.
+                St[part * 4 * BQ + r] = m2;
+                St[part * 4 * BQ + BQ + r] = de;
+                St[part * 4 * BQ + 2 * BQ + r] = il;
             }
             __syncthreads();
         }
