@@ -835,11 +835,14 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
     };
 
     // The second half: dV^T += dO^T P and dK^T += Q^T dS from the stage's rows.
-    auto back = [&](int stg, const StageAt cur, const f4 (&p)[NU], const f4 (&dsv)[NU]) {
+    // mid: the scalar bookkeeping of the stage after next, placed among the
+    // products (at the loop's head it ran beside no MFMA).
+    auto back = [&](int stg, const StageAt cur, const f4 (&p)[NU], const f4 (&dsv)[NU], auto &&mid) {
         const int t0 = cur.t0;
         const float *qs = Qs + stage_off(stg) + hs * BQ * LW, *ds = Ds + stage_off(stg) + hs * BQ * LW;
 #pragma unroll
         for (int u = 0; u < NU; ++u) {
+            if (u == 1) mid();
             if (t0 + 16 * u + 15 < s0) continue;  // wave-uniform: this sub-tile is wholly masked
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk) {
@@ -857,27 +860,36 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
     };
 
     // One whole stage: the first half, then the second.
-    auto work = [&](int stg, const StageAt cur, const StageAt nx) {
+    auto work = [&](int stg, const StageAt cur, const StageAt nx, auto &&mid) {
         if (!visible(cur)) {
             if constexpr (PF) fetch(nx);
             if constexpr (DS > 1) __syncthreads();  // the partial-dP exchange's barrier, met by every wave
+            mid();
             return;
         }
         f4 p[NU], dsv[NU];
         front(stg, cur, nx, p, dsv);
-        back(stg, cur, p, dsv);
+        back(stg, cur, p, dsv, mid);
+        if constexpr (NU < 2) mid();
     };
 
     if constexpr (PF) {
         put(0);
         __syncthreads();
     }
-    int shi = 0, sri = 0;  // the next stage's head and row tile
-    StageAt cur = stage_at(0, 0);
+    int shi = 0, sri = 0;  // the head and row tile of the stage after the current one
+    if (n_stage > 1 && ++shi == hpp) { shi = 0; ++sri; }
+    StageAt cur = stage_at(0, 0), nx = n_stage > 1 ? stage_at(shi, sri) : cur;
     for (int stg = 0; stg < n_stage; ++stg) {
-        // The last stage fetches its own rows again, unused.
-        if (stg + 1 < n_stage && ++shi == hpp) { shi = 0; ++sri; }
-        const StageAt nx = stg + 1 < n_stage ? stage_at(shi, sri) : cur;
+        // The stage after nx, formed while this stage computes (the last stages
+        // fetch their own rows again, unused).
+        StageAt nn = nx;
+        auto mid = [&]() {
+            if (stg + 2 < n_stage) {
+                if (++shi == hpp) { shi = 0; ++sri; }
+                nn = stage_at(shi, sri);
+            }
+        };
         if constexpr (!PF) {
             __syncthreads();
             const int hi = cur.hi, t0 = cur.t0;
@@ -906,8 +918,9 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
             }
             __syncthreads();
         }
-        work(stg, cur, nx);
+        work(stg, cur, nx, mid);
         cur = nx;
+        nx = nn;
         if constexpr (PF) {
             if (stg + 1 < n_stage) put(((stg + 1) & 1) * STAGE_F);
             __syncthreads();
