@@ -1006,12 +1006,19 @@ __device__ __forceinline__ void bwd_dkdv_dma_tile(const BwdArgs &a, const int kt
     const int n_t = (a.T - wg_s0 + BQ - 1) / BQ;  // 16-row tiles of the suffix
     const int n_rt = RS ? (n_t + HS - 1) / HS : n_t;  // row-tile groups per head (RS: one tile per part)
     const int n_stage = hpp * n_rt;                // times the heads of a part
-    // Part `part` of stage `st`: its head, first row, and whether it has rows
-    // (RS: the last group can leave a part without a tile; its copies and
-    // statistics then repeat the last tile and it computes nothing).
+    // Part `part` of a stage (head hi of the part, row group rj): its head,
+    // first row, and whether it has rows (RS: the last group can leave a part
+    // without a tile; its copies and statistics then repeat the last tile and
+    // it computes nothing).  The stage loop steps (hi, rj) along, with no
+    // division per stage.
     struct PartRows { int hh, t0; bool ok; };
-    auto part_rows = [&](int st, int part) {
-        const int hi = st / n_rt, rj = st % n_rt;
+    struct StagePos { int hi, rj; };
+    auto step = [&](StagePos x) {
+        if (++x.rj == n_rt) { x.rj = 0; ++x.hi; }
+        return x;
+    };
+    auto part_rows = [&](StagePos x, int part) {
+        const int hi = x.hi, rj = x.rj;
         if constexpr (RS) {
             const int ri = rj * HS + part;
             return PartRows{kvh * group + hi, wg_s0 + min(ri, n_t - 1) * BQ, ri < n_t};
@@ -1024,7 +1031,19 @@ __device__ __forceinline__ void bwd_dkdv_dma_tile(const BwdArgs &a, const int kt
     // registers and are written to LDS by put_stats after the current compute.
     float sm2 = 0.f, sil = 0.f, sde = 0.f;
     f4 sn = zero4(), sc = zero4();  // this wave's score tile of the next / this stage (SIN)
-    auto issue = [&](int st, int buf) {
+    // A lane's byte offsets for its dma16 copies (j-th copy of this wave:
+    // tile row r_j, swizzled chunk c_j), fixed for the kernel; a copy reads
+    // row min(t0 + r_j, T - 1), i.e. the row offset clamped by one min.
+    constexpr int NPW = HS * 2 * NI / NW;  // copies per wave per stage
+    static_assert(HS * 2 * NI % NW == 0, "whole copies per wave");
+    unsigned crow[NPW], ccol[NPW];
+#pragma unroll
+    for (int j = 0; j < NPW; ++j) {
+        const int ii = (w + j * NW) % NI, e = ii * 64 + lane, r = e / CPR;
+        crow[j] = (unsigned)(r * (int)qld) * 4u;
+        ccol[j] = (unsigned)swz<CPR>(e % CPR, r) * 16u;
+    }
+    auto issue = [&](StagePos st, int buf) {
         if constexpr (SIN) {
             const PartRows pr = part_rows(st, hs);
             sn = zero4();
@@ -1045,14 +1064,17 @@ __device__ __forceinline__ void bwd_dkdv_dma_tile(const BwdArgs &a, const int kt
                 sde = a.row_del[o];
             }
         }
-        for (int i = w; i < HS * 2 * NI; i += NW) {
+#pragma unroll
+        for (int j = 0; j < NPW; ++j) {
+            const int i = w + j * NW;  // wave-uniform
             const int part = i / (2 * NI), arr = (i / NI) & 1, ii = i % NI;
             const PartRows pr = part_rows(st, part);
-            const float *src = (arr ? a.dout : a.q) + qbat + (size_t)pr.hh * DP;
-            const int e = ii * 64 + lane;
-            const int r = e / CPR, c = swz<CPR>(e % CPR, r);
-            const int t = min(pr.t0 + r, a.T - 1);  // rows past T: a real row, masked below
-            dma16(src + (size_t)t * qld + 4 * c, smem + buf * STAGE + (part * 2 + arr) * TILE + ii * 256);
+            // Rows past T: a real row (T - 1), masked below.
+            const char *src = reinterpret_cast<const char *>((arr ? a.dout : a.q) + qbat + (size_t)pr.hh * DP +
+                                                             (size_t)pr.t0 * qld);
+            const unsigned last = (unsigned)(min(a.T - 1 - pr.t0, BQ - 1) * (int)qld) * 4u;
+            dma16(reinterpret_cast<const float *>(src + (min(crow[j], last) + ccol[j])),
+                  smem + buf * STAGE + (part * 2 + arr) * TILE + ii * 256);
         }
     };
     auto put_stats = [&](int buf) {
@@ -1064,15 +1086,17 @@ __device__ __forceinline__ void bwd_dkdv_dma_tile(const BwdArgs &a, const int kt
         }
     };
 
-    issue(0, 0);
+    StagePos pos{0, 0};
+    issue(pos, 0);
     put_stats(0);
     wait_dma();
     __syncthreads();
     for (int st = 0; st < n_stage; ++st) {
         const int buf = st & 1;
+        const StagePos nxt = step(pos);
         if constexpr (SIN) sc = sn;
-        if (st + 1 < n_stage) issue(st + 1, buf ^ 1);
-        const PartRows mine = part_rows(st, hs);
+        if (st + 1 < n_stage) issue(nxt, buf ^ 1);
+        const PartRows mine = part_rows(pos, hs);
         const int t0 = mine.t0;
         if (mine.ok && !(t0 + 15 < s0 || s0 >= a.T)) {
             const float *qs = smem + buf * STAGE + (hs * 2 + 0) * TILE;
@@ -1162,6 +1186,7 @@ __device__ __forceinline__ void bwd_dkdv_dma_tile(const BwdArgs &a, const int kt
         if (st + 1 < n_stage) put_stats(buf ^ 1);
         wait_dma();
         __syncthreads();
+        pos = nxt;
     }
 
     if constexpr (HS > 1) {
