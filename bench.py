@@ -36,6 +36,26 @@ PEAK_HBM = 8000.0       # GB/s, MI355X HBM3E
 THETA = 500000.0
 SEEDS = {"q": 0x5EED0001, "k": 0x5EED0002, "v": 0x5EED0003, "do": 0x5EED0004, "kc": 0x5EED0005,
          "vc": 0x5EED0006, "x": 0x5EED0007, "w": 0x5EED0008}
+# The reference's own attention benchmark shapes (src/cuda/attn_twin.zig:82-111: tag, T, query heads,
+# kv heads, head_dim; B = 1) and what it published for them on its RTX 3080 Ti (src/cuda/README.md:
+# 516-539: forward kernel_us, backward bwd_us).  Context for the same-shape rows, not a target.
+REF_ATTN_SHAPES = [
+    ("ctx256", 256, 4, 2, 32, 104.690, 588.80), ("ctx512", 512, 4, 2, 32, 336.031, 1474.56),
+    ("ctx1024", 1024, 4, 2, 32, 1160.164, 4727.10), ("ctx2048", 2048, 4, 2, 32, 4576.780, 17725.34),
+    ("ctx4096", 4096, 4, 2, 32, 18374.339, 70319.87), ("llama3-T256", 256, 32, 8, 128, 3155.822, 31140.86),
+    ("llama3-T512", 512, 32, 8, 128, 11803.331, 115709.92), ("gqa-96-T256", 256, 32, 8, 96, 2468.086, 18982.82),
+    ("gqa-96-T512", 512, 32, 8, 96, 9295.332, 69966.66), ("mha-192-T256", 256, 16, 16, 192, 2411.664, 30832.64),
+    ("gqa-256-T256", 256, 8, 4, 256, 1656.361, 28313.25),
+]
+# The reference's RMSNorm shapes and its published gpu / gpu_sync / gpu_e2e microseconds per call
+# (src/cuda/README.md:255-266, same card), timed here the same three ways (src/cuda/norm.cu:486-571).
+REF_NORM_SHAPES = [
+    ("micro", 32, 32, 3.68, 7.51, 16.49), ("small", 32, 128, 3.16, 6.91, 18.95),
+    ("mid", 128, 128, 4.53, 8.33, 32.95), ("ship", 256, 128, 7.31, 11.06, 50.45),
+    ("tall", 4096, 128, 76.56, 80.35, 541.32), ("r1024c512", 1024, 512, 21.49, 25.31, 498.58),
+    ("r256c2048", 256, 2048, 8.60, 12.43, 478.94), ("r1024c2048", 1024, 2048, 28.79, 32.56, 1769.64),
+    ("big", 4096, 4096, 232.11, 235.96, 19672.66),
+]
 
 
 def _load(name, rel):
@@ -64,6 +84,285 @@ def _event_time_once(torch, fn, n):
     e.record()
     e.synchronize()
     return s.elapsed_time(e) / n
+
+
+def event_time_after(torch, pre, fn, n, reps=3):
+    """Average ms of fn alone over n calls, each preceded by pre() on the same
+    stream (events around fn only): for a stage that consumes what pre leaves,
+    such as the dk/dv stage reading the scores a forward stored.  Minimum of
+    `reps` measurements."""
+    best = None
+    for _ in range(reps):
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+        for s, e in ev:
+            pre()
+            s.record()
+            fn()
+            e.record()
+        torch.cuda.synchronize()
+        t = sum(s.elapsed_time(e) for s, e in ev) / n
+        best = t if best is None else min(best, t)
+    return best
+
+
+def _hip():
+    """The HIP runtime, for the synchronous copies and device synchronisations
+    the reference's end-to-end timings are made of (cudaMemcpy /
+    cudaDeviceSynchronize, src/cuda/norm.cu:556-571): the copy of the runtime
+    already in the process (by soname; torch and libzt_attn share it), never a
+    second one loaded by path."""
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    hip.hipMemcpy.restype = ctypes.c_int
+    hip.hipDeviceSynchronize.restype = ctypes.c_int
+    return hip
+
+
+def wall_us(fn, n, reps=3):
+    """Host wall-clock microseconds per call of a synchronous fn (min of reps)."""
+    best = None
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        for _ in range(n):
+            fn()
+        t = (time.perf_counter() - t0) * 1e6 / n
+        best = t if best is None else min(best, t)
+    return best
+
+
+def norm_views(torch, zt, dev):
+    """RMSNorm at the reference's shapes, three ways as src/cuda/norm.cu:486-571
+    times it: kernel_us (launches back to back, one synchronise), sync_us
+    (launch and synchronise on every call) and e2e_us (host-to-device copy of
+    x, kernel, device-to-host copy of y, on every call, pageable host memory),
+    beside the reference's published figures for the same shapes."""
+    import numpy as np
+    hip = _hip()
+    fn = zt.lib().zt_rmsnorm_forward
+    sp = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    rows_out = []
+    for tag, rows, cols, r_gpu, r_sync, r_e2e in REF_NORM_SHAPES:
+        x = torch.empty(rows * cols, device=dev)
+        zt.fill_normal(x, SEEDS["x"], 0.0, 1.0)
+        w = torch.empty(cols, device=dev)
+        zt.fill_uniform(w, SEEDS["w"], 0.5, 1.5)
+        y = torch.empty_like(x)
+        hx = x.cpu().numpy()
+        hy = np.empty_like(hx)
+        nb = rows * cols * 4
+        px, pw, py = (ctypes.c_void_p(t.data_ptr()) for t in (x, w, y))
+
+        def launch():
+            if fn(px, pw, py, rows, cols, 1e-5, sp):
+                raise RuntimeError("zt_rmsnorm_forward refused")
+
+        def synced():
+            launch()
+            if hip.hipDeviceSynchronize():
+                raise RuntimeError("hipDeviceSynchronize failed")
+
+        def e2e():
+            if hip.hipMemcpy(px, hx.ctypes.data, nb, 1):
+                raise RuntimeError("hipMemcpy H2D failed")
+            launch()
+            if hip.hipMemcpy(hy.ctypes.data, py, nb, 2):
+                raise RuntimeError("hipMemcpy D2H failed")
+
+        iters = 200 if nb <= (1 << 20) else 40
+        launch()
+        torch.cuda.synchronize()
+        k_us = event_time(torch, launch, iters) * 1e3
+        s_us = wall_us(synced, iters)
+        e_us = wall_us(e2e, max(5, iters // 4))
+        rows_out.append({"shape": tag, "rows": rows, "cols": cols, "kernel_us": round(k_us, 2),
+                         "sync_us": round(s_us, 2), "e2e_us": round(e_us, 2),
+                         "reference_rtx3080ti": {"kernel_us": r_gpu, "sync_us": r_sync, "e2e_us": r_e2e}})
+        log(f"RMSNorm {tag} {rows}x{cols}: kernel {k_us:.2f} us, sync {s_us:.2f} us, e2e {e_us:.2f} us "
+            f"(reference, its card: {r_gpu} / {r_sync} / {r_e2e})")
+        del x, w, y
+    return rows_out
+
+
+def reference_shape_rows(torch, zt, dev):
+    """The reference's attention benchmark shapes (B = 1) through its own two
+    entry points, as its harness times them (launches back to back; min of 3):
+    zt_attn_forward and zt_attn_backward, and beside them the training pair
+    (zt_attn_forward_train_ws + zt_attn_backward_train_ws with the forward's
+    scores)."""
+    L = zt.lib()
+    sp = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    out_rows = []
+    for tag, T, H, Hkv, D, r_fwd, r_bwd in REF_ATTN_SHAPES:
+        q, do = (torch.empty(T * H * D, device=dev) for _ in range(2))
+        k, v = (torch.empty(T * Hkv * D, device=dev) for _ in range(2))
+        for t, sd in ((q, "q"), (k, "k"), (v, "v"), (do, "do")):
+            zt.fill_normal(t, SEEDS[sd], 0.0, 1.0)
+        out, dq = torch.empty_like(q), torch.empty_like(q)
+        dk, dv = torch.empty_like(k), torch.empty_like(v)
+        rm, rl, rd, lse = (torch.empty(T * H, device=dev) for _ in range(4))
+        work = torch.empty(zt.backward_train_workspace_bytes(1, T, H, Hkv, D) // 4, device=dev)
+        P = lambda t: ctypes.c_void_p(t.data_ptr())
+        fargs = (P(q), P(k), P(v), P(out), T, H, Hkv, D, 1, 64, 0, T, sp)
+        bargs = (P(q), P(k), P(v), P(do), P(dq), P(dk), P(dv), P(rm), P(rl), P(rd), T, H, Hkv, D, 64, sp)
+
+        def fwd():
+            if L.zt_attn_forward(*fargs):
+                raise RuntimeError("zt_attn_forward refused")
+
+        def bwd():
+            if L.zt_attn_backward(*bargs):
+                raise RuntimeError("zt_attn_backward refused")
+
+        def train():
+            zt.forward_train_ws(q, k, v, out, lse, work, T, H, Hkv, D)
+            zt.backward_train_ws(q, k, v, out, do, lse, dq, dk, dv, work, T, H, Hkv, D, stage=3 | zt.ZT_WS_SCORES)
+
+        n = 50 if T <= 512 else 20
+        fwd()
+        bwd()
+        train()
+        torch.cuda.synchronize()
+        t_f = event_time(torch, fwd, n) * 1e3
+        t_b = event_time(torch, bwd, n) * 1e3
+        t_t = event_time(torch, train, n) * 1e3
+        fl = 2.0 * H * D * T * (T + 1)      # one causal T x T x d matmul
+        out_rows.append({"shape": tag, "T": T, "n_heads": H, "n_kv_heads": Hkv, "head_dim": D,
+                         "fwd_us": round(t_f, 2), "bwd_us": round(t_b, 2), "train_step_us": round(t_t, 2),
+                         "fwd_TFLOP/s": round(2 * fl / (t_f * 1e-6) / 1e12, 2),
+                         "reference_rtx3080ti": {"fwd_us": r_fwd, "bwd_us": r_bwd}})
+        log(f"{tag}: zt_attn_forward {t_f:.1f} us, zt_attn_backward {t_b:.1f} us, training pair {t_t:.1f} us "
+            f"(reference, its card: {r_fwd} / {r_bwd} us)")
+        del q, k, v, do, out, dq, dk, dv, rm, rl, rd, lse, work
+    return out_rows
+
+
+def seam_e2e(torch, zt, dev, T, H, Hkv, D, reps):
+    """The drop-in seams as the patched reference issues them through the
+    holder (device.Attn), host buffers in and out:
+      forward  = model.cudaForward (src/model.zig:467-516): upload q, k, v;
+                 forward(1, 64); download out;
+      backward = autograd's deviceAttentionBackward (integration patch):
+                 upload q, k, v, dout; forward(1, 64); backward(64); download
+                 dq, dk, dv;
+    each synchronous end to end (pageable host memory, as Zig's slices are),
+    beside the same calls on device-resident buffers (no copies)."""
+    import numpy as np
+    L = zt.lib()
+    hp = ctypes.c_void_p()
+    if L.zt_holder_init(T, H, Hkv, D, ctypes.byref(hp)) != 0:
+        raise RuntimeError("zt_holder_init refused")
+    try:
+        host = {}
+        for which, n, seed in ((zt.ZT_BUF_Q, T * H * D, SEEDS["q"]), (zt.ZT_BUF_K, T * Hkv * D, SEEDS["k"]),
+                               (zt.ZT_BUF_V, T * Hkv * D, SEEDS["v"]), (zt.ZT_BUF_DOUT, T * H * D, SEEDS["do"])):
+            t = torch.empty(n, device=dev)
+            zt.fill_normal(t, seed, 0.0, 1.0)
+            host[which] = t.cpu().numpy()
+            del t
+        outs = {w: np.empty(T * (H if w in (zt.ZT_BUF_OUT, zt.ZT_BUF_DQ) else Hkv) * D, np.float32)
+                for w in (zt.ZT_BUF_OUT, zt.ZT_BUF_DQ, zt.ZT_BUF_DK, zt.ZT_BUF_DV)}
+
+        def up(*ws):
+            for w in ws:
+                a = host[w]
+                if L.zt_holder_upload(hp, w, ctypes.c_void_p(a.ctypes.data), a.size):
+                    raise RuntimeError("zt_holder_upload refused")
+
+        def down(*ws):
+            for w in ws:
+                a = outs[w]
+                if L.zt_holder_download(hp, ctypes.c_void_p(a.ctypes.data), w, a.size):
+                    raise RuntimeError("zt_holder_download refused")
+
+        def fwd_dev():
+            if L.zt_holder_forward(hp, 1, 64):
+                raise RuntimeError("zt_holder_forward refused")
+
+        def bwd_dev():
+            fwd_dev()
+            if L.zt_holder_backward(hp, 64):
+                raise RuntimeError("zt_holder_backward refused")
+
+        def fwd_e2e():
+            up(zt.ZT_BUF_Q, zt.ZT_BUF_K, zt.ZT_BUF_V)
+            fwd_dev()
+            down(zt.ZT_BUF_OUT)
+
+        def bwd_e2e():
+            up(zt.ZT_BUF_Q, zt.ZT_BUF_K, zt.ZT_BUF_V, zt.ZT_BUF_DOUT)
+            bwd_dev()
+            down(zt.ZT_BUF_DQ, zt.ZT_BUF_DK, zt.ZT_BUF_DV)
+
+        up(zt.ZT_BUF_Q, zt.ZT_BUF_K, zt.ZT_BUF_V, zt.ZT_BUF_DOUT)
+        for _ in range(2):
+            bwd_e2e()
+            fwd_e2e()
+        res = {"forward_e2e_us": wall_us(fwd_e2e, reps), "backward_e2e_us": wall_us(bwd_e2e, reps),
+               "forward_device_us": event_time(torch, fwd_dev, reps) * 1e3,
+               "forward_backward_device_us": event_time(torch, bwd_dev, reps) * 1e3}
+        res = {k2: round(v2, 2) for k2, v2 in res.items()}
+        res["bytes_up_down"] = {"forward": 4 * T * (2 * H + 2 * Hkv) * D,
+                                "backward": 4 * T * (2 * H + 2 * Hkv) * D + 4 * T * (H + 2 * Hkv) * D}
+        return res
+    finally:
+        L.zt_holder_deinit(hp)
+
+
+def decode_seam_holder(torch, zt, dev, n_ctx, H, Hkv, D, n_holders, calls):
+    """decode.zig:462's forwardAt(1, 64, n_keys - 1, n_keys, 1) through the
+    holder, which splits the keys over the device: on device-resident caches
+    (n_holders sequences, cycled so the caches exceed the 256 MB MALL) in
+    microseconds per call, and end to end as src/decode.zig:405-473 issues it
+    (upload the query row and the n_keys cache rows of K and V, forwardAt,
+    download the output row)."""
+    import numpy as np
+    L = zt.lib()
+    hs = []
+    try:
+        for _ in range(n_holders):
+            hp = ctypes.c_void_p()
+            if L.zt_holder_init(n_ctx, H, Hkv, D, ctypes.byref(hp)) != 0:
+                raise RuntimeError("zt_holder_init refused")
+            hs.append(hp)
+        for i, hp in enumerate(hs):
+            for which, n, seed in ((zt.ZT_BUF_Q, H * D, SEEDS["q"]), (zt.ZT_BUF_K, n_ctx * Hkv * D, SEEDS["kc"]),
+                                   (zt.ZT_BUF_V, n_ctx * Hkv * D, SEEDS["vc"])):
+                if L.zt_fill_normal(L.zt_holder_buffer(hp, which), n, seed + 64 * i, 0.0, 1.0, None):
+                    raise RuntimeError("zt_fill_normal refused")
+        it = [0]
+
+        def call():
+            hp = hs[it[0] % n_holders]
+            it[0] += 1
+            if L.zt_holder_forward_at(hp, 1, 64, n_ctx - 1, n_ctx, 1):
+                raise RuntimeError("zt_holder_forward_at refused")
+
+        for _ in range(2 * n_holders):
+            call()
+        t_call = event_time(torch, call, calls) * 1e3
+        hq = np.empty(H * D, np.float32)
+        hk = np.empty(n_ctx * Hkv * D, np.float32)
+        hv = np.empty_like(hk)
+        ho = np.empty(H * D, np.float32)
+        hp = hs[0]
+        for a, w in ((hq, zt.ZT_BUF_Q), (hk, zt.ZT_BUF_K), (hv, zt.ZT_BUF_V)):
+            L.zt_holder_download(hp, ctypes.c_void_p(a.ctypes.data), w, a.size)
+
+        def e2e():
+            for a, w in ((hq, zt.ZT_BUF_Q), (hk, zt.ZT_BUF_K), (hv, zt.ZT_BUF_V)):
+                if L.zt_holder_upload(hp, w, ctypes.c_void_p(a.ctypes.data), a.size):
+                    raise RuntimeError("zt_holder_upload refused")
+            if L.zt_holder_forward_at(hp, 1, 64, n_ctx - 1, n_ctx, 1):
+                raise RuntimeError("zt_holder_forward_at refused")
+            if L.zt_holder_download(hp, ctypes.c_void_p(ho.ctypes.data), zt.ZT_BUF_OUT, ho.size):
+                raise RuntimeError("zt_holder_download refused")
+
+        e2e()
+        t_e2e = wall_us(e2e, 5)
+        return t_call, t_e2e
+    finally:
+        for hp in hs:
+            L.zt_holder_deinit(hp)
 
 
 def main():
@@ -134,33 +433,35 @@ def main():
     paths = {
         "train": dict(
             fwd=lambda: zt.forward_train_ws(q, k, v, out, lse, work, T, H, Hkv, D),
-            # Repeated on its own, the dk/dv stage reads the dS its previous
-            # launch left in place of the scores; its work does not depend on the values.
+            # The dk/dv stage consumes the scores the forward stored (a second
+            # ZT_WS_SCORES stage without a forward between is refused), so it is
+            # timed after a forward each time, with events around the stage only.
             dkdv=lambda: zt.backward_train_ws(q, k, v, out, do, lse, dq, dk, dv, work, T, H, Hkv, D,
                                               stage=1 | zt.ZT_WS_SCORES),
+            dkdv_after_fwd=True,
             dq=lambda: zt.backward_train_ws(q, k, v, out, do, lse, dq, dk, dv, work, T, H, Hkv, D, stage=2),
             bwd=lambda: zt.backward_train_ws(q, k, v, out, do, lse, dq, dk, dv, work, T, H, Hkv, D, stage=scores),
-            names=zt.plan_train(B, T, H, Hkv, D), dkdv_units=3),
+            names=zt.plan_train(B, T, H, Hkv, D), dkdv_units=3, dq_exec_units=1),
         "train_recompute_scores": dict(
             fwd=lambda: zt.forward_train(q, k, v, out, lse, T, H, Hkv, D),
             dkdv=lambda: zt.backward_train_ws(q, k, v, out, do, lse, dq, dk, dv, work, T, H, Hkv, D, stage=1),
             dq=lambda: zt.backward_train_ws(q, k, v, out, do, lse, dq, dk, dv, work, T, H, Hkv, D, stage=2),
             bwd=lambda: zt.backward_train_ws(q, k, v, out, do, lse, dq, dk, dv, work, T, H, Hkv, D),
             names=(zt.plan(B, T, H, Hkv, D)[0], zt.plan_train(B, T, H, Hkv, D)[1], zt.plan(B, T, H, Hkv, D)[2]),
-            dkdv_units=4),
+            dkdv_units=4, dq_exec_units=1),
         "train_dq_kernel": dict(
             fwd=lambda: zt.forward_train(q, k, v, out, lse, T, H, Hkv, D),
             dq=lambda: zt.bwd_dq_train(q, k, v, out, do, lse, dq, delta, T, H, Hkv, D),
             dkdv=lambda: zt.bwd_dkdv_train(q, k, v, out, do, lse, delta, dk, dv, T, H, Hkv, D),
             bwd=lambda: zt.backward_train(q, k, v, out, do, lse, dq, dk, dv, delta, T, H, Hkv, D),
             names=(zt.plan(B, T, H, Hkv, D)[0], "zt_bwd_dql_d%d_k32" % D, zt.plan(B, T, H, Hkv, D)[2]),
-            dkdv_units=4),
+            dkdv_units=4, dq_exec_units=3),
         "reference_abi": dict(
             fwd=lambda: zt.forward(q, k, v, out, T, H, Hkv, D),
             dq=lambda: zt.bwd_dq(q, k, v, do, dq, rm, rl, rd, T, H, Hkv, D),
             dkdv=lambda: zt.bwd_dkdv(q, k, v, do, dk, dv, rm, rl, rd, T, H, Hkv, D),
             bwd=lambda: zt.backward(q, k, v, do, dq, dk, dv, rm, rl, rd, T, H, Hkv, D),
-            names=zt.plan(B, T, H, Hkv, D), dkdv_units=4),
+            names=zt.plan(B, T, H, Hkv, D), dkdv_units=4, dq_exec_units=4),
     }
     res = {}
     for pname, pth in paths.items():
@@ -186,8 +487,12 @@ def main():
 
         n_k = max(3, args.steps)
         t_fwd = event_time(torch, pth["fwd"], n_k)
-        pth["dkdv"]()  # the dq stage reads what the dk/dv stage wrote (row statistics or dS)
-        t_dkdv = event_time(torch, pth["dkdv"], n_k)
+        if pth.get("dkdv_after_fwd"):
+            t_dkdv = event_time_after(torch, pth["fwd"], pth["dkdv"], n_k)
+        else:
+            pth["dkdv"]()
+            t_dkdv = event_time(torch, pth["dkdv"], n_k)
+        # the dq stage reads what the dk/dv stage last wrote (row statistics or dS)
         t_dq = event_time(torch, pth["dq"], n_k)
         # Algorithmic FLOPs per launch: the forward's two matmuls; of the
         # backward's five (S recompute, dP, dV, dK, dQ) the dk/dv kernel owns
@@ -206,10 +511,15 @@ def main():
                 f"of FP32 MFMA peak)")
         fwd_tflops = fwd_flop / (t_fwd * 1e-3) / 1e12
         bwd_tflops = bwd_flop / ((t_dq + t_dkdv) * 1e-3) / 1e12
-        log(f"  forward {fwd_tflops:.2f} TFLOP/s ({100 * fwd_tflops / PEAK_MFMA_F32:.1f}%), backward "
-            f"{bwd_tflops:.2f} TFLOP/s ({100 * bwd_tflops / PEAK_MFMA_F32:.1f}%)")
+        # What the backward's kernels execute (dk/dv's matmuls plus the dq
+        # kernel's own, recomputes included): the utilisation figure.  The FA2
+        # count above credits 5 units whatever runs, so it is no fraction of peak.
+        bwd_exec = (pth["dkdv_units"] + pth["dq_exec_units"]) * unit / ((t_dq + t_dkdv) * 1e-3) / 1e12
+        log(f"  forward {fwd_tflops:.2f} TFLOP/s ({100 * fwd_tflops / PEAK_MFMA_F32:.1f}% of FP32 MFMA peak); "
+            f"backward {bwd_tflops:.2f} TFLOP/s by the FA2 count, {bwd_exec:.2f} TFLOP/s executed "
+            f"({100 * bwd_exec / PEAK_MFMA_F32:.1f}% of peak)")
         res[pname] = dict(ms_step=ms_step, value=val, kernels=kernels, fwd_tflops=fwd_tflops,
-                          bwd_tflops=bwd_tflops)
+                          bwd_tflops=bwd_tflops, bwd_exec_tflops=bwd_exec)
     # The drop-in holder (include/zt_holder.h, device.zig's Attn) on device-resident
     # buffers: zt_holder_forward + zt_holder_backward as device.Attn.forward(1, 64) +
     # backward(64) issue them, on the same C3 inputs (copied into the holder's buffers).
@@ -341,6 +651,12 @@ def main():
     log(f"C4 reference decode seam (zt_attn_forward, T=1, one call per sequence): {t_seam * 1e3:.1f} us, "
         f"{seam_gbs:.0f} GB/s")
     del kc, vc, qd, od, ws, kn, vn, ws2
+    # The same seam through the holder (device.Attn.forwardAt, which splits the keys).
+    t_hcall, t_he2e = decode_seam_holder(torch, zt, dev, n_ctx, H, Hkv, D, n_holders=8, calls=64)
+    call_bytes = dec_bytes / Bd
+    log(f"C4 decode seam through the holder: {t_hcall:.1f} us per call ({call_bytes / (t_hcall * 1e-6) / 1e9:.0f} "
+        f"GB/s), {Bd * t_hcall:.1f} us per 64-sequence step; end to end with the cache upload {t_he2e:.0f} us "
+        f"per call")
 
     # ---------------- dense products (tensor.matmul and its gradients) ----------------
     mm = {}
@@ -431,6 +747,14 @@ def main():
     log(f"device copy 1 GiB: {t_cp * 1e3:.0f} us, {copy_gbs:.0f} GB/s")
     del src, dst
 
+    # ---------------- The reference's own views: same shapes, sync and end-to-end ----------------
+    norm_sync_e2e = norm_views(torch, zt, dev)
+    ref_shapes = reference_shape_rows(torch, zt, dev)
+    seams = {"GPT-mini T=256 Hq=4 Hkv=2 d=32": seam_e2e(torch, zt, dev, 256, 4, 2, 32, 50),
+             "C3 T=4096 Hq=32 Hkv=8 d=128": seam_e2e(torch, zt, dev, 4096, 32, 8, 128, 5)}
+    for tag, r in seams.items():
+        log(f"seams {tag}: {r}")
+
     # ---------------- CPU baseline: the restatement on a bounded sample ----------------
     cpu = None
     if not args.no_cpu:
@@ -485,6 +809,8 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "fwd_tflops": round(fwd_tflops, 3), "bwd_tflops": round(bwd_tflops, 3),
+        "bwd_executed_tflops": round(res["train"]["bwd_exec_tflops"], 3),
+        "bwd_executed_frac": round(res["train"]["bwd_exec_tflops"] / PEAK_MFMA_F32, 4),
         "step_path": "zt_attn_forward_train_ws + zt_attn_backward_train_ws with ZT_WS_SCORES (saved log-sum-exp "
                      "and scores; the dk/dv kernel reads the scores and stores dS in their place; dq = dS k)",
         "executed_tflops": round(exec_flop / (ms_step * 1e-3) / 1e12, 3),
@@ -513,8 +839,19 @@ def main():
                    "step_us": round(t_step * 1e3, 2), "step_GB/s": round(step_gbs, 1),
                    "reference_seam": {"path": "zt_attn_forward(T=1, q_offset=n_keys-1, n_keys) once per sequence, "
                                               "as src/decode.zig:462 issues it",
-                                      "us": round(t_seam * 1e3, 2), "GB/s": round(seam_gbs, 1)}},
+                                      "us": round(t_seam * 1e3, 2), "GB/s": round(seam_gbs, 1)},
+                   "holder_seam": {"path": "zt_holder_forward_at(1, 64, n_keys-1, n_keys, 1) on one sequence's "
+                                           "device-resident cache (device.Attn.forwardAt, keys split over the "
+                                           "device), 8 holders cycled",
+                                   "us_per_call": round(t_hcall, 2), "us_per_64_sequences": round(Bd * t_hcall, 1),
+                                   "GB/s": round(call_bytes / (t_hcall * 1e-6) / 1e9, 1),
+                                   "e2e_us_per_call": round(t_he2e, 1),
+                                   "e2e_path": "src/decode.zig:405-473 as issued: upload the query row and 8192 "
+                                               "cache rows of K and V, forwardAt, download the output row"}},
         "rmsnorm": norm,
+        "rmsnorm_reference_shapes": norm_sync_e2e,
+        "reference_shapes": ref_shapes,
+        "seams_e2e": seams,
         "matmul": mm,
         "calibration": {"mfma_f32_tflops": round(cal_tflops, 1), "read_GB/s": round(cal_gbs, 1),
                         "dominant_frac_of_sustained": round(dom["tflops"] / cal_tflops, 4),

@@ -140,7 +140,12 @@ int zt_attn_decode(const float *q, const float *k_cache, const float *v_cache, f
  * wider split forced with ZT_DEC_WGS can exceed it).  No part of the scratch
  * needs to start at zero: the combine reads only partials the same call wrote.
  * Every call on one GPU shares that GPU's scratch, so calls that overlap on
- * one GPU (concurrent streams, threads) race: serialise them. */
+ * one GPU (concurrent streams, threads) race: serialise them.
+ * Set-up: the library's first call of any entry point on a device loads its
+ * code objects there (hipModuleLoadData), looks up the scratch's address and
+ * resolves the decode kernels; that first call is not allocation-free.  Make
+ * one call on each device outside graph capture (any entry point, e.g. a
+ * warm-up zt_attn_decode_noalloc); every later call only launches. */
 int zt_attn_decode_noalloc(const float *q, const float *k_cache, const float *v_cache, float *out,
                            const int *n_keys, int B, int n_ctx, int n_heads, int n_kv_heads, int dim,
                            hipStream_t stream);
@@ -208,11 +213,15 @@ int zt_attn_bwd_dkdv_train(const float *q, const float *k, const float *v, const
  * stage: 1 = delta + dk/dv (+ dS), 2 = dq from dS, 3 = both; | ZT_WS_SCORES
  * when the workspace holds the scores zt_attn_forward_train_ws wrote for these
  * q, k (the dk/dv kernel then reads each score tile and overwrites it with dS
- * instead of forming Q K^T again).  ZT_WS_SCORES is single use: nothing
- * checks what the tiles hold, so it is for the first stage 1 after the
- * zt_attn_forward_train_ws of the same q, k and shape (after stage 1 the
- * tiles hold dS, and a plain zt_attn_forward_train writes none); otherwise
- * dq/dk/dv are wrong and the call still returns 0.  No reference counterpart. */
+ * instead of forming Q K^T again).  ZT_WS_SCORES is single use: it is for
+ * the first stage 1 after the zt_attn_forward_train_ws of the same q, k (the
+ * same pointers) and shape on the same device; after that stage 1 the tiles
+ * hold dS.  The library keeps a host-side record of which workspace holds
+ * whose scores (set by zt_attn_forward_train_ws, consumed by the stage 1 that
+ * reads them, dropped by a stage 1 that overwrites them) and refuses with 1
+ * a ZT_WS_SCORES stage 1 that does not match it, rather than reading stale
+ * tiles.  It cannot see q or k rewritten in place between the two calls;
+ * that leaves out and lse stale as well.  No reference counterpart. */
 #define ZT_WS_SCORES 4
 size_t zt_attn_backward_train_workspace(int B, int T, int n_heads, int n_kv_heads, int dim);
 int zt_attn_backward_train_ws(const float *q, const float *k, const float *v, const float *out, const float *dout,

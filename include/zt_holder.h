@@ -49,25 +49,42 @@ typedef struct zt_holder zt_holder;
 
 /* device.zig:221-299 (Attn.init): refuses via zt_attn_dim_ok and the group
  * check BEFORE allocating; on an allocation failure frees what it took.
- * Beyond the eleven buffers it also tries to allocate the score workspace of
- * the saved-statistics backward (zt_attn_backward_train_workspace bytes for
- * one sequence of t rows: 1.0 GiB at t = 4096 with 32 heads); a failure there
- * is no error, the holder then runs without it (see zt_holder_backward). */
+ * Beyond the eleven buffers the holder takes two workspaces, neither of
+ * which is needed for correctness (a failed allocation is no error):
+ *   - here, the one-row forward's chunk partials (zt_attn_decode_workspace
+ *     bytes for one sequence of t rows: 1.0 MiB at t = 8192 with 32 heads,
+ *     d = 128); without them see zt_holder_forward_at;
+ *   - at the first whole-shape forward (zt_holder_forward), the score
+ *     workspace of the saved-statistics backward
+ *     (zt_attn_backward_train_workspace bytes for one sequence of t rows:
+ *     1.0 GiB at t = 4096 with 32 heads, 4.0 GiB at 8192), only when it is at
+ *     most a quarter of the device's free memory (hipMemGetInfo) then; a
+ *     holder that only decodes never takes it; without it see
+ *     zt_holder_backward.
+ * zt_holder_workspace_bytes reports what is taken, beside
+ * zt_holder_total_bytes's eleven buffers: budget VRAM with the sum. */
 int zt_holder_init(size_t t, size_t n_heads, size_t n_kv_heads, size_t dim, zt_holder **out);
-/* The same holder running the reference pair only (zt_attn_forward then
- * zt_attn_backward, which rebuilds the statistics): no workspace, and
+/* The same holder running the reference entry points only (zt_attn_forward,
+ * also for one query row, then zt_attn_backward, which rebuilds the
+ * statistics): no workspace at all, and
  * row_max / row_den hold the reference's max and denominator.  No reference
  * counterpart (device.zig has one mode). */
 int zt_holder_init_exact(size_t t, size_t n_heads, size_t n_kv_heads, size_t dim, zt_holder **out);
 void zt_holder_deinit(zt_holder *h);                                   /* :328-330 */
 /* :332-341: the eleven buffers' bytes, as the reference counts them (the
- * workspace is not included: zt_holder_workspace_bytes). */
+ * workspaces are not included: zt_holder_workspace_bytes). */
 size_t zt_holder_total_bytes(const zt_holder *h);
+/* Bytes of the optional workspaces the holder holds now (0 for
+ * zt_holder_init_exact).  No reference counterpart. */
 size_t zt_holder_workspace_bytes(const zt_holder *h);
-/* A buffer's device pointer.  Writing q, k, v, out or row_max through it
- * between a forward and a backward is not seen by the holder: upload through
- * zt_holder_upload, run the forward again, or call zt_holder_forget first. */
+/* A buffer's writable device pointer.  Asking for q, k, v, out or row_max
+ * drops the forward's saved state, as an upload does (the caller may now
+ * change what the forward saw), so the next backward rebuilds the statistics;
+ * the other buffers leave it.  To read without that, use zt_holder_buffer_ro. */
 float *zt_holder_buffer(const zt_holder *h, int which);
+/* The same pointer, read-only: keeps the saved state.  No reference
+ * counterpart. */
+const float *zt_holder_buffer_ro(const zt_holder *h, int which);
 /* :376-379.  The whole-cache forward.  It also keeps what the backward would
  * otherwise rebuild (device.zig:400-402 requires the forward to run first on
  * the same buffers): row_max receives each row's log-sum-exp and row_den 1.0,
@@ -76,8 +93,14 @@ float *zt_holder_buffer(const zt_holder *h, int which);
  * zt_attn_forward admits them (an argument it refuses is refused the same way). */
 int zt_holder_forward(const zt_holder *h, int group_q, int max_tile);
 /* :381-398.  forward_at with q_offset 0, n_keys t_cap and t t_cap is
- * zt_holder_forward; any other (decode-shaped) call runs zt_attn_forward and
- * drops the saved state. */
+ * zt_holder_forward; any other (decode-shaped) call drops the saved state and
+ * runs zt_attn_forward, except one query row (t = 1, the reference's decode
+ * seam, src/decode.zig:462) on a holder from zt_holder_init with its chunk
+ * partials: that runs zt_attn_decode over the q_offset + 1 visible cache rows,
+ * keys split into chunks across the device (the one-row zt_attn_forward gives
+ * a single sequence only one workgroup per kv head and head sub-group).  Same
+ * result to rounding; group_q and max_tile are admitted as zt_attn_forward
+ * admits them. */
 int zt_holder_forward_at(const zt_holder *h, int group_q, int max_tile, int q_offset, int n_keys,
                          int t);
 /* :400-406.  dq, dk, dv from the buffers.  After zt_holder_forward with no

@@ -114,9 +114,13 @@ def test_holder_scratch_contract_in_both_modes(gpu, zt, oracle, exact):
     init = zt.lib().zt_holder_init_exact if exact else zt.lib().zt_holder_init
     assert init(T, H, Hkv, D, ctypes.byref(p)) == 0
     try:
-        assert (zt.lib().zt_holder_workspace_bytes(p) == 0) == exact
+        dec_ws = zt.decode_workspace_bytes(1, T, H, Hkv, D)
+        assert zt.lib().zt_holder_workspace_bytes(p) == (0 if exact else dec_ws)
         q, k, v, do = _inputs(zt, p, T, H, Hkv, D)
         assert zt.lib().zt_holder_forward(p, 1, 64) == 0
+        # the first whole-shape forward takes the score workspace
+        assert zt.lib().zt_holder_workspace_bytes(p) == (
+            0 if exact else dec_ws + zt.backward_train_workspace_bytes(1, T, H, Hkv, D))
         assert zt.lib().zt_holder_backward(p, 64) == 0
         m, l, d = oracle.attention_row_stats(q, k, v, do, 1, T, H, Hkv, D)
         rm, rl, rd = (_down(zt, p, w, T * H) for w in (zt.ZT_BUF_ROW_MAX, zt.ZT_BUF_ROW_DEN, zt.ZT_BUF_ROW_DEL))
@@ -175,25 +179,69 @@ def test_holder_backward_follows_what_the_buffers_hold(gpu, zt, oracle):
         L.zt_holder_deinit(p)
 
 
-def test_holder_at_c3_whole_kv_group(gpu, zt, oracle, threads):
-    """The drop-in holder at the headline shape (C3, RoPE'd Q/K): its default
-    forward + backward graded on every row of kv group 7 against the twin."""
-    T, H, Hkv, D, kv = 4096, 32, 8, 128, 7
+def test_holder_buffer_pointer_drops_the_saved_state_and_the_read_only_one_keeps_it(gpu, zt, oracle):
+    """A writable pointer to q (or k, v, out, row_max) may be used to change what
+    the forward saw, so asking for one drops the saved state and the next
+    backward rebuilds the statistics from the buffers as they now are; the
+    read-only accessor leaves it (the saved-statistics backward leaves
+    row_den = 1, the rebuilding one the softmax denominators)."""
+    T, H, Hkv, D = 150, 4, 2, 128
     p = _holder(zt, T, H, Hkv, D)
     L = zt.lib()
     try:
-        q, k, v, do = _inputs(zt, p, T, H, Hkv, D, rope=True)
-        assert L.zt_holder_forward(p, 1, 64) == 0 and L.zt_holder_backward(p, 64) == 0
-        out = _down(zt, p, zt.ZT_BUF_OUT, T * H * D)
-        dq, dk, dv = _grads(zt, p, T, H, Hkv, D)
-        ro = oracle.attention_forward_groups(q, k, v, 1, T, H, Hkv, D, kv, kv + 1, threads=threads)
-        rq, rk, rv = oracle.attention_backward_groups(q, k, v, do, 1, T, H, Hkv, D, kv, kv + 1, threads=threads)
-        g = H // Hkv
-        hq = lambda x: x.reshape(T, H, D)[:, kv * g:(kv + 1) * g]
-        hk = lambda x: x.reshape(T, Hkv, D)[:, kv]
-        assert np.max(np.abs(hq(out) - hq(ro))) <= 1e-4
-        assert _rel(hq(dq), hq(rq)) <= 1e-3
-        assert _rel(hk(dk), hk(rk)) <= 1e-3
-        assert _rel(hk(dv), hk(rv)) <= 1e-3
+        q, k, v, do = _inputs(zt, p, T, H, Hkv, D)
+        assert L.zt_holder_forward(p, 1, 64) == 0
+        inputs = (zt.ZT_BUF_Q, zt.ZT_BUF_K, zt.ZT_BUF_V, zt.ZT_BUF_OUT, zt.ZT_BUF_ROW_MAX)
+        for w in inputs:                              # read-only pointers to the forward's inputs
+            assert L.zt_holder_buffer_ro(p, w)
+        for w in (zt.ZT_BUF_DOUT, zt.ZT_BUF_DQ, zt.ZT_BUF_DK, zt.ZT_BUF_DV, zt.ZT_BUF_ROW_DEN, zt.ZT_BUF_ROW_DEL):
+            assert L.zt_holder_buffer(p, w) == L.zt_holder_buffer_ro(p, w)
+        assert L.zt_holder_backward(p, 64) == 0     # none of those drops the saved state
+        assert np.all(_down(zt, p, zt.ZT_BUF_ROW_DEN, T * H) == 1.0)
+        assert L.zt_holder_forward(p, 1, 64) == 0
+        qp = L.zt_holder_buffer(p, zt.ZT_BUF_Q)     # writable q: the state is dropped
+        assert zt.lib().zt_fill_normal(qp, T * H * D, 0x5EED00AA, 0.0, 1.0, None) == 0
+        q2 = _down(zt, p, zt.ZT_BUF_Q, T * H * D)
+        assert L.zt_holder_backward(p, 64) == 0
+        assert not np.all(_down(zt, p, zt.ZT_BUF_ROW_DEN, T * H) == 1.0)
+        rq, rk, rv = oracle.attention_backward(q2, k, v, do, 1, T, H, Hkv, D)
+        for got, want in zip(_grads(zt, p, T, H, Hkv, D), (rq, rk, rv)):
+            assert _rel(got, want) <= 1e-3
     finally:
         L.zt_holder_deinit(p)
+
+
+def test_holder_decode_seam_at_the_c4_sequence_shape(gpu, zt, oracle, threads):
+    """decode.zig:462's call on one C4 sequence (8192 cached keys, 32 / 8 heads,
+    d = 128) through the holder, which splits the keys over the device with
+    its own chunk partials: against the twin at the full cache and at a
+    partly filled one, and equal to zt_attn_decode bit for bit."""
+    n_ctx, H, Hkv, D = 8192, 32, 8, 128
+    p = _holder(zt, n_ctx, H, Hkv, D)
+    L = zt.lib()
+    try:
+        dec_ws = zt.decode_workspace_bytes(1, n_ctx, H, Hkv, D)
+        assert L.zt_holder_workspace_bytes(p) == dec_ws   # a decode-only holder takes no score workspace
+        _fill(zt, p, zt.ZT_BUF_Q, H * D, 0x5EED0001)
+        _fill(zt, p, zt.ZT_BUF_K, n_ctx * Hkv * D, 0x5EED0005)
+        _fill(zt, p, zt.ZT_BUF_V, n_ctx * Hkv * D, 0x5EED0006)
+        qh = _down(zt, p, zt.ZT_BUF_Q, H * D)
+        kc = _down(zt, p, zt.ZT_BUF_K, n_ctx * Hkv * D)
+        vc = _down(zt, p, zt.ZT_BUF_V, n_ctx * Hkv * D)
+        for n_keys in (n_ctx, 5000, 1):
+            assert L.zt_holder_forward_at(p, 1, 64, n_keys - 1, n_keys, 1) == 0
+            out = _down(zt, p, zt.ZT_BUF_OUT, H * D)
+            ref = oracle.attn_step(qh, kc, vc, [n_keys], 1, n_ctx, H, Hkv, D, threads=threads)
+            assert np.max(np.abs(out - ref)) <= 1e-4, n_keys
+            want = gpu.empty(H * D, device="cuda")
+            ws = gpu.empty(dec_ws // 4 + 1, device="cuda")
+            qd, kd, vd = (gpu.from_numpy(x).cuda() for x in (qh, kc, vc))
+            zt.decode(qd, kd, vd, want, [n_keys], 1, n_ctx, H, Hkv, D, ws)
+            gpu.cuda.synchronize()
+            assert np.array_equal(out.view(np.uint32), host_np(want).view(np.uint32)), n_keys
+    finally:
+        L.zt_holder_deinit(p)
+
+
+def host_np(t):
+    return t.detach().cpu().numpy().ravel()

@@ -251,3 +251,40 @@ def test_train_paired_tiles_and_128_products_at_small_shapes(gpu, zt, oracle, th
     assert rel_err(dv, rv) <= BWD_REL
 
 
+
+
+@pytest.mark.parametrize("B,T,H,Hkv,D", [(1, 333, 8, 2, 128), (1, 90, 8, 2, 256)])
+def test_stale_scores_are_refused_not_read(gpu, zt, oracle, capfd, B, T, H, Hkv, D):
+    """ZT_WS_SCORES is single use and tied to the forward's q, k and shape: a
+    second stage 1 after one forward, a stage 1 for other q or another shape,
+    and one after a stage 1 that overwrote the tiles with dS are each refused
+    (return 1, reason on stderr) instead of reading tiles that do not hold
+    these scores; the call that matches still grades against the twin."""
+    q, k, v, do = _inputs(gpu, zt, B, T, H, Hkv, D)
+    work = _nan(gpu, zt.backward_train_workspace_bytes(B, T, H, Hkv, D) // 4)
+    out, lse = _nan(gpu, q.numel()), _nan(gpu, B * T * H)
+    dq, dk, dv = (_nan(gpu, n) for n in (q.numel(), k.numel(), k.numel()))
+    scores1 = 1 | zt.ZT_WS_SCORES
+
+    def bwd(qq, stage, T_=T):
+        return zt.lib().zt_attn_backward_train_ws(*(zt._ptr(x) for x in (qq, k, v, out, do, lse, dq, dk, dv, work)),
+                                                  work.numel() * 4, B, T_, H, Hkv, D, stage, None)
+
+    zt.forward_train_ws(q, k, v, out, lse, work, T, H, Hkv, D, B=B)
+    q2 = q.clone()
+    capfd.readouterr()
+    assert bwd(q2, scores1) == 1                 # other q: refused, the scores stay usable
+    assert bwd(q, scores1, T_=T - 1) == 1        # another shape: refused
+    assert "ZT_WS_SCORES" in capfd.readouterr().err
+    assert bwd(q, scores1) == 0                  # the matching call consumes them
+    assert bwd(q, 2) == 0
+    gpu.cuda.synchronize()
+    rq, rk, rv = oracle.attention_backward(*(host(x) for x in (q, k, v, do)), B, T, H, Hkv, D)
+    assert max(rel_err(host(dq), rq), rel_err(host(dk), rk), rel_err(host(dv), rv)) <= BWD_REL
+    assert bwd(q, scores1) == 1                  # consumed: the tiles now hold dS
+    zt.forward_train_ws(q, k, v, out, lse, work, T, H, Hkv, D, B=B)
+    assert bwd(q, 1) == 0                        # a stage 1 that forms S again overwrites them
+    assert bwd(q, scores1) == 1
+    zt.forward_train(q, k, v, out, lse, T, H, Hkv, D, B=B)
+    assert bwd(q, scores1) == 1                  # a forward that stores no scores stamps nothing
+    gpu.cuda.synchronize()

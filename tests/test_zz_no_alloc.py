@@ -57,3 +57,58 @@ def test_noalloc_decode_refuses_beyond_its_scratch(gpu, zt, tune, capfd):
     arr = (ctypes.c_int * B)(n_ctx)
     assert L.zt_attn_decode_noalloc(None, None, None, None, arr, B, n_ctx, H, Hkv, D, None) == 1
     assert "beyond the library's fixed" in capfd.readouterr().err
+
+
+def test_noalloc_decode_allocates_nothing_and_replays_from_a_graph(gpu, zt):
+    """After one warm-up call (the library's set-up on the device), a call
+    leaves the device's free memory unchanged, and the call captured into a
+    HIP graph replays to zt_attn_decode's result bit for bit, replay after
+    replay, with eager calls on other inputs (which reuse the same scratch)
+    and synchronisations between the replays."""
+    B, n_ctx, H, Hkv, D = 2, 8192, 32, 8, 128      # keys split into chunks: the partials use the scratch
+    n_keys = [8192, 5000]
+    arr = (ctypes.c_int * B)(*n_keys)
+    L = zt.lib()
+
+    def tensors(off):
+        return (dev_normal(gpu, zt, B * H * D, SEED_Q + off), dev_normal(gpu, zt, B * n_ctx * Hkv * D, SEED_KC + off),
+                dev_normal(gpu, zt, B * n_ctx * Hkv * D, SEED_VC + off))
+
+    def call(q, kc, vc, out, stream):
+        return L.zt_attn_decode_noalloc(ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(kc.data_ptr()),
+                                        ctypes.c_void_p(vc.data_ptr()), ctypes.c_void_p(out.data_ptr()), arr, B,
+                                        n_ctx, H, Hkv, D, ctypes.c_void_p(stream.cuda_stream))
+
+    print(f"[noalloc graph] B={B} n_ctx={n_ctx} H={H}/{Hkv} d={D}", flush=True)
+    q, kc, vc = tensors(0)
+    q2, kc2, vc2 = tensors(32)
+    got = gpu.full((B * H * D,), float("nan"), device="cuda", dtype=gpu.float32)
+    other = gpu.empty_like(got)
+    cur = gpu.cuda.current_stream()
+    assert call(q, kc, vc, got, cur) == 0          # warm-up
+    gpu.cuda.synchronize()
+    free0 = gpu.cuda.mem_get_info()[0]
+    assert call(q, kc, vc, got, cur) == 0
+    gpu.cuda.synchronize()
+    assert gpu.cuda.mem_get_info()[0] == free0
+
+    want = gpu.empty_like(got)
+    ws = gpu.empty(zt.decode_workspace_bytes(B, n_ctx, H, Hkv, D) // 4 + 1, device="cuda", dtype=gpu.float32)
+    zt.decode(q, kc, vc, want, n_keys, B, n_ctx, H, Hkv, D, ws)
+    gpu.cuda.synchronize()
+    want_h = host(want)
+
+    graph = gpu.cuda.CUDAGraph()
+    got.fill_(float("nan"))
+    gpu.cuda.synchronize()
+    with gpu.cuda.graph(graph):
+        assert call(q, kc, vc, got, gpu.cuda.current_stream()) == 0
+    for i in range(4):
+        got.fill_(float("nan"))
+        graph.replay()
+        gpu.cuda.synchronize()
+        assert np.array_equal(host(got).view(np.uint32), want_h.view(np.uint32)), i
+        assert call(q2, kc2, vc2, other, cur) == 0     # eager use of the same scratch between replays
+        gpu.cuda.synchronize()
+        assert np.all(np.isfinite(host(other)))
+    del graph

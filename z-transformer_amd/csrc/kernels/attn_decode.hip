@@ -12,13 +12,18 @@
 // head, key chunk) and serves all G query heads of the group from one read.
 // Layout in a wave: LPR = DP/4 lanes cover one cache row with 128-bit loads,
 // so one load instruction reads RPI = 64/LPR whole rows (fully coalesced).
-// A step is NI = 8 such loads of K and of V.  Partial q.k dots are reduced
+// A step is NI = 4 such loads of K and of V, and a wave keeps two steps'
+// loads in flight (two register buffers, refilled alternately): eight loads
+// per step in one buffer fed from a copy of a prefetched one measured C4
+// 652 us and one sequence of 8192 keys 24.6 us; two buffers of eight needed
+// 288 registers (one wave per SIMD: 703 us) or spilled at 256 (1577 us); two
+// of four: 637 us and 22.5 us.  Partial q.k dots are reduced
 // across the LPR lanes with a butterfly reduce-scatter (each exchange halves
 // what a lane holds), which leaves every lane with complete scores and costs
 // fewer cross-lane moves than one tree per (key, head).  p is broadcast back
 // through a small wave-private LDS table; P.V accumulates in registers.
 // Per-chunk (max, denominator, accumulator) partials go to a caller-provided
-// workspace and zt_dec_combine merges them; with one chunk per sequence the
+// workspace and zt_dec_combine_* merges them; with one chunk per sequence the
 // workgroup writes the output itself and no combine runs.
 //
 // NW waves per workgroup take a chunk's steps in turn: four when the grid
@@ -32,6 +37,8 @@
 // eight 143 us; loads two or three steps ahead instead of one gained at most
 // 8 % at four waves and nothing at eight, and sixteen waves with half the
 // loads per step (to stay within 128 registers) 150 us.
+#include <type_traits>
+
 #include "common.h"
 #include "args.h"
 
@@ -75,7 +82,7 @@ template <int DP, int G, int NW>
 __device__ __forceinline__ void decode_body(const DecArgs &a) {
     constexpr int LPR = DP / 4;        // lanes per cache row
     constexpr int RPI = 64 / LPR;      // rows per load instruction
-    constexpr int NI = 8;              // load instructions per step
+    constexpr int NI = 4;              // load instructions per step (per buffer)
     constexpr int KS = NI * RPI;       // keys per step
     constexpr int V0 = NI * G;         // partial dots per lane
     constexpr int CNT = V0 >= LPR ? V0 / LPR : 1;  // complete scores per lane
@@ -137,7 +144,13 @@ __device__ __forceinline__ void decode_body(const DecArgs &a) {
     for (int gi = 0; gi < G; ++gi) { acc[gi] = zero4(); m[gi] = -INFINITY; ls[gi] = 0.f; }
 
     const int nsteps = (key1 - key0 + KS - 1) / KS;
-    f4 kx[NI], vx[NI], kn[NI], vn[NI];
+    // Two register buffers that the wave's steps alternate between: the loads
+    // of a wave's first two steps are both in flight before either is used,
+    // and a buffer is refilled (two steps ahead) as soon as its step is done.
+    // (Copying a prefetched buffer into a working one made every refill wait
+    // for the previous step's data first: one HBM round trip per step, which a
+    // single sequence split into short chunks -- two steps per wave -- paid twice.)
+    f4 ka[NI], va[NI], kb2[NI], vb2[NI];
     auto load_step = [&](int st, f4 (&kd)[NI], f4 (&vd)[NI]) {
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
@@ -146,7 +159,8 @@ __device__ __forceinline__ void decode_body(const DecArgs &a) {
             vd[i] = ld4(vb + (size_t)key * kld);
         }
     };
-    if (w < nsteps) load_step(w, kn, vn);
+    if (w < nsteps) load_step(w, ka, va);
+    if (w + NW < nsteps) load_step(w + NW, kb2, vb2);
 
     // Which (row i, head gi) each of this lane's complete scores belongs to.
     // With fewer partial dots than lanes per row, LPR / V0 lanes hold each complete score.
@@ -156,10 +170,7 @@ __device__ __forceinline__ void decode_body(const DecArgs &a) {
     for (int cc = 0; cc < CNT; ++cc) jidx[cc] = (V0 >= LPR) ? sub * CNT + cc : sub / SHARE;
     const bool counted = sub % SHARE == 0;
 
-    for (int st = w; st < nsteps; st += NW) {
-#pragma unroll
-        for (int i = 0; i < NI; ++i) { kx[i] = kn[i]; vx[i] = vn[i]; }
-        if (st + NW < nsteps) load_step(st + NW, kn, vn);
+    auto step = [&](int st, const f4 (&kx)[NI], const f4 (&vx)[NI]) {
         const int kbase = key0 + st * KS;
 
         float part[V0];
@@ -215,6 +226,20 @@ __device__ __forceinline__ void decode_body(const DecArgs &a) {
             for (int gi = 0; gi < G; ++gi) acc[gi] += pr[gi] * vx[i];
         }
         __builtin_amdgcn_wave_barrier();
+    };
+
+    // The fences keep the compiler from interleaving one step's arithmetic with
+    // the other's (which held both steps' temporaries live: 288 registers, one
+    // wave per SIMD, against 216 with the steps apart).
+    for (int st = w; st < nsteps; st += 2 * NW) {
+        step(st, ka, va);
+        if (st + 2 * NW < nsteps) load_step(st + 2 * NW, ka, va);
+        __builtin_amdgcn_sched_barrier(0);
+        if (st + NW < nsteps) {
+            step(st + NW, kb2, vb2);
+            if (st + 3 * NW < nsteps) load_step(st + 3 * NW, kb2, vb2);
+        }
+        __builtin_amdgcn_sched_barrier(0);
     }
 
     // Fold the row groups of this wave, then the NW waves of the workgroup.
@@ -272,26 +297,117 @@ __device__ __forceinline__ void decode_body(const DecArgs &a) {
     }
 }
 
-// One workgroup per (sequence, query head): merge the chunk partials.
-extern "C" __global__ void __launch_bounds__(256) zt_dec_combine(DecArgs a) {
+// Block-wide max / sum over the 256 threads of a combine workgroup (red:
+// four floats of LDS, reusable: the leading barrier orders a reuse after the
+// previous reduction's reads).
+DEVI float block_max256(float v, float *red) {
+    v = wave_max(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+DEVI float block_sum256(float v, float *red) {
+    v = wave_sum(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+// One workgroup per (sequence, query head): merge the chunk partials,
+// M = max_c m_c, L = sum_c l_c 2^(m_c - M), out = sum_c acc_c 2^(m_c - M) / L.
+// A single sequence split into 64 chunks leaves one short step of work here,
+// so what counts is the number of dependent global reads: a thread takes a
+// column piece (VW floats: a float4 when the row is, else one float) of
+// chunks g, g + NR, ... (NR = 256 / CPT chunk groups, CPT threads covering a
+// row), issues the loads of eight chunks' statistics and accumulator pieces
+// together, folds them into a running (max, sum, accumulator) of its own, and
+// the workgroup merges the threads' triples once: M by a block-wide max, the
+// weighted sums through LDS in a fixed order.  Up to 8 NR chunks per sequence
+// (the host's default split stays within that) take one round trip to memory.
+template <int CPT, int VW>
+__device__ __forceinline__ void combine_body(const DecArgs &a) {
+    constexpr int NR = 256 / CPT;
+    using vec = typename std::conditional<VW == 4, f4, float>::type;
+    __shared__ float red[4];
+    __shared__ vec part[NR][CPT];
+    __shared__ float lpart[NR];
+    const int tid = threadIdx.x;
     const int bl = (int)blockIdx.x / a.H, h = (int)blockIdx.x % a.H;
     const int b = a.b_base + bl;
     const int nch = (a.n_keys[bl] + a.chunk - 1) / a.chunk;
     const size_t slot0 = ((size_t)b * a.H + h) * a.n_chunks;
-    float M = -INFINITY;
-    for (int c = 0; c < nch; ++c) M = fmaxf(M, a.part_ml[(slot0 + c) * 2]);
-    float L = 0.f;
-    for (int c = 0; c < nch; ++c) L += a.part_ml[(slot0 + c) * 2 + 1] * fast_exp2(a.part_ml[(slot0 + c) * 2] - M);
-    const float inv = 1.f / L;
-    for (int n = threadIdx.x; n < a.dim; n += blockDim.x) {
-        float o = 0.f;
-        for (int c = 0; c < nch; ++c) o += a.part_acc[(slot0 + c) * a.dim + n] * fast_exp2(a.part_ml[(slot0 + c) * 2] - M);
-        a.out[(size_t)b * a.H * a.dim + (size_t)h * a.dim + n] = o * inv;
+    const float *ml = a.part_ml + slot0 * 2;
+    const int n = tid % CPT, g = tid / CPT;
+    const bool col_ok = VW * n < a.dim;
+    const float *pa = a.part_acc + slot0 * a.dim + VW * n;
+    auto zero = [] { vec z; if constexpr (VW == 4) z = zero4(); else z = 0.f; return z; };
+    float mt = -INFINITY, lt = 0.f;
+    vec ot = zero();
+    for (int c0 = g; c0 < nch; c0 += 8 * NR) {
+        float e[8], lv[8];
+        vec x[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int c = c0 + j * NR;
+            const bool ok = c < nch;
+            e[j] = ok ? ml[2 * c] : -INFINITY;
+            lv[j] = ok ? ml[2 * c + 1] : 0.f;
+            x[j] = (ok && col_ok) ? *reinterpret_cast<const vec *>(pa + (size_t)c * a.dim) : zero();
+        }
+        float mb = mt;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) mb = fmaxf(mb, e[j]);
+        const float r = mt == -INFINITY ? 0.f : fast_exp2(mt - mb);
+        lt *= r;
+        ot *= r;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float wj = e[j] == -INFINITY ? 0.f : fast_exp2(e[j] - mb);
+            lt += lv[j] * wj;
+            ot += x[j] * wj;
+        }
+        mt = mb;
+    }
+    const float M = block_max256(mt, red);
+    const float f = mt == -INFINITY ? 0.f : fast_exp2(mt - M);
+    part[g][n] = ot * f;
+    if (n == 0) lpart[g] = lt * f;
+    __syncthreads();
+    if (g == 0 && col_ok) {
+        float L = lpart[0];
+        vec sum = part[0][n];
+#pragma unroll
+        for (int rr = 1; rr < NR; ++rr) {
+            L += lpart[rr];
+            sum += part[rr][n];
+        }
+        float *po = a.out + (size_t)b * a.H * a.dim + (size_t)h * a.dim + VW * n;
+        *reinterpret_cast<vec *>(po) = sum * (1.f / L);
     }
 }
 
+// zt_dec_combine_v<C>: rows of whole float4 (d % 4 == 0), C = the padded
+// width / 4 threads per row; zt_dec_combine_s<C>: any even width, one float
+// per thread, C threads per row.
+#define ZT_DEC_COMBINE(NAME, CPT, VW)                                                              \
+    extern "C" __global__ void __launch_bounds__(256) zt_dec_combine_##NAME(DecArgs a) {         \
+        combine_body<CPT, VW>(a);                                                                  \
+    }
+ZT_DEC_COMBINE(v16, 16, 4)
+ZT_DEC_COMBINE(v32, 32, 4)
+ZT_DEC_COMBINE(v64, 64, 4)
+ZT_DEC_COMBINE(s64, 64, 1)
+ZT_DEC_COMBINE(s128, 128, 1)
+ZT_DEC_COMBINE(s256, 256, 1)
+
+// Two workgroups per CU (two waves per SIMD, at most 256 registers each): the
+// grid the host sizes for a full device is two per CU.  Eight heads per
+// workgroup do not fit 256 registers without spilling and keep one per CU.
 #define ZT_DEC(DP, G)                                                                              \
-    extern "C" __global__ void __launch_bounds__(256) zt_dec_d##DP##_g##G(DecArgs a) {           \
+    extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(G < 8 ? 2 : 1))) \
+    zt_dec_d##DP##_g##G(DecArgs a) {                                                               \
         decode_body<DP, G, 4>(a);                                                                  \
     }
 // Eight waves for one or two query heads per workgroup (more would spill).

@@ -30,13 +30,24 @@ DEVI double wave_sum_d(double v) {
     return v;
 }
 
-// Block-wide f64 sum over 256 threads.
-DEVI double block_sum_d(double v, double *red) {
+// Block-wide f64 sum over NWV waves (a workgroup of 64 * NWV threads): each
+// wave's sum goes to red[w], and the NWV of them are added as a pairwise tree
+// (for four waves (r0 + r1) + (r2 + r3)).
+template <int NWV>
+DEVI double block_sum_d(double v, double (&red)[NWV]) {
+    static_assert(NWV >= 1 && (NWV & (NWV - 1)) == 0, "the wave count must be a power of two");
     v = wave_sum_d(v);
     const int w = threadIdx.x >> 6;
     if ((threadIdx.x & 63) == 0) red[w] = v;
     __syncthreads();
-    return (red[0] + red[1]) + (red[2] + red[3]);
+    double t[NWV];
+#pragma unroll
+    for (int i = 0; i < NWV; ++i) t[i] = red[i];
+#pragma unroll
+    for (int n = NWV; n > 1; n >>= 1)
+#pragma unroll
+        for (int i = 0; i < n / 2; ++i) t[i] = t[2 * i] + t[2 * i + 1];
+    return t[0];
 }
 
 // cols % 4 == 0: each of the 256 threads keeps NV float4 of the row (cols <= 1024 * NV).

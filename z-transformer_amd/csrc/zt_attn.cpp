@@ -56,6 +56,32 @@ struct DeviceState {
 };
 DeviceState g_dev[kMaxDevices];
 
+// Kernels live in the code object named by their prefix; a lookup never
+// touches another module, so no failed hipModuleGetFunction is left behind in
+// the thread's last-error slot for the caller's next HIP call to report.
+int module_of(const char *name) {
+    if (strncmp(name, "zt_fwd", 6) == 0) return 0;
+    if (strncmp(name, "zt_bwd", 6) == 0) return 1;
+    if (strncmp(name, "zt_dec", 6) == 0) return 2;
+    if (strncmp(name, "zt_cal", 6) == 0) return 4;
+    if (strncmp(name, "zt_gem", 6) == 0) return 5;
+    return 3;
+}
+
+// A kernel's handle, from the cache or the code object (cached then); the
+// caller holds st.mu, or is load_device (before any other thread sees st).
+hipFunction_t resolve_fn(DeviceState &st, const char *name) {
+    auto it = st.fns.find(name);
+    if (it != st.fns.end()) return it->second;
+    hipFunction_t f = nullptr;
+    if (hipModuleGetFunction(&f, st.mods[module_of(name)], name) != hipSuccess || !f) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    st.fns.emplace(name, f);
+    return f;
+}
+
 void load_device(DeviceState &st, int dev) {
     int lds = 0;
     if (hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || lds <= 0)
@@ -75,6 +101,23 @@ void load_device(DeviceState &st, int dev) {
     // once while the device is current (each device holds its own copy).
     void *scratch = nullptr;
     if (zt_noalloc_scratch_address(&scratch) == 0) st.scratch = static_cast<float *>(scratch);
+    // The decode kernels' handles, resolved now so that a later
+    // zt_attn_decode_noalloc (possibly under graph capture) only looks them up.
+    char name[32];
+    for (int dp : {32, 64, 128, 256}) {
+        for (int g : {1, 2, 4, 8}) {
+            snprintf(name, sizeof name, "zt_dec_d%d_g%d", dp, g);
+            resolve_fn(st, name);
+        }
+        for (int g : {1, 2}) {
+            snprintf(name, sizeof name, "zt_dec8_d%d_g%d", dp, g);
+            resolve_fn(st, name);
+        }
+    }
+    for (const char *c : {"v16", "v32", "v64", "s64", "s128", "s256"}) {
+        snprintf(name, sizeof name, "zt_dec_combine_%s", c);
+        resolve_fn(st, name);
+    }
     st.ok = true;
 }
 
@@ -91,30 +134,11 @@ DeviceState *device_state() {
     return st.ok ? &st : nullptr;
 }
 
-// Kernels live in the code object named by their prefix; a lookup never
-// touches another module, so no failed hipModuleGetFunction is left behind in
-// the thread's last-error slot for the caller's next HIP call to report.
-int module_of(const char *name) {
-    if (strncmp(name, "zt_fwd", 6) == 0) return 0;
-    if (strncmp(name, "zt_bwd", 6) == 0) return 1;
-    if (strncmp(name, "zt_dec", 6) == 0) return 2;
-    if (strncmp(name, "zt_cal", 6) == 0) return 4;
-    if (strncmp(name, "zt_gem", 6) == 0) return 5;
-    return 3;
-}
-
 hipFunction_t get_fn(DeviceState *st, const char *name) {
     std::lock_guard<std::mutex> lk(st->mu);
-    auto it = st->fns.find(name);
-    if (it != st->fns.end()) return it->second;
-    hipFunction_t f = nullptr;
-    if (hipModuleGetFunction(&f, st->mods[module_of(name)], name) != hipSuccess || !f) {
-        (void)hipGetLastError();
-        return nullptr;
-    }
-    st->fns.emplace(name, f);
-    return f;
+    return resolve_fn(*st, name);
 }
+
 
 template <class Args>
 int launch(DeviceState *st, const char *name, unsigned blocks, const Args &args, hipStream_t stream,
@@ -619,7 +643,7 @@ DecGeom decode_geom(int B, int n_ctx, int n_heads, int n_kv_heads, int dim) {
     g.G = group % 8 == 0 ? 8 : group % 4 == 0 ? 4 : group % 2 == 0 ? 2 : 1;
     g.n_gsub = group / g.G;
     g.dp = dim <= 32 ? 32 : dim <= 64 ? 64 : dim <= 128 ? 128 : 256;
-    g.ks = 8 * (64 / (g.dp / 4));
+    g.ks = 4 * (64 / (g.dp / 4));  // the kernel's step: 4 loads of 64 / (dp / 4) rows
     const long long pairs = (long long)B * n_kv_heads * g.n_gsub;
     // Workgroups to aim for: 512, two per CU of MI355X's 256 (the workspace
     // size must not depend on the device). Measured on MI355X against 1024 / 2048
@@ -628,7 +652,7 @@ DecGeom decode_geom(int B, int n_ctx, int n_heads, int n_kv_heads, int dim) {
     long long per_seq = (target + pairs - 1) / pairs;
     if (per_seq < 1) per_seq = 1;
     long long chunk = (n_ctx + per_seq - 1) / per_seq;
-    const long long gran = 4LL * g.ks;  // every wave gets at least one step
+    const long long gran = 8LL * g.ks;  // every wave of four gets at least its two buffers' steps
     chunk = (chunk + gran - 1) / gran * gran;
     if (chunk < gran) chunk = gran;
     g.chunk = (int)chunk;
@@ -771,6 +795,65 @@ static float *ws_tiles(void *workspace, int B, int T, int n_heads) {
     return reinterpret_cast<float *>(static_cast<char *>(workspace) + align256((size_t)B * T * n_heads * sizeof(float)));
 }
 
+// Which workspaces hold scores, and of what.  zt_attn_forward_train_ws stamps
+// the workspace it wrote scores into with the call's device, q, k and shape;
+// the first backward stage 1 that consumes them (ZT_WS_SCORES) checks the
+// stamp against its own arguments and removes it, and so does any stage 1
+// that writes dS over the tiles without reading them.  A ZT_WS_SCORES call
+// with no matching stamp is refused instead of reading tiles that hold dS,
+// another shape's scores, or nothing.  Host-side only: no device read, so the
+// calls stay asynchronous.  What it cannot see is q or k rewritten in place
+// between the two calls (the same pointers, other values) -- a change that
+// makes the forward's out and lse stale too.
+struct ScoreStamp {
+    int dev;
+    const void *ws;
+    const float *q, *k;
+    int B, T, H, Hkv, dim;
+};
+std::mutex g_stamp_mu;
+std::vector<ScoreStamp> g_stamps;
+
+static int current_device() {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess) {
+        (void)hipGetLastError();
+        return -1;
+    }
+    return dev;
+}
+
+static void stamp_drop_locked(int dev, const void *ws) {
+    g_stamps.erase(std::remove_if(g_stamps.begin(), g_stamps.end(),
+                                  [&](const ScoreStamp &s) { return s.dev == dev && s.ws == ws; }),
+                   g_stamps.end());
+}
+
+static void stamp_set(const ScoreStamp &s) {
+    std::lock_guard<std::mutex> lk(g_stamp_mu);
+    stamp_drop_locked(s.dev, s.ws);
+    g_stamps.push_back(s);
+}
+
+static void stamp_drop(const void *ws) {
+    const int dev = current_device();
+    std::lock_guard<std::mutex> lk(g_stamp_mu);
+    stamp_drop_locked(dev, ws);
+}
+
+// True (and the stamp consumed) when `ws` holds the scores of exactly this q, k and shape.
+static bool stamp_take(const ScoreStamp &want) {
+    std::lock_guard<std::mutex> lk(g_stamp_mu);
+    for (auto it = g_stamps.begin(); it != g_stamps.end(); ++it) {
+        if (it->dev != want.dev || it->ws != want.ws) continue;
+        const bool same = it->q == want.q && it->k == want.k && it->B == want.B && it->T == want.T &&
+                          it->H == want.H && it->Hkv == want.Hkv && it->dim == want.dim;
+        if (same) g_stamps.erase(it);  // a refused call writes nothing: the scores stay usable
+        return same;
+    }
+    return false;
+}
+
 int zt_attn_forward_train_ws(const float *q, const float *k, const float *v, float *out, float *lse, void *workspace,
                              size_t workspace_bytes, int B, int T, int n_heads, int n_kv_heads, int dim,
                              hipStream_t stream) {
@@ -788,7 +871,13 @@ int zt_attn_forward_train_ws(const float *q, const float *k, const float *v, flo
     DeviceState *st = need ? device_state() : nullptr;
     float *s_out = (st && scores_path(dim, n_heads, n_kv_heads, st->lds_limit)) ? ws_tiles(workspace, B, T, n_heads)
                                                                                 : nullptr;
-    return forward_impl(q, k, v, out, B, T, n_heads, n_kv_heads, dim, 1, 64, 0, T, T, stream, lse, s_out);
+    const int rc = forward_impl(q, k, v, out, B, T, n_heads, n_kv_heads, dim, 1, 64, 0, T, T, stream, lse, s_out);
+    // (A refused call wrote nothing, so whatever stamp the workspace had still holds.)
+    if (rc == 0 && s_out)
+        stamp_set(ScoreStamp{current_device(), workspace, q, k, B, T, n_heads, n_kv_heads, dim});
+    else if (rc == 0 && workspace)
+        stamp_drop(workspace);
+    return rc;
 }
 
 int zt_attn_backward_train_ws(const float *q, const float *k, const float *v, const float *out, const float *dout,
@@ -829,7 +918,17 @@ int zt_attn_backward_train_ws(const float *q, const float *k, const float *v, co
     a.ds_out = ds;
     const int dp = pad32(dim);
     const bool qd_aligned = (uintptr_t)q % 16 == 0 && (uintptr_t)dout % 16 == 0;
-    if (scores && scores_path(dim, n_heads, n_kv_heads, st->lds_limit) && qd_aligned) {
+    const bool read_scores = scores && (stage & 1) && scores_path(dim, n_heads, n_kv_heads, st->lds_limit) &&
+                             qd_aligned;
+    if (read_scores &&
+        !stamp_take(ScoreStamp{current_device(), workspace, q, k, B, T, n_heads, n_kv_heads, dim})) {
+        fprintf(stderr,
+                "zt_attn: ZT_WS_SCORES, but this workspace holds no scores that zt_attn_forward_train_ws wrote for\n"
+                "       these q, k and this shape (or a backward stage 1 has already replaced them with dS).\n"
+                "       Refusing rather than reading stale tiles: run the forward again, or drop ZT_WS_SCORES.\n");
+        return 1;
+    }
+    if (read_scores) {
         // The forward left the scores in the dS tiles: a kernel that reads
         // them, 2 head halves x 64 keys (eight waves, d <= 128) or x 32 keys
         // (wider heads: eight waves splitting the columns, or four waves with
@@ -850,6 +949,8 @@ int zt_attn_backward_train_ws(const float *q, const float *k, const float *v, co
                  dp);
     }
     if (stage & 1) {
+        // Stage 1 writes dS over the tiles: whatever scores they held are gone.
+        if (!read_scores) stamp_drop(workspace);
         const unsigned long long rows = (unsigned long long)B * T * n_heads;
         if (!grid_ok((rows + 15) / 16)) return 1;
         if (launch(st, "zt_bwd_delta", (unsigned)((rows + 15) / 16), a, stream)) return 1;
@@ -985,8 +1086,14 @@ static int decode_launch(DeviceState *st, const float *q, const float *k_cache, 
     a.n_ctx = n_ctx; a.H = n_heads; a.Hkv = n_kv_heads; a.dim = dim;
     a.chunk = g.chunk; a.n_chunks = g.n_chunks; a.n_gsub = g.n_gsub;
     a.scale_log2e = (float)(1.4426950408889634 / std::sqrt((double)dim));
-    char name[64];
+    char name[64], combine[64];
     snprintf(name, sizeof name, "zt_dec_d%d_g%d", g.dp, g.G);
+    // The combine: float4 columns when rows are whole float4 (16-byte aligned
+    // partial rows: d % 4 == 0), dp / 4 threads per row; else one float each.
+    if (dim % 4 == 0)
+        snprintf(combine, sizeof combine, "zt_dec_combine_v%d", g.dp <= 64 ? 16 : g.dp / 4);
+    else
+        snprintf(combine, sizeof combine, "zt_dec_combine_s%d", g.dp < 64 ? 64 : g.dp);
     for (int b0 = 0; b0 < B; b0 += ZT_DEC_MAXB) {
         a.b_base = b0;
         a.nb = B - b0 < ZT_DEC_MAXB ? B - b0 : ZT_DEC_MAXB;
@@ -995,7 +1102,7 @@ static int decode_launch(DeviceState *st, const float *q, const float *k_cache, 
         if (!grid_ok(blocks)) return 1;
         if (launch(st, name, (unsigned)blocks, a, stream)) return 1;
         // One chunk per sequence: the decode kernel wrote the output itself.
-        if (g.n_chunks > 1 && launch(st, "zt_dec_combine", (unsigned)(a.nb * n_heads), a, stream)) return 1;
+        if (g.n_chunks > 1 && launch(st, combine, (unsigned)(a.nb * n_heads), a, stream)) return 1;
     }
     return 0;
 }

@@ -14,8 +14,18 @@
 // dropped by any upload into q, k, v, out or row_max, by a decode-shaped
 // forward_at, and by zt_holder_forget; a backward without a current forward
 // runs the reference pair (zt_attn_backward), which rebuilds the statistics.
-// Without the workspace (its allocation failed, or zt_holder_init_exact) the
-// fast pair is zt_attn_forward_train + zt_attn_backward_train.
+// The workspace is taken at the first whole-shape forward (a holder that only
+// decodes never takes it).  Without it (its allocation failed, it would take
+// more than a quarter of the device's free memory, or zt_holder_init_exact)
+// the fast pair is zt_attn_forward_train + zt_attn_backward_train.
+//
+// One query row.  device.zig's forwardAt with t = 1 is the reference's decode
+// seam (src/decode.zig:462): one sequence, so the one-row forward of
+// zt_attn_forward has only (kv head x head sub-group) workgroups and cannot
+// fill the device.  The holder owns a small partials buffer (allocated at
+// init, zt_attn_decode_workspace bytes for one sequence of t rows) and runs
+// zt_attn_decode instead, which splits the visible keys into chunks across
+// the device and merges the chunk partials.
 #include <hip/hip_runtime_api.h>
 
 #include <climits>
@@ -78,8 +88,33 @@ struct Attn {
     int c_t = 0, c_heads = 0, c_kv_heads = 0, c_dim = 0;
     void *ws = nullptr;  // zt_attn_backward_train_workspace bytes, or null
     size_t ws_bytes = 0;
+    void *dec_ws = nullptr;  // zt_attn_decode_workspace bytes for one sequence, or null
+    size_t dec_bytes = 0;
     bool fast = true;    // false: the reference pair only (zt_holder_init_exact)
+    mutable bool ws_tried = false;  // the first whole-shape forward has asked for the score workspace
     mutable Saved saved = Saved::None;
+
+    // The score workspace, asked for once (by the first whole-shape forward).
+    // It is an optimisation: without it the holder still runs the
+    // saved-statistics pair, so a failed allocation is no error.  It grows
+    // with t^2 (1.0 GiB at t = 4096 with 32 heads, 4.0 GiB at 8192), so it is
+    // taken only while it stays within a quarter of the device's free memory,
+    // leaving the rest to the caller.
+    void take_workspace() const {
+        if (ws_tried) return;
+        ws_tried = true;
+        const size_t wsb = zt_attn_backward_train_workspace(1, c_t, c_heads, c_kv_heads, c_dim);
+        size_t free_b = 0, total_b = 0;
+        const bool fits = hipMemGetInfo(&free_b, &total_b) == hipSuccess && wsb <= free_b / 4;
+        void *p = nullptr;
+        if (wsb != 0 && fits && hipMalloc(&p, wsb) == hipSuccess && p) {
+            Attn *self = const_cast<Attn *>(this);
+            self->ws = p;
+            self->ws_bytes = wsb;
+        } else {
+            (void)hipGetLastError();
+        }
+    }
 
     size_t buffer_bytes(int which) const {
         size_t n = 0;
@@ -97,6 +132,9 @@ struct Attn {
         if (ws) (void)hipFree(ws);
         ws = nullptr;
         ws_bytes = 0;
+        if (dec_ws) (void)hipFree(dec_ws);
+        dec_ws = nullptr;
+        dec_bytes = 0;
     }
 };
 
@@ -157,13 +195,15 @@ static int holder_init(size_t t, size_t n_heads, size_t n_kv_heads, size_t dim, 
     h->a.c_t = c_t; h->a.c_heads = c_heads; h->a.c_kv_heads = c_kv; h->a.c_dim = c_dim;
     h->a.fast = fast;
     if (fast) {
-        // The score workspace is an optimisation: without it the holder still
-        // runs the saved-statistics pair, so a failed allocation is no error.
-        const size_t wsb = zt_attn_backward_train_workspace(1, c_t, c_heads, c_kv, c_dim);
+        // The one-row forward's chunk partials (about 1 MiB at t = 8192 with 32
+        // heads); without them forward_at(t = 1) takes zt_attn_forward, so a
+        // failed allocation is no error.  (The score workspace is taken by the
+        // first whole-shape forward: a decode-only holder never needs it.)
+        const size_t decb = zt_attn_decode_workspace(1, c_t, c_heads, c_kv, c_dim);
         void *p = nullptr;
-        if (wsb != 0 && hipMalloc(&p, wsb) == hipSuccess && p) {
-            h->a.ws = p;
-            h->a.ws_bytes = wsb;
+        if (decb != 0 && hipMalloc(&p, decb) == hipSuccess && p) {
+            h->a.dec_ws = p;
+            h->a.dec_bytes = decb;
         } else {
             (void)hipGetLastError();
         }
@@ -180,7 +220,7 @@ int zt_holder_init_exact(size_t t, size_t n_heads, size_t n_kv_heads, size_t dim
     return holder_init(t, n_heads, n_kv_heads, dim, false, out);
 }
 
-size_t zt_holder_workspace_bytes(const zt_holder *h) { return h ? h->a.ws_bytes : 0; }
+size_t zt_holder_workspace_bytes(const zt_holder *h) { return h ? h->a.ws_bytes + h->a.dec_bytes : 0; }
 
 void zt_holder_forget(const zt_holder *h) {
     if (h) h->a.saved = zt::Saved::None;
@@ -203,6 +243,15 @@ size_t zt_holder_total_bytes(const zt_holder *h) {
 
 float *zt_holder_buffer(const zt_holder *h, int which) {
     if (!h || which < 0 || which >= ZT_N_BUFFERS) return nullptr;
+    // A writable pointer to an input of the saved state: the caller may change
+    // what the forward saw, so the next backward rebuilds the statistics.
+    if (which == ZT_BUF_Q || which == ZT_BUF_K || which == ZT_BUF_V || which == ZT_BUF_OUT || which == ZT_BUF_ROW_MAX)
+        h->a.saved = zt::Saved::None;
+    return h->a.buf[which];
+}
+
+const float *zt_holder_buffer_ro(const zt_holder *h, int which) {
+    if (!h || which < 0 || which >= ZT_N_BUFFERS) return nullptr;
     return h->a.buf[which];
 }
 
@@ -212,6 +261,7 @@ int zt_holder_forward_at(const zt_holder *h, int group_q, int max_tile, int q_of
     a.saved = zt::Saved::None;
     const bool whole = q_offset == 0 && n_keys == a.c_t && t == a.c_t;
     if (a.fast && whole && zt::forward_args_ok(group_q, max_tile, a.c_dim)) {
+        a.take_workspace();
         float *lse = a.buf[ZT_BUF_ROW_MAX];
         const int rc = a.ws ? zt_attn_forward_train_ws(a.buf[ZT_BUF_Q], a.buf[ZT_BUF_K], a.buf[ZT_BUF_V],
                                                        a.buf[ZT_BUF_OUT], lse, a.ws, a.ws_bytes, 1, a.c_t, a.c_heads,
@@ -228,6 +278,14 @@ int zt_holder_forward_at(const zt_holder *h, int group_q, int max_tile, int q_of
         }
         a.saved = a.ws ? zt::Saved::Scores : zt::Saved::Lse;
         return ZT_OK;
+    }
+    if (a.dec_ws && t == 1 && zt::forward_args_ok(group_q, max_tile, a.c_dim)) {
+        // The query at q_offset sees keys 0..q_offset (q_offset + 1 <= n_keys by
+        // forward_bounds): the split-K decode over those rows of the holder's cache.
+        const int visible = q_offset + 1;
+        const int rc = zt_attn_decode(a.buf[ZT_BUF_Q], a.buf[ZT_BUF_K], a.buf[ZT_BUF_V], a.buf[ZT_BUF_OUT], &visible,
+                                      1, a.c_t, a.c_heads, a.c_kv_heads, a.c_dim, a.dec_ws, a.dec_bytes, nullptr);
+        return rc != 0 ? ZT_CONFIG_REFUSED : ZT_OK;
     }
     const int rc = zt_attn_forward(a.buf[ZT_BUF_Q], a.buf[ZT_BUF_K], a.buf[ZT_BUF_V], a.buf[ZT_BUF_OUT], t, a.c_heads,
                                    a.c_kv_heads, a.c_dim, group_q, max_tile, q_offset, n_keys, nullptr);

@@ -32,7 +32,7 @@ HOLDER_SYMBOLS = [
     "zt_bytes_for", "zt_to_cint", "zt_forward_bounds", "zt_holder_init", "zt_holder_deinit",
     "zt_holder_total_bytes", "zt_holder_buffer", "zt_holder_forward", "zt_holder_forward_at",
     "zt_holder_backward", "zt_holder_upload", "zt_holder_download", "zt_holder_init_exact",
-    "zt_holder_workspace_bytes", "zt_holder_forget",
+    "zt_holder_workspace_bytes", "zt_holder_forget", "zt_holder_buffer_ro",
 ]
 
 # include/zt_holder.h enum zt_error
@@ -115,6 +115,7 @@ def load_library(path):
         "zt_holder_deinit": (None, [P]),
         "zt_holder_total_bytes": (Z, [P]),
         "zt_holder_buffer": (P, [P, I]),
+        "zt_holder_buffer_ro": (P, [P, I]),
         "zt_holder_forward": (I, [P, I, I]),
         "zt_holder_forward_at": (I, [P, I, I, I, I, I]),
         "zt_holder_backward": (I, [P, I]),
