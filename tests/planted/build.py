@@ -1,8 +1,10 @@
 """Builds the planted-defect test libraries (TEST INFRASTRUCTURE ONLY).
 
 Each entry of PLANTS compiles one kernel source with -DZT_PLANT=<n> (the
-defect points in z-transformer_amd/csrc/kernels/common.h), keeping only the
-kernels of the negative-control shape (d = 32), and links it with the other,
+defect points in z-transformer_amd/csrc/kernels/common.h) -- for the forward
+and backward sources only the kernels of the negative-control shapes (d = 32
+for the reference entry points, d = 128 for the training path), for the dense
+product and decode sources all of them -- and links it with the other,
 unmodified code objects and the library's own host objects into
 tests/planted/_build/<name>/libzt_attn.so.  tests/test_gpu_planted.py loads
 each one and checks that its parity gate rejects it.  Nothing shipped loads
@@ -23,6 +25,9 @@ PLANTS = {
     "fwd_mask": (1, "fwd"), "fwd_gqa": (2, "fwd"), "fwd_rescale": (3, "fwd"), "fwd_scale": (4, "fwd"),
     "bwd_mask": (11, "bwd"), "bwd_gqa": (12, "bwd"), "bwd_jacobian": (13, "bwd"), "bwd_scale": (14, "bwd"),
     "norm_weight": (21, "misc"), "norm_mean": (22, "misc"), "norm_tensor": (23, "misc"),
+    # The training path's headline kernels and the decode combine.
+    "train_fwd_scores": (5, "fwd"), "train_ds_tiles": (15, "bwd"), "train_dq_scale": (16, "gemm"),
+    "decode_merge": (17, "dec"),
 }
 
 

@@ -826,7 +826,9 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
             for (int u = 0; u < NU; ++u) {
                 // wave-uniform: a sub-tile past the last row or above the diagonal has no slot
                 if (t0 + 16 * u >= a.T || t0 + 16 * u + 15 < s0) continue;
-                const size_t tile = cur.sblk + zt_tri_index((t0 >> 4) + u, s0 >> 4);
+                // (ZT_PLANT 15 swaps the two sub-tiles' slots where both exist.)
+                const int us = (ZT_PLANT == 15 && NU == 2 && t0 + 16 < a.T && t0 + 15 >= s0) ? NU - 1 - u : u;
+                const size_t tile = cur.sblk + zt_tri_index((t0 >> 4) + us, s0 >> 4);
                 // Scalar tile base plus the lane's 32-bit byte offset.
                 __builtin_nontemporal_store(
                     dsv[u], reinterpret_cast<f4 *>(reinterpret_cast<char *>(a.ds_out + tile * 256) + lane * 16u));
@@ -1388,8 +1390,9 @@ ZT_BWD_DKDV8PD(192) ZT_BWD_DKDV8PD(256)
     }
 ZT_BWD_DKDV8PD1(64) ZT_BWD_DKDV8PD1(128)
 #else
-// A planted-defect build (test-only): the kernels of the negative-control shape, d = 32.
-ZT_BWD_DQ_PF(32) ZT_BWD_DQ_LSE(32) ZT_BWD_DKDV8(32)
+// A planted-defect build (test-only): the kernels of the negative-control
+// shapes, d = 32 (the reference entry points) and d = 128 (the training path).
+ZT_BWD_DQ_PF(32) ZT_BWD_DQ_LSE(32) ZT_BWD_DKDV8(32) ZT_BWD_DKDV8S(128)
 #endif
 
 // delta[row] = sum_d o[row, d] * dout[row, d] over the B*T*H rows of dim

@@ -12,12 +12,12 @@
 // head, key chunk) and serves all G query heads of the group from one read.
 // Layout in a wave: LPR = DP/4 lanes cover one cache row with 128-bit loads,
 // so one load instruction reads RPI = 64/LPR whole rows (fully coalesced).
-// A step is NI = 4 such loads of K and of V, and a wave keeps two steps'
-// loads in flight (two register buffers, refilled alternately): eight loads
-// per step in one buffer fed from a copy of a prefetched one measured C4
-// 652 us and one sequence of 8192 keys 24.6 us; two buffers of eight needed
-// 288 registers (one wave per SIMD: 703 us) or spilled at 256 (1577 us); two
-// of four: 637 us and 22.5 us.  Partial q.k dots are reduced
+// A step is NI such loads of K and of V, and a wave keeps two steps' loads in
+// flight (two register buffers, refilled alternately).  For the four-wave
+// kernels NI = 4: eight loads per step in one buffer fed from a copy of a
+// prefetched one measured C4 652 us and one sequence of 8192 keys 24.6 us;
+// two buffers of eight needed 288 registers (one wave per SIMD: 703 us) or
+// spilled at 256 (1577 us); two of four: 637 us and 22.5 us.  Partial q.k dots are reduced
 // across the LPR lanes with a butterfly reduce-scatter (each exchange halves
 // what a lane holds), which leaves every lane with complete scores and costs
 // fewer cross-lane moves than one tree per (key, head).  p is broadcast back
@@ -78,11 +78,11 @@ DEVI float wave_sum(float v) {
     return v;
 }
 
-template <int DP, int G, int NW>
+template <int DP, int G, int NW, int NI>
 __device__ __forceinline__ void decode_body(const DecArgs &a) {
     constexpr int LPR = DP / 4;        // lanes per cache row
     constexpr int RPI = 64 / LPR;      // rows per load instruction
-    constexpr int NI = 4;              // load instructions per step (per buffer)
+    // NI: load instructions per step (per buffer)
     constexpr int KS = NI * RPI;       // keys per step
     constexpr int V0 = NI * G;         // partial dots per lane
     constexpr int CNT = V0 >= LPR ? V0 / LPR : 1;  // complete scores per lane
@@ -336,7 +336,7 @@ __device__ __forceinline__ void combine_body(const DecArgs &a) {
     const int tid = threadIdx.x;
     const int bl = (int)blockIdx.x / a.H, h = (int)blockIdx.x % a.H;
     const int b = a.b_base + bl;
-    const int nch = (a.n_keys[bl] + a.chunk - 1) / a.chunk;
+    const int nch = (a.n_keys[bl] + a.chunk - 1) / a.chunk - (ZT_PLANT == 17 ? 1 : 0);
     const size_t slot0 = ((size_t)b * a.H + h) * a.n_chunks;
     const float *ml = a.part_ml + slot0 * 2;
     const int n = tid % CPT, g = tid / CPT;
@@ -408,12 +408,16 @@ ZT_DEC_COMBINE(s256, 256, 1)
 #define ZT_DEC(DP, G)                                                                              \
     extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(G < 8 ? 2 : 1))) \
     zt_dec_d##DP##_g##G(DecArgs a) {                                                               \
-        decode_body<DP, G, 4>(a);                                                                  \
+        decode_body<DP, G, 4, 4>(a);                                                               \
     }
-// Eight waves for one or two query heads per workgroup (more would spill).
+// Eight waves for one or two query heads per workgroup (more would spill),
+// with steps of eight loads: the one-row forward gives a workgroup a whole
+// sequence, so it is the step's arithmetic between loads that counts there
+// (one C4 sequence of 8192 keys per call: four-load steps 160 us a call,
+// eight 144 us; the single-buffer kernel before them 148 us).
 #define ZT_DEC8(DP, G)                                                                             \
     extern "C" __global__ void __launch_bounds__(512) zt_dec8_d##DP##_g##G(DecArgs a) {          \
-        decode_body<DP, G, 8>(a);                                                                  \
+        decode_body<DP, G, 8, 8>(a);                                                               \
     }
 #define ZT_DEC_ALL(DP) ZT_DEC(DP, 1) ZT_DEC(DP, 2) ZT_DEC(DP, 4) ZT_DEC(DP, 8) ZT_DEC8(DP, 1) ZT_DEC8(DP, 2)
 ZT_DEC_ALL(32)

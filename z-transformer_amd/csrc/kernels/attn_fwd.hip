@@ -167,7 +167,9 @@ __device__ __forceinline__ void attn_fwd_tile(const FwdArgs &a, const int tile) 
             for (int j = 0; j < NJ; ++j) {
                 if (k0 + 16 * j >= kend_w) continue;  // wave-uniform: above the diagonal
 #pragma unroll
-                for (int r = 0; r < 4; ++r) __builtin_nontemporal_store(s[j][r], srow + j * 256 + (4 * grp + r) * 4);
+                for (int r = 0; r < 4; ++r)
+                    __builtin_nontemporal_store(ZT_PLANT == 5 ? s[j][r] / a.scale_log2e : s[j][r],
+                                                srow + j * 256 + (4 * grp + r) * 4);
             }
         }
         if (k0 + BK - 1 > a.q_offset + row0 || k0 + BK > a.n_keys) {  // wave-uniform: a key past a row or past n_keys
@@ -266,6 +268,13 @@ __device__ __forceinline__ void attn_fwd_body(const FwdArgs &a) {
         attn_fwd_body<DP, 32, 8, true>(a);                                                         \
     }
 
+// The same eight-wave kernel under its own name for launches that keep the
+// scores (s_out set), so that a profile tells the two roles apart.
+#define ZT_FWD_PFS(DP)                                                                             \
+    extern "C" __global__ void __launch_bounds__(512, 4) zt_fwd8ps_d##DP##_k32(FwdArgs a) {      \
+        attn_fwd_body<DP, 32, 8, true>(a);                                                         \
+    }
+
 #if ZT_PLANT == 0
 ZT_FWD(32, 32) ZT_FWD(32, 64)
 ZT_FWD(64, 32) ZT_FWD(64, 64)
@@ -277,14 +286,9 @@ ZT_FWD(224, 32) ZT_FWD(224, 64)
 ZT_FWD(256, 32) ZT_FWD(256, 64)
 ZT_FWD_PF(32) ZT_FWD_PF(64) ZT_FWD_PF(96) ZT_FWD_PF(128)
 ZT_FWD_PF(160) ZT_FWD_PF(192) ZT_FWD_PF(224) ZT_FWD_PF(256)
-// The same eight-wave kernel under its own name for launches that keep the
-// scores (s_out set), so that a profile tells the two roles apart.
-#define ZT_FWD_PFS(DP)                                                                             \
-    extern "C" __global__ void __launch_bounds__(512, 4) zt_fwd8ps_d##DP##_k32(FwdArgs a) {      \
-        attn_fwd_body<DP, 32, 8, true>(a);                                                         \
-    }
 ZT_FWD_PFS(32) ZT_FWD_PFS(64) ZT_FWD_PFS(96) ZT_FWD_PFS(128)
 #else
-// A planted-defect build (test-only): the kernels of the negative-control shape, d = 32.
-ZT_FWD_PF(32)
+// A planted-defect build (test-only): the kernels of the negative-control
+// shapes, d = 32 (the reference entry points) and d = 128 (the training path).
+ZT_FWD_PF(32) ZT_FWD_PF(128) ZT_FWD_PFS(128)
 #endif

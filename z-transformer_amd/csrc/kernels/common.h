@@ -38,10 +38,16 @@
 //   2  forward: every query head reads kv head 0 (GQA collapsed)
 //   3  forward: the online softmax's running-max rescale skipped
 //   4  forward: the 1/sqrt(d) scale dropped
+//   5  training forward: the score tiles it keeps for the backward are stored
+//      without the log2(e)/sqrt(d) scale (O and lse stay right)
 //   11 backward: causal mask dropped in the dq and dk/dv kernels
 //   12 backward: K and V read from kv head 0 for every kv group
 //   13 backward: the softmax Jacobian dropped (dS = P, so dv stays right)
 //   14 backward: the 1/sqrt(d) scale dropped (scores, dq and dk)
+//   15 score-reading dk/dv: a stage's two dS sub-tiles stored in each other's
+//      slots (dk and dv stay right, the dq product reads the wrong tiles)
+//   16 dq-from-dS product: the 1/sqrt(d) scale dropped (dq = sqrt(d) x right)
+//   17 decode combine: the last chunk of a split sequence left out of the merge
 //   21 RMSNorm: the first weight element moved by 1e-3
 //   22 RMSNorm: the mean of x instead of the mean of its squares
 //   23 RMSNorm: the weight read from x (the wrong tensor at the right index)

@@ -412,7 +412,7 @@ DEVI void dq_ds_tile(const DqDsArgs &g, const int tm, const int tn, const int bh
 #pragma unroll
             for (int j = 0; j < TW; ++j) {
                 const int n = n0 + wn + local_index<TW, false>(j, l16);
-                if (n < g.dim) crow[n] = acc[i][j][r] * g.scale;
+                if (n < g.dim) crow[n] = ZT_PLANT == 16 ? acc[i][j][r] : acc[i][j][r] * g.scale;
             }
         }
 }
