@@ -365,6 +365,68 @@ def decode_seam_holder(torch, zt, dev, n_ctx, H, Hkv, D, n_holders, calls):
             L.zt_holder_deinit(hp)
 
 
+def other_configs(torch, zt, dev, args, normal, scores):
+    # ---------------- C2, C5: the other training configurations ----------------
+    # Secondary figures (C3 is the headline): the same training step -- the
+    # forward keeping its scores where the shape allows, then the backward --
+    # and the reference's own entry points, on the configurations' inputs
+    # (C5: N(0, 2), sigma = sqrt(2)).
+    other = {}
+    other_cfgs = {"C2": (4, 1024, 8, 8, 64, 1.0), "C5": (2, 2048, 16, 4, 256, 2.0 ** 0.5)}
+    for cname, (Bo, To, Ho, Hkvo, Do, sig) in other_cfgs.items():
+        qo, do_ = normal(Bo * To * Ho * Do, SEEDS["q"], sig), normal(Bo * To * Ho * Do, SEEDS["do"], sig)
+        ko, vo = normal(Bo * To * Hkvo * Do, SEEDS["k"], sig), normal(Bo * To * Hkvo * Do, SEEDS["v"], sig)
+        oo, dqo = torch.empty_like(qo), torch.empty_like(qo)
+        dko, dvo = torch.empty_like(ko), torch.empty_like(vo)
+        lseo, rmo, rlo, rdo = (torch.empty(Bo * To * Ho, device=dev) for _ in range(4))
+        wo = torch.empty(zt.backward_train_workspace_bytes(Bo, To, Ho, Hkvo, Do) // 4, device=dev)
+        flop_o = 7 * 2 * Do * Bo * Ho * To * (To + 1) / 2
+
+        def train_o():
+            zt.forward_train_ws(qo, ko, vo, oo, lseo, wo, To, Ho, Hkvo, Do, B=Bo)
+            zt.backward_train_ws(qo, ko, vo, oo, do_, lseo, dqo, dko, dvo, wo, To, Ho, Hkvo, Do, B=Bo, stage=scores)
+
+        def ref_o():
+            zt.forward(qo, ko, vo, oo, To, Ho, Hkvo, Do, B=Bo)
+            zt.backward(qo, ko, vo, do_, dqo, dko, dvo, rmo, rlo, rdo, To, Ho, Hkvo, Do, B=Bo)
+
+        entry = {"workload": f"{cname} B={Bo} T={To} Hq={Ho} Hkv={Hkvo} d={Do} f32"}
+        for tag, fn in (("train", train_o), ("reference_abi", ref_o)):
+            for _ in range(args.warmup):
+                fn()
+            t_o = event_time(torch, fn, max(3, args.steps))
+            entry[tag] = {"ms_per_step": round(t_o, 4), "TFLOP/s": round(flop_o / (t_o * 1e-3) / 1e12, 3)}
+            log(f"{cname} step ({tag}): {t_o:.3f} ms, {flop_o / (t_o * 1e-3) / 1e12:.2f} TFLOP/s fwd+bwd")
+        # Per kernel of the training step, as for C3: the forward, the dk/dv
+        # stage (zt_bwd_delta + the dk/dv kernel, after a forward each time
+        # when it reads the forward's scores) and the dq product.
+        unit_o = flop_o / 7
+        n_fwd, n_dq, n_dkdv = zt.plan_train(Bo, To, Ho, Hkvo, Do)
+        reads_scores = "dkdv8s" in n_dkdv or "dkdv_dmas" in n_dkdv
+        fwd_o = lambda: zt.forward_train_ws(qo, ko, vo, oo, lseo, wo, To, Ho, Hkvo, Do, B=Bo)
+        st1 = 1 | (zt.ZT_WS_SCORES if reads_scores else 0)
+        dkdv_o = lambda: zt.backward_train_ws(qo, ko, vo, oo, do_, lseo, dqo, dko, dvo, wo, To, Ho, Hkvo, Do, B=Bo,
+                                              stage=st1)
+        dq_o = lambda: zt.backward_train_ws(qo, ko, vo, oo, do_, lseo, dqo, dko, dvo, wo, To, Ho, Hkvo, Do, B=Bo,
+                                            stage=2)
+        nk = max(5, args.steps)
+        t_f = event_time(torch, fwd_o, nk)
+        t_kv = event_time_after(torch, fwd_o, dkdv_o, nk) if reads_scores else event_time(torch, dkdv_o, nk)
+        t_q = event_time(torch, dq_o, nk)
+        ks = []
+        for kname, t_k, units in ((n_fwd, t_f, 2), (n_dkdv, t_kv, 3 if reads_scores else 4), (n_dq, t_q, 1)):
+            tf_k = units * unit_o / (t_k * 1e-3) / 1e12
+            ks.append({"kernel": kname, "ms": round(t_k, 4), "flop": units * unit_o, "tflops": round(tf_k, 3),
+                       "frac_mfma_f32": round(tf_k / PEAK_MFMA_F32, 4)})
+            log(f"  {cname} {kname}: {t_k * 1e3:.1f} us, {tf_k:.2f} TFLOP/s ({100 * tf_k / PEAK_MFMA_F32:.1f}%)")
+        entry["train"]["kernels"] = ks
+        entry["train"]["launch_gaps_ms"] = round(entry["train"]["ms_per_step"] - t_f - t_kv - t_q, 4)
+        other[cname] = entry
+        del qo, ko, vo, do_, oo, dqo, dko, dvo, lseo, rmo, rlo, rdo, wo
+
+    return other
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -373,6 +435,8 @@ def main():
     ap.add_argument("--cpu-rows", type=int, default=48, help="query rows of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-other", action="store_true", help="skip the C2 / C5 figures (profiling runs)")
+    ap.add_argument("--only-other", action="store_true",
+                    help="run the C2 / C5 section alone and print its figures (profiling runs)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -390,6 +454,11 @@ def main():
         t = torch.empty(n, device=dev, dtype=torch.float32)
         zt.fill_normal(t, seed, 0.0, sigma)
         return t
+
+    if args.only_other:
+        other = other_configs(torch, zt, dev, args, normal, 3 | zt.ZT_WS_SCORES)
+        print(json.dumps({"other_configs": other}), flush=True)
+        return
 
     # ---------------- calibration: what this device sustains ----------------
     cal_src = torch.empty(1 << 30, device=dev)          # 4 GiB streaming-read source
@@ -561,40 +630,7 @@ def main():
                 "frac": round(dom["tflops"] / PEAK_MFMA_F32, 4), "traffic": traffic, "kernel": dom["kernel"]}
     del out, dq, dk, dv, do, q, k, v, rm, rl, rd, lse, delta, work
 
-    # ---------------- C2, C5: the other training configurations ----------------
-    # Secondary figures (C3 is the headline): the same training step -- the
-    # forward keeping its scores where the shape allows, then the backward --
-    # and the reference's own entry points, on the configurations' inputs
-    # (C5: N(0, 2), sigma = sqrt(2)).
-    other = {}
-    other_cfgs = {} if args.no_other else {"C2": (4, 1024, 8, 8, 64, 1.0), "C5": (2, 2048, 16, 4, 256, 2.0 ** 0.5)}
-    for cname, (Bo, To, Ho, Hkvo, Do, sig) in other_cfgs.items():
-        qo, do_ = normal(Bo * To * Ho * Do, SEEDS["q"], sig), normal(Bo * To * Ho * Do, SEEDS["do"], sig)
-        ko, vo = normal(Bo * To * Hkvo * Do, SEEDS["k"], sig), normal(Bo * To * Hkvo * Do, SEEDS["v"], sig)
-        oo, dqo = torch.empty_like(qo), torch.empty_like(qo)
-        dko, dvo = torch.empty_like(ko), torch.empty_like(vo)
-        lseo, rmo, rlo, rdo = (torch.empty(Bo * To * Ho, device=dev) for _ in range(4))
-        wo = torch.empty(zt.backward_train_workspace_bytes(Bo, To, Ho, Hkvo, Do) // 4, device=dev)
-        flop_o = 7 * 2 * Do * Bo * Ho * To * (To + 1) / 2
-
-        def train_o():
-            zt.forward_train_ws(qo, ko, vo, oo, lseo, wo, To, Ho, Hkvo, Do, B=Bo)
-            zt.backward_train_ws(qo, ko, vo, oo, do_, lseo, dqo, dko, dvo, wo, To, Ho, Hkvo, Do, B=Bo, stage=scores)
-
-        def ref_o():
-            zt.forward(qo, ko, vo, oo, To, Ho, Hkvo, Do, B=Bo)
-            zt.backward(qo, ko, vo, do_, dqo, dko, dvo, rmo, rlo, rdo, To, Ho, Hkvo, Do, B=Bo)
-
-        entry = {"workload": f"{cname} B={Bo} T={To} Hq={Ho} Hkv={Hkvo} d={Do} f32"}
-        for tag, fn in (("train", train_o), ("reference_abi", ref_o)):
-            for _ in range(args.warmup):
-                fn()
-            t_o = event_time(torch, fn, max(3, args.steps))
-            entry[tag] = {"ms_per_step": round(t_o, 4), "TFLOP/s": round(flop_o / (t_o * 1e-3) / 1e12, 3)}
-            log(f"{cname} step ({tag}): {t_o:.3f} ms, {flop_o / (t_o * 1e-3) / 1e12:.2f} TFLOP/s fwd+bwd")
-        entry["train"]["kernels"] = list(zt.plan_train(Bo, To, Ho, Hkvo, Do))
-        other[cname] = entry
-        del qo, ko, vo, do_, oo, dqo, dko, dvo, lseo, rmo, rlo, rdo, wo
+    other = {} if args.no_other else other_configs(torch, zt, dev, args, normal, scores)
 
     # ---------------- C4: decode step ----------------
     Bd, n_ctx = 64, 8192

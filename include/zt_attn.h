@@ -328,7 +328,9 @@ int zt_attn_plan(int B, int T, int n_heads, int n_kv_heads, int dim, int max_til
  *   the slab kernels), ZT_GEMM_SK_TILE 16|32 (split-K tile), ZT_DQDS_TILE
  *   64|128 (dq-from-dS product tile), ZT_ROW_G
  *   1|2|4|8 and ZT_ROW_W 4|8 (query heads and waves per workgroup of the
- *   one-row forward, T = 1).
+ *   one-row forward, T = 1), ZT_ATTN_FKS 1|2 (key parts of the forward for
+ *   one query head per workgroup: 2 = the key-split eight-wave kernel),
+ *   ZT_DQDS_K 1|2 (key parts of the dq-from-dS product).
  * Returns 0, or 1 (reason on stderr) for an unknown name or value.  The
  * process environment is never read.  Not synchronised with launches in
  * flight on other threads: set before launching. */

@@ -193,3 +193,42 @@ def test_forward_gate_catches_broken_references(gpu, zt, oracle):
         full[:, h * D:(h + 1) * D] = (p / p.sum(1, keepdims=True)) @ va[:, h // g]
     assert max_abs(out, full.ravel()) > FWD_TOL
     assert max_abs(out, attention_f64(qh, kh, vh, T, H, Hkv, D).ravel()) <= FWD_TOL
+
+
+@pytest.mark.parametrize("fks", ["1", "2"])
+@pytest.mark.parametrize("B,T,H,Hkv,D", [(4, 1024, 8, 8, 64), (1, 77, 3, 3, 32), (2, 130, 6, 2, 96), (1, 200, 5, 5, 128),
+                                         (1, 16, 2, 2, 64), (3, 65, 4, 4, 128)])
+def test_forward_key_split_against_twin(gpu, zt, oracle, tune, threads, fks, B, T, H, Hkv, D):
+    """The key-split forward (4 row blocks x 2 key parts, merged at the end)
+    forced on and off for one query head per workgroup -- MHA and odd
+    groups, ragged T, widths to 128 -- through zt_attn_forward and the
+    training forward's lse."""
+    tune({"ZT_ATTN_FKS": fks})
+    name = zt.plan(B, T, H, Hkv, D)[0]
+    assert name.startswith("zt_fwdpk_" if fks == "2" else "zt_fwdp_"), name
+    q, k, v = _inputs(gpu, zt, B, T, H, Hkv, D)
+    out = _run(gpu, zt, q, k, v, B, T, H, Hkv, D)
+    qh, kh, vh = host(q), host(k), host(v)
+    ref = oracle.attention_forward(qh, kh, vh, B, T, H, Hkv, D, threads=threads)
+    assert max_abs(out, ref) <= FWD_TOL
+    out2 = gpu.full((B * T * H * D,), float("nan"), device="cuda")
+    lse = gpu.full((B * T * H,), float("nan"), device="cuda")
+    zt.forward_train(q, k, v, out2, lse, T, H, Hkv, D, B=B)
+    gpu.cuda.synchronize()
+    assert max_abs(host(out2), ref) <= FWD_TOL
+    m, l, _ = oracle.attention_row_stats(qh, kh, vh, np.zeros_like(qh), B, T, H, Hkv, D)
+    want = m + np.log(l)
+    assert np.max(np.abs(host(lse) - want)) <= 1e-5 * max(1.0, np.abs(want).max())
+
+
+@pytest.mark.parametrize("T,q_offset,n_keys", [(5, 20, 25), (16, 100, 116), (70, 30, 100), (33, 0, 33), (40, 90, 130)])
+def test_forward_key_split_at_offset(gpu, zt, oracle, tune, T, q_offset, n_keys):
+    """Chunked prefill (queries at an offset over a longer key range, so the
+    second key part's first tile can lie wholly past a row) on the key-split kernel."""
+    tune({"ZT_ATTN_FKS": "2"})
+    B, H, Hkv, D = 1, 4, 4, 64
+    assert zt.plan(B, T, H, Hkv, D)[0].startswith("zt_fwdpk_")
+    q, k, v = _inputs(gpu, zt, B, T, H, Hkv, D, n_keys=n_keys)
+    out = _run(gpu, zt, q, k, v, B, T, H, Hkv, D, q_offset=q_offset, n_keys=n_keys)
+    ref = oracle.attention_forward_at(host(q), host(k), host(v), B, T, H, Hkv, D, q_offset, n_keys)
+    assert max_abs(out, ref) <= FWD_TOL

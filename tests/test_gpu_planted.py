@@ -167,7 +167,7 @@ def _train_scores(torch, zt, L, q, k, v, do):
 
 
 def test_the_planted_training_kernels_are_the_ones_the_shape_launches(gpu, zt):
-    assert zt.plan_train(TB, TT, TH, THkv, TD) == ("zt_fwd8ps_d128_k32", "zt_gemm_dqds_64", "zt_bwd_dkdv8s_d128_hs2")
+    assert zt.plan_train(TB, TT, TH, THkv, TD) == ("zt_fwd8ps_d128_k32", "zt_gemm_dqds2_64", "zt_bwd_dkdv8s_d128_hs2")
 
 
 def test_training_gate_rejects_planted_headline_kernels_with_their_own_signatures(gpu, zt, oracle, planted):

@@ -185,7 +185,9 @@ def test_train_scores_stages_and_repeats(gpu, zt, B, T, H, Hkv, D):
 def test_train_scores_plan_names_the_score_reading_kernel(gpu, zt):
     assert zt.plan_train(1, 4096, 32, 8, 128) == ("zt_fwd8ps_d128_k32", "zt_gemm_dqds_128", "zt_bwd_dkdv8s_d128_hs2")
     assert "dkdv8s" not in zt.plan_train(1, 256, 8, 8, 128)[2]   # MHA: no score-reading kernel
-    assert zt.plan_train(4, 1024, 8, 8, 64)[0] == "zt_fwdp_d64_k32"   # MHA: four waves, prefetched
+    assert zt.plan_train(4, 1024, 8, 8, 64)[2] == "zt_bwd_dkdv_dmar_d64"   # C2: S formed again, rows split
+    assert zt.plan_train(8, 1024, 8, 8, 64)[0] == "zt_fwdp_d64_k32"   # MHA: four waves, prefetched
+    assert zt.plan_train(4, 1024, 8, 8, 64)[0] == "zt_fwdpk_d64_k32"  # C2: one workgroup per CU, keys split
     assert zt.plan_train(1, 300, 4, 4, 66)[0] == "zt_fwd_d96_k32"     # rows not 16-byte chunks: no prefetch
     assert zt.plan_train(1, 256, 8, 2, 256)[2] == "zt_bwd_dkdv8sd_d256_hs2"   # wide heads: columns split
     assert zt.plan_train(1, 256, 8, 2, 192)[2] == "zt_bwd_dkdv8sd_d192_hs2"
@@ -239,7 +241,7 @@ def test_train_paired_tiles_and_128_products_at_small_shapes(gpu, zt, oracle, th
     dk/dv key tiles and the 128 x 128 dq-from-dS product -- are made by the
     shape rules only on C3/C5-sized grids; forced here on ragged small shapes
     and graded in full against the twin."""
-    tune({"ZT_ATTN_FPAIR": 1, "ZT_ATTN_BPAIR": 1, "ZT_DQDS_TILE": 128})
+    tune({"ZT_ATTN_FPAIR": 1, "ZT_ATTN_BPAIR": 1, "ZT_DQDS_TILE": 128, "ZT_DQDS_K": 1})
     assert zt.plan_train(B, T, H, Hkv, D)[1] == "zt_gemm_dqds_128"
     q, k, v, do = _inputs(gpu, zt, B, T, H, Hkv, D)
     out, lse, dq, dk, dv, delta = _train(gpu, zt, q, k, v, do, B, T, H, Hkv, D, ws=ws)
@@ -288,3 +290,36 @@ def test_stale_scores_are_refused_not_read(gpu, zt, oracle, capfd, B, T, H, Hkv,
     zt.forward_train(q, k, v, out, lse, T, H, Hkv, D, B=B)
     assert bwd(q, scores1) == 1                  # a forward that stores no scores stamps nothing
     gpu.cuda.synchronize()
+
+
+@pytest.mark.parametrize("ws", MODES, ids=MODE_IDS)
+def test_train_c2_in_full(gpu, zt, oracle, threads, ws):
+    """C2 (B=4, T=1024, 8/8 heads, d=64) graded in full on every training path
+    (the key-split forward; MHA keeps no scores, so ZT_WS_SCORES is ignored and
+    the row-split dk/dv kernel forms S again)."""
+    B, T, H, Hkv, D = 4, 1024, 8, 8, 64
+    assert zt.plan_train(B, T, H, Hkv, D) == ("zt_fwdpk_d64_k32", "zt_gemm_dqds2_64", "zt_bwd_dkdv_dmar_d64")
+    q, k, v, do = _inputs(gpu, zt, B, T, H, Hkv, D)
+    out, lse, dq, dk, dv, delta = _train(gpu, zt, q, k, v, do, B, T, H, Hkv, D, ws=ws)
+    qh, kh, vh, dh = (host(x) for x in (q, k, v, do))
+    assert max_abs(out, oracle.attention_forward(qh, kh, vh, B, T, H, Hkv, D, threads=threads)) <= FWD_TOL
+    rq, rk, rv = oracle.attention_backward(qh, kh, vh, dh, B, T, H, Hkv, D, threads=threads)
+    assert rel_err(dq, rq) <= BWD_REL
+    assert rel_err(dk, rk) <= BWD_REL
+    assert rel_err(dv, rv) <= BWD_REL
+
+
+@pytest.mark.parametrize("parts", [1, 2])
+@pytest.mark.parametrize("tile", [64, 128])
+@pytest.mark.parametrize("B,T,H,Hkv,D", [(2, 130, 8, 2, 64), (1, 333, 8, 2, 128), (1, 200, 4, 2, 256),
+                                         (1, 40, 4, 4, 96), (1, 17, 2, 2, 32)])
+def test_train_dq_product_key_parts(gpu, zt, oracle, tune, parts, tile, B, T, H, Hkv, D):
+    """The dq-from-dS product with one or two key parts (two four-wave parts
+    taking alternate key slabs, their tiles added at the end), on either tile,
+    ragged T (a part without a slab in the last step), graded in full."""
+    tune({"ZT_DQDS_K": parts, "ZT_DQDS_TILE": tile})
+    assert zt.plan_train(B, T, H, Hkv, D)[1] == (f"zt_gemm_dqds2_{tile}" if parts == 2 else f"zt_gemm_dqds_{tile}")
+    q, k, v, do = _inputs(gpu, zt, B, T, H, Hkv, D)
+    out, lse, dq, dk, dv, delta = _train(gpu, zt, q, k, v, do, B, T, H, Hkv, D, ws="ds")
+    rq, rk, rv = oracle.attention_backward(*(host(x) for x in (q, k, v, do)), B, T, H, Hkv, D)
+    assert rel_err(dq, rq) <= BWD_REL

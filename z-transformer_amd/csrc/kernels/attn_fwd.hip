@@ -21,27 +21,39 @@
 #include "args.h"
 
 
-template <int DP, int BK, int NW, bool PF>
+// KS > 1 (key split): the workgroup's waves are KS key parts x (NW / KS) row
+// blocks; a step stages KS consecutive BK-key tiles, part kh computes with
+// tile kh, each keeps its own running max, sum and output, and the parts are
+// merged through LDS at the end.  KS times the waves for the same rows: on
+// grids that give a four-wave workgroup per CU (one wave per SIMD, MHA at
+// small batch) the other waves of a SIMD cover each one's latencies.
+template <int DP, int BK, int NW, bool PF, int KS = 1>
 __device__ __forceinline__ void attn_fwd_tile(const FwdArgs &a, const int tile) {
+    static_assert(KS == 1 || PF, "the key split stages with the register prefetch");
     constexpr int LW = DP + 4;  // LDS row stride: +16 B spreads row starts over banks
     constexpr int DQ = DP / 4;  // d values per lane group
     constexpr int NT = DP / 16; // 16-wide column tiles of the output
     constexpr int NJ = BK / 16; // 16-key sub-blocks per LDS tile
     constexpr int NTH = 64 * NW;
-    __shared__ float Ks[BK * LW];
-    __shared__ float Vs[BK * LW];
+    constexpr int KBK = KS * BK;  // keys staged per step
+    constexpr int MRG_F = (KS - 1) * (NW / KS) * 64 * (4 * NT + 2);  // the key parts' merge
+    constexpr int SM_F = 2 * KBK * LW > MRG_F ? 2 * KBK * LW : MRG_F;
+    __shared__ float smem[SM_F];
+    float *const Ks = smem, *const Vs = smem + KBK * LW;
 
     const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, grp = lane >> 4;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // in a scalar register: wave-uniform branches stay scalar
-    const int RB = NW / a.HW;  // 16-row blocks per head in this workgroup
+    const int kh = w / (NW / KS);  // key part (KS > 1)
+    const int wr = w % (NW / KS);  // the wave's (head, row block) slot
+    const int RB = NW / KS / a.HW;  // 16-row blocks per head in this workgroup
     const int per_tile = a.n_head_blocks * a.B;
     const int rem = (int)blockIdx.x % per_tile;
     const int hb = rem % a.n_head_blocks, b = rem / a.n_head_blocks;
     const int group = a.H / a.Hkv;
-    const int h = hb * a.HW + (w % a.HW);
+    const int h = hb * a.HW + (wr % a.HW);
     const int kvh = ZT_PLANT == 2 ? 0 : h / group;
     const int wg_row0 = tile * 16 * RB;
-    const int row0 = wg_row0 + 16 * (w / a.HW);
+    const int row0 = wg_row0 + 16 * (wr / a.HW);
     const bool vec4 = (a.dim & 3) == 0;
     const size_t qld = (size_t)a.H * a.dim, kld = (size_t)a.Hkv * a.dim;
     const float *qb = a.q + (size_t)b * a.T * qld + (size_t)h * a.dim;
@@ -70,8 +82,8 @@ __device__ __forceinline__ void attn_fwd_tile(const FwdArgs &a, const int tile) 
     // (met by Q's zero columns, or landing in output columns never stored); the
     // host picks this kernel only for dim % 4 == 0, whose rows are 16-byte aligned.
     constexpr int CPR = DP / 4;
-    constexpr int NPF = PF ? 2 * BK * CPR / NTH : 1;
-    static_assert(!PF || (2 * BK * CPR) % NTH == 0, "prefetch split");
+    constexpr int NPF = PF ? 2 * KBK * CPR / NTH : 1;
+    static_assert(!PF || (2 * KBK * CPR) % NTH == 0, "prefetch split");
     f4 pf[NPF];
     // A thread's byte offsets within a tile's rows (rows tid / CPR + j RPN,
     // its column), fixed for the kernel: a piece is one load from the tile's
@@ -79,7 +91,7 @@ __device__ __forceinline__ void attn_fwd_tile(const FwdArgs &a, const int tile) 
     // n_keys - 1, with no per-piece address arithmetic (C3 training forward
     // 1.092 -> 1.066 ms, C5 0.563 -> 0.551 ms).
     constexpr int RPN = NTH / CPR;
-    constexpr int NOFF = PF && (BK * CPR) % NTH == 0 && BK % RPN == 0 ? BK / RPN : 1;
+    constexpr int NOFF = PF && (KBK * CPR) % NTH == 0 && KBK % RPN == 0 ? KBK / RPN : 1;
     unsigned voff[NOFF];
     const unsigned coff = (unsigned)min((tid % CPR) * 4, a.dim - 4) * 4u;
 #pragma unroll
@@ -88,14 +100,14 @@ __device__ __forceinline__ void attn_fwd_tile(const FwdArgs &a, const int tile) 
         const int e = tid + n * NTH;
         // With whole arrays per piece, the piece's array follows from n alone
         // (tid < NTH): the base stays in scalar registers.
-        const int arr = (NOFF > 1 ? n * NTH : e) / (BK * CPR);
+        const int arr = (NOFF > 1 ? n * NTH : e) / (KBK * CPR);
         if constexpr (NOFF > 1) {
             // Key n_keys - 1, counted within the tile (no 32-bit overflow however many keys).
-            const unsigned last = (unsigned)(min(a.n_keys - 1 - k0, BK - 1) * (int)kld) * 4u + coff;
-            const unsigned off = min(voff[(n * RPN % BK) / RPN], last);
+            const unsigned last = (unsigned)(min(a.n_keys - 1 - k0, KBK - 1) * (int)kld) * 4u + coff;
+            const unsigned off = min(voff[(n * RPN % KBK) / RPN], last);
             pf[n] = *reinterpret_cast<const f4 *>(reinterpret_cast<const char *>((arr ? vb : kb) + (size_t)k0 * kld) + off);
         } else {
-            const int r = min((e / CPR) % BK, a.n_keys - 1 - k0), c = min((e % CPR) * 4, a.dim - 4);
+            const int r = min((e / CPR) % KBK, a.n_keys - 1 - k0), c = min((e % CPR) * 4, a.dim - 4);
             pf[n] = *reinterpret_cast<const f4 *>((arr ? vb : kb) + (size_t)k0 * kld + (r * (int)kld + c));
         }
     };
@@ -105,15 +117,17 @@ __device__ __forceinline__ void attn_fwd_tile(const FwdArgs &a, const int tile) 
     };
     if constexpr (PF) fetch(0);
 
-    for (int k0 = 0; k0 < kend_wg; k0 += BK) {
+    for (int ks0 = 0; ks0 < kend_wg; ks0 += KBK) {
         __syncthreads();
         // The tile the prefetch loads meanwhile (the last one loads itself again, unused).
-        const int kn = k0 + BK < kend_wg ? k0 + BK : k0;
+        const int kn = ks0 + KBK < kend_wg ? ks0 + KBK : ks0;
+        // This wave's tile of the step: keys k0 .. k0 + BK - 1, its rows in LDS from kt.
+        const int k0 = ks0 + kh * BK, kt = kh * BK * LW;
         if constexpr (PF) {
 #pragma unroll
             for (int n = 0; n < NPF; ++n) {
                 const int e = tid + n * NTH;
-                const int arr = e / (BK * CPR), r = (e / CPR) % BK, c = (e % CPR) * 4;
+                const int arr = e / (KBK * CPR), r = (e / CPR) % KBK, c = (e % CPR) * 4;
                 *reinterpret_cast<f4 *>((arr ? Vs : Ks) + r * LW + c) = pf[n];
             }
             __syncthreads();
@@ -134,7 +148,7 @@ __device__ __forceinline__ void attn_fwd_tile(const FwdArgs &a, const int tile) 
         f4 s[NJ];
 #pragma unroll
         for (int j = 0; j < NJ; ++j) s[j] = zero4();
-        const float *krow = Ks + l16 * LW + grp * DQ;
+        const float *krow = Ks + kt + l16 * LW + grp * DQ;
 #pragma unroll
         for (int kk = 0; kk < DQ; kk += 4) {
 #pragma unroll
@@ -206,10 +220,14 @@ __device__ __forceinline__ void attn_fwd_tile(const FwdArgs &a, const int tile) 
 #pragma unroll
             for (int i = 0; i < NT; ++i) o[i] *= ZT_PLANT == 3 ? 1.f : corr;
         }
+        // A key part after the first (KS > 1) can meet a row whose every key so far is masked
+        // (its first tile lies past the row, with queries at an offset): the
+        // base is still -inf there, and is taken as 0 so that exp2(-inf) = 0.
+        const float mb = (KS > 1 && m == -INFINITY) ? 0.f : m;
 #pragma unroll
         for (int j = 0; j < NJ; ++j)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) s[j][r] = fast_exp2(s[j][r] - m);
+            for (int r = 0; r < 4; ++r) s[j][r] = fast_exp2(s[j][r] - mb);
         float ps = s[0][0];  // = 0 + s[0][0]: the weights are >= +0
 #pragma unroll
         for (int i = 1; i < 4 * NJ; ++i) ps += s[i / 4][i % 4];
@@ -222,13 +240,44 @@ __device__ __forceinline__ void attn_fwd_tile(const FwdArgs &a, const int tile) 
             for (int kk = 0; kk < 4; ++kk) {
                 // A operand V^T in the row-owner layout: V[key 16 j + 4 grp + kk][l16 * NT + i].
                 float vx[NT];
-                lds_run<NT>(vx, Vs + (16 * j + 4 * grp + kk) * LW, l16);
+                lds_run<NT>(vx, Vs + kt + (16 * j + 4 * grp + kk) * LW, l16);
 #pragma unroll
                 for (int i = 0; i < NT; ++i) o[i] = mfma16(vx[i], s[j][kk], o[i]);
             }
         }
     }
 
+    if constexpr (KS > 1) {
+        // Merge the key parts: parts 1.. leave their base, partial sum and
+        // output in LDS, part 0 rescales to the larger base and adds them, in
+        // part order (a part that saw no visible key has m = -inf and
+        // contributes nothing).
+        __syncthreads();  // every wave's last reads of the staged tiles
+        auto slot = [&](int part) { return smem + (((part - 1) * (NW / KS) + wr) * 64 + lane) * (4 * NT + 2); };
+        if (kh > 0) {
+            float *mb = slot(kh);
+#pragma unroll
+            for (int i = 0; i < NT; ++i) *reinterpret_cast<f4 *>(mb + 4 * i) = o[i];
+            mb[4 * NT] = m;
+            mb[4 * NT + 1] = lsum;
+        }
+        __syncthreads();
+        if (kh == 0) {
+#pragma unroll
+            for (int part = 1; part < KS; ++part) {
+                const float *mb = slot(part);
+                const float m2 = mb[4 * NT], l2 = mb[4 * NT + 1];
+                const float mm = fmaxf(m, m2);
+                const float f1 = m == -INFINITY ? 0.f : fast_exp2(m - mm);
+                const float f2 = m2 == -INFINITY ? 0.f : fast_exp2(m2 - mm);
+                lsum = lsum * f1 + l2 * f2;
+#pragma unroll
+                for (int i = 0; i < NT; ++i) o[i] = o[i] * f1 + *reinterpret_cast<const f4 *>(mb + 4 * i) * f2;
+                m = mm;
+            }
+        }
+        if (kh != 0) return;  // the merged rows are part 0's to write (no barrier follows in this tile)
+    }
     const float l = sum4grp(lsum);
     const float inv = 1.f / l;
     if (a.lse && grp == 0 && my_row < a.T)  // natural log: (m + log2 l) ln 2
@@ -242,13 +291,13 @@ __device__ __forceinline__ void attn_fwd_tile(const FwdArgs &a, const int tile) 
 
 // Row tile n - 1 - p (latest, heaviest first); with a.pair also row tile p,
 // so that every workgroup has the same causal work.
-template <int DP, int BK, int NW, bool PF>
+template <int DP, int BK, int NW, bool PF, int KS = 1>
 __device__ __forceinline__ void attn_fwd_body(const FwdArgs &a) {
     const int p = (int)blockIdx.x / (a.n_head_blocks * a.B);
-    attn_fwd_tile<DP, BK, NW, PF>(a, a.n_row_tiles - 1 - p);
+    attn_fwd_tile<DP, BK, NW, PF, KS>(a, a.n_row_tiles - 1 - p);
     if (a.pair && p < a.n_row_tiles - 1 - p) {  // workgroup-uniform
         __syncthreads();  // the first tile's last LDS reads before the second's writes
-        attn_fwd_tile<DP, BK, NW, PF>(a, p);
+        attn_fwd_tile<DP, BK, NW, PF, KS>(a, p);
     }
 }
 
@@ -275,6 +324,15 @@ __device__ __forceinline__ void attn_fwd_body(const FwdArgs &a) {
         attn_fwd_body<DP, 32, 8, true>(a);                                                         \
     }
 
+// The key-split variant for heads that share no kv group with another (HW =
+// 1) on small grids: eight waves, 4 row blocks x 2 key parts.  (Four key parts
+// in sixteen waves measured no better: C2's forward 51.3 us against 54.1 us,
+// one 16-head sequence of 2048 rows at d = 64 85.5 against 86.7 us.)
+#define ZT_FWD_PFK(DP)                                                                             \
+    extern "C" __global__ void __launch_bounds__(512) zt_fwdpk_d##DP##_k32(FwdArgs a) {          \
+        attn_fwd_body<DP, 32, 8, true, 2>(a);                                                      \
+    }
+
 #if ZT_PLANT == 0
 ZT_FWD(32, 32) ZT_FWD(32, 64)
 ZT_FWD(64, 32) ZT_FWD(64, 64)
@@ -287,6 +345,7 @@ ZT_FWD(256, 32) ZT_FWD(256, 64)
 ZT_FWD_PF(32) ZT_FWD_PF(64) ZT_FWD_PF(96) ZT_FWD_PF(128)
 ZT_FWD_PF(160) ZT_FWD_PF(192) ZT_FWD_PF(224) ZT_FWD_PF(256)
 ZT_FWD_PFS(32) ZT_FWD_PFS(64) ZT_FWD_PFS(96) ZT_FWD_PFS(128)
+ZT_FWD_PFK(32) ZT_FWD_PFK(64) ZT_FWD_PFK(96) ZT_FWD_PFK(128)
 #else
 // A planted-defect build (test-only): the kernels of the negative-control
 // shapes, d = 32 (the reference entry points) and d = 128 (the training path).

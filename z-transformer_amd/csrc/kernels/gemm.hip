@@ -301,17 +301,23 @@ DEVI void gemm_sk_body(const GemmArgs &g) {
 // Grid: row-tile pairs, then (sequence, head), then column tiles.
 // The dS and K slabs: one allocation per tile size, shared by the aligned and
 // unaligned instantiations.
-template <int BT>
+template <int BT, int KSP>
 DEVI float *dq_ds_slabs() {
-    __shared__ __attribute__((aligned(16))) float slabs[2 * BK * Tile<BT>::LIC];
+    __shared__ __attribute__((aligned(16))) float slabs[KSP * 2 * BK * Tile<BT>::LIC];
     return slabs;
 }
-template <int BT, bool VEC>
+// KSP key parts (KSP = 2: eight waves, for grids that give a workgroup of four
+// per CU): part kp of the workgroup's threads -- four waves, a whole tile --
+// takes key slabs kp, kp + KSP, ... into its own LDS slabs, and the parts'
+// tiles are added through LDS in part order at the end.
+template <int BT, bool VEC, int KSP = 1>
 DEVI void dq_ds_tile(const DqDsArgs &g, const int tm, const int tn, const int bh) {
     using TL = Tile<BT>;
     constexpr int TW = TL::TW, NCH = TL::NCH;
-    float *const As = dq_ds_slabs<BT>(), *const Bs = As + BK * TL::LIC;
-    const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, grp = lane >> 4;
+    static_assert(KSP == 1 || VEC, "the key split takes the unconditional loads");
+    const int kp = KSP > 1 ? __builtin_amdgcn_readfirstlane((int)threadIdx.x / NTHR) : 0;
+    float *const As = dq_ds_slabs<BT, KSP>() + kp * 2 * BK * TL::LIC, *const Bs = As + BK * TL::LIC;
+    const int tid = (int)threadIdx.x % NTHR, lane = tid & 63, l16 = lane & 15, grp = lane >> 4;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = TL::WT * (w >> 1), wn = TL::WT * (w & 1);
     const int b = bh / g.H, h = bh % g.H, kvh = h / (g.H / g.Hkv);
@@ -376,17 +382,26 @@ DEVI void dq_ds_tile(const DqDsArgs &g, const int tm, const int tn, const int bh
             *reinterpret_cast<f4 *>(As + sl * TL::LIC + tl) = pa[n];
         }
     };
-    fetch_a(0);
-    fetch_b(0);
-    for (int k0 = 0; k0 < kend; k0 += BK) {
+    // Step ks covers slabs ks .. ks + KSP - 1, this part's being ks + kp; a
+    // part without a slab in the last step fetches the last one again and
+    // computes nothing (every part meets every barrier).
+    const int last = ((kend - 1) / BK) * BK;
+    fetch_a(min(kp * BK, last));
+    fetch_b(min(kp * BK, last));
+    for (int ks = 0; ks < kend; ks += KSP * BK) {
+        const int k0 = ks + kp * BK;
         __syncthreads();
         put_a();
         put<BT, false>(Bs, pb, tid);
         __syncthreads();
         // The next slab (the last one fetches itself again, unused): dS
         // chunks now, K chunks between the two halves' products.
-        const int kn = k0 + BK < kend ? k0 + BK : k0;
+        const int kn = k0 + KSP * BK < kend ? k0 + KSP * BK : min(k0, last);
         if (VEC || k0 + BK < kend) fetch_a(kn);
+        if (KSP > 1 && k0 >= kend) {  // wave-uniform: this part has no slab in this step
+            fetch_b(kn);
+            continue;
+        }
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
             if (hh == 1 && (VEC || k0 + BK < kend)) fetch_b(kn);
@@ -400,6 +415,26 @@ DEVI void dq_ds_tile(const DqDsArgs &g, const int tm, const int tn, const int bh
 #pragma unroll
                     for (int j = 0; j < TW; ++j) acc[i][j] = mfma16(av[i][c], bv[j][c], acc[i][j]);
         }
+    }
+    if constexpr (KSP > 1) {
+        // The parts' tiles, added in part order by part 0 (which stores them).
+        static_assert((KSP - 1) * NTHR * TW * TW * 4 <= KSP * 2 * BK * TL::LIC, "merge buffer");
+        f4 *const red = reinterpret_cast<f4 *>(dq_ds_slabs<BT, KSP>());
+        __syncthreads();  // every part's last operand reads
+        if (kp > 0) {
+#pragma unroll
+            for (int i = 0; i < TW; ++i)
+#pragma unroll
+                for (int j = 0; j < TW; ++j) red[(((kp - 1) * TW + i) * TW + j) * NTHR + tid] = acc[i][j];
+        }
+        __syncthreads();
+        if (kp > 0) return;  // no barrier follows in this tile
+#pragma unroll
+        for (int q = 1; q < KSP; ++q)
+#pragma unroll
+            for (int i = 0; i < TW; ++i)
+#pragma unroll
+                for (int j = 0; j < TW; ++j) acc[i][j] += red[(((q - 1) * TW + i) * TW + j) * NTHR + tid];
     }
 
 #pragma unroll
@@ -420,18 +455,18 @@ DEVI void dq_ds_tile(const DqDsArgs &g, const int tm, const int tn, const int bh
 // A workgroup takes row tiles tiles_m - 1 - p and p one after the other, so
 // every workgroup has the same causal work (C3: 0.64 -> 0.58 ms against one
 // row tile per workgroup, heaviest first).
-template <int BT>
+template <int BT, int KSP = 1>
 DEVI void dq_ds_body(const DqDsArgs &g) {
     int rem = (int)blockIdx.x;
     const int tn = rem % g.tiles_n;
     rem /= g.tiles_n;
     const int bh = rem % (g.B * g.H);
     const int p = rem / (g.B * g.H);
-    if (g.vec) {
-        dq_ds_tile<BT, true>(g, g.tiles_m - 1 - p, tn, bh);
+    if (KSP > 1 || g.vec) {  // (the host takes the key-split kernels only with vec)
+        dq_ds_tile<BT, true, KSP>(g, g.tiles_m - 1 - p, tn, bh);
         if (p < g.tiles_m - 1 - p) {  // workgroup-uniform
             __syncthreads();  // the first tile's last LDS reads before the second's writes
-            dq_ds_tile<BT, true>(g, p, tn, bh);
+            dq_ds_tile<BT, true, KSP>(g, p, tn, bh);
         }
     } else {
         dq_ds_tile<BT, false>(g, g.tiles_m - 1 - p, tn, bh);
@@ -465,3 +500,6 @@ ZT_GEMM_SK(2, 32)
 
 extern "C" __global__ void __launch_bounds__(256) zt_gemm_dqds_128(DqDsArgs g) { dq_ds_body<128>(g); }
 extern "C" __global__ void __launch_bounds__(256) zt_gemm_dqds_64(DqDsArgs g) { dq_ds_body<64>(g); }
+// Two key parts, eight waves (grids of at most one four-wave workgroup per CU).
+extern "C" __global__ void __launch_bounds__(512) zt_gemm_dqds2_64(DqDsArgs g) { dq_ds_body<64, 2>(g); }
+extern "C" __global__ void __launch_bounds__(512) zt_gemm_dqds2_128(DqDsArgs g) { dq_ds_body<128, 2>(g); }

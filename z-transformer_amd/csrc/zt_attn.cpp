@@ -166,7 +166,7 @@ int launch(DeviceState *st, const char *name, unsigned blocks, const Args &args,
 enum Tune {
     kTuneBK, kTuneFwdW, kTuneFPF, kTuneFPair, kTuneQPF, kTuneDqW, kTuneHS, kTuneW8, kTunePF, kTuneDMA, kTuneBPair,
     kTuneDSplit, kTuneRSplit, kTuneDecWgs, kTuneGemmTile, kTuneGemmSk, kTuneGemmSkTile, kTuneDqdsTile, kTuneRowG,
-    kTuneRowW, kTuneCount
+    kTuneRowW, kTuneFKS, kTuneDqdsK, kTuneCount
 };
 struct TuneSpec {
     const char *name;
@@ -194,6 +194,8 @@ const TuneSpec kTuneSpecs[kTuneCount] = {
     {"ZT_DQDS_TILE", {64, 128}, 2},
     {"ZT_ROW_G", {1, 2, 4, 8}, 4},
     {"ZT_ROW_W", {4, 8}, 2},
+    {"ZT_ATTN_FKS", {1, 2}, 2},
+    {"ZT_DQDS_K", {1, 2}, 2},
 };
 std::atomic<int> g_tune[kTuneCount] = {};  // 0 = unset (no allowed value is 0 except a flag, stored as value + 1)
 
@@ -237,13 +239,30 @@ int fwd_waves(int hw) { return tuned(kTuneFwdW, hw >= 2 ? 8 : 4); }
 // MI355X: eight waves, C3 1.315 -> 1.225 ms and C5 0.758 -> 0.630 ms; four
 // waves (MHA and head groups of two), C2 0.074 -> 0.057 ms and one 16-head
 // sequence of 2048 rows at d = 128 0.30 -> 0.185 ms.
-void fwd_kernel_name(char *name, size_t len, int dim, int dp, int bk, int nw) {
+void fwd_kernel_name(char *name, size_t len, int dim, int dp, int bk, int nw, int ks = 1) {
     // The prefetching kernels load 16-byte row chunks unconditionally (dim % 4 == 0).
     const bool pf = bk == 32 && dim % 4 == 0 && tuned(kTuneFPF, 1) == 1;
-    if (pf)
+    if (pf && ks > 1)
+        snprintf(name, len, "zt_fwdpk_d%d_k32", dp);
+    else if (pf)
         snprintf(name, len, nw == 8 ? "zt_fwd8p_d%d_k32" : "zt_fwdp_d%d_k32", dp);
     else
         snprintf(name, len, nw == 8 ? "zt_fwd8_d%d_k%d" : "zt_fwd_d%d_k%d", dp, bk);
+}
+
+// Key parts of the forward: 1, or 2 for the key-split kernel (zt_fwdpk_*:
+// eight waves, 4 row blocks x 2 key parts merged at the end) for one query
+// head per workgroup (HW = 1) where the four-wave kernel's grid, after
+// pairing, gives at most one workgroup per CU: one wave per SIMD there, and
+// the split doubles it for the same rows.  Measured on MI355X (training
+// forward): C2 60.8 -> 51.3 us, one 16-head sequence of 2048 rows at d = 64
+// 104.5 -> 85.5 us, 12 heads of 1024 rows at d = 128, B = 2, 94.9 -> 89.5 us.
+// Needs the prefetching kernel (32-key tiles, dim % 4 == 0) and d <= 128.
+int fwd_key_split(int B, int T, int n_heads, int hw, int dp, int dim, int bk, int cus) {
+    const bool able = hw == 1 && dp <= 128 && bk == 32 && dim % 4 == 0 && tuned(kTuneFPF, 1) == 1;
+    const long long tiles = (T + 63) / 64;  // 64-row tiles (4 row blocks) per head
+    const long long wgs = (tiles + 1) / 2 * (long long)n_heads * B;  // paired
+    return able ? tuned(kTuneFKS, wgs <= cus ? 2 : 1) : 1;
 }
 int dq_waves(int dp) {
     const int w = tuned(kTuneDqW, 4);
@@ -454,8 +473,10 @@ int forward_impl(const float *q, const float *k, const float *v, float *out, int
     a.B = B; a.T = T; a.H = n_heads; a.Hkv = n_kv_heads; a.dim = dim;
     a.q_offset = q_offset; a.n_keys = n_keys; a.kv_rows = kv_rows;
     a.HW = heads_per_wg(n_heads / n_kv_heads);
-    const int nw = fwd_waves(a.HW);
-    const int rows_per_wg = 16 * (nw / a.HW);
+    // (Not with scores kept: no shape that keeps them has one query head per workgroup.)
+    const int ks = s_out ? 1 : fwd_key_split(B, T, n_heads, a.HW, dp, dim, bk, st->cus);
+    const int nw = ks > 1 ? 8 : fwd_waves(a.HW);
+    const int rows_per_wg = 16 * (nw / ks / a.HW);
     a.n_row_tiles = (T + rows_per_wg - 1) / rows_per_wg;
     a.n_head_blocks = n_heads / a.HW;
     a.scale_log2e = (float)(1.4426950408889634 / std::sqrt((double)dim));
@@ -468,7 +489,7 @@ int forward_impl(const float *q, const float *k, const float *v, float *out, int
         (unsigned long long)(a.pair ? (a.n_row_tiles + 1) / 2 : a.n_row_tiles) * a.n_head_blocks * B;
     if (!grid_ok(blocks, 64u * nw)) return 1;
     char name[64];
-    fwd_kernel_name(name, sizeof name, dim, dp, bk, nw);
+    fwd_kernel_name(name, sizeof name, dim, dp, bk, nw, ks);
     if (s_out && dp <= 128 && strncmp(name, "zt_fwd8p_d", 10) == 0)
         snprintf(name, sizeof name, "zt_fwd8ps_d%d_k32", dp);  // same kernel, named for its role
     return launch(st, name, (unsigned)blocks, a, stream, 64u * nw);
@@ -772,6 +793,18 @@ static int dqds_tile(int B, int T, int n_heads, int dim, int cus) {
     return tuned(kTuneDqdsTile, (dim > 64 && wgs128 >= (unsigned long long)cus) ? 128 : 64);
 }
 
+// Key parts of the dq-from-dS product: 2 (zt_gemm_dqds2_*: eight waves, two
+// four-wave parts taking alternate key slabs, their tiles added at the end)
+// where the four-wave grid gives at most one workgroup per CU (one wave per
+// SIMD), else 1.  The split kernels take 16-byte k rows (vec).
+static int dqds_parts(int B, int T, int n_heads, int dim, int bt, bool vec, int cus) {
+    const unsigned long long wgs = (unsigned long long)(((T + bt - 1) / bt + 1) / 2) * ((dim + bt - 1) / bt) * B * n_heads;
+    return vec ? tuned(kTuneDqdsK, wgs <= (unsigned long long)cus ? 2 : 1) : 1;
+}
+static void dqds_name(char *name, size_t len, int bt, int parts) {
+    snprintf(name, len, parts > 1 ? "zt_gemm_dqds2_%d" : "zt_gemm_dqds_%d", bt);
+}
+
 size_t zt_attn_backward_train_workspace(int B, int T, int n_heads, int n_kv_heads, int dim) {
     if (B < 1 || T < 1 || !zt_attn_dim_ok(dim) || n_heads <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads != 0)
         return 0;
@@ -784,7 +817,10 @@ size_t zt_attn_backward_train_workspace(int B, int T, int n_heads, int n_kv_head
 // rebuilding them, all with a two-way head split (an even head group) and
 // 16-byte row chunks (d % 4 == 0): up to d = 128 the eight-wave kernel with
 // 32 query rows per stage, above it the asynchronously staged kernel
-// (whole-head rows: d a multiple of 32).  The forward writes scores only for these.
+// (whole-head rows: d a multiple of 32).  The forward writes scores only for
+// these.  (Groups that cannot be split were measured reading them too, on the
+// row-split kernel at C2: dk/dv 101.7 -> 92.2 us, but the forward's score
+// stores 49.2 -> 56.1 us, the step 0.200 -> 0.207 ms; they form S again.)
 static bool scores_path(int dim, int n_heads, int n_kv_heads, size_t lds_limit) {
     const int dp = pad32(dim);
     if (n_kv_heads <= 0 || (n_heads / n_kv_heads) % 2 != 0 || dim % 4 != 0) return false;
@@ -967,8 +1003,11 @@ int zt_attn_backward_train_ws(const float *q, const float *k, const float *v, co
         g.tiles_m = (T + bt - 1) / bt;
         g.tiles_n = (dim + bt - 1) / bt;
         const unsigned long long blocks = (unsigned long long)((g.tiles_m + 1) / 2) * g.tiles_n * B * n_heads;
-        if (!grid_ok(blocks)) return 1;
-        if (launch(st, bt == 128 ? "zt_gemm_dqds_128" : "zt_gemm_dqds_64", (unsigned)blocks, g, stream)) return 1;
+        const int parts = dqds_parts(B, T, n_heads, dim, bt, g.vec, st->cus);
+        char name[64];
+        dqds_name(name, sizeof name, bt, parts);
+        if (!grid_ok(blocks, 256u * parts)) return 1;
+        if (launch(st, name, (unsigned)blocks, g, stream, 256u * parts)) return 1;
     }
     return 0;
 }
@@ -1314,7 +1353,8 @@ int zt_attn_plan(int B, int T, int n_heads, int n_kv_heads, int dim, int max_til
         int G = 0, nw = 0;
         one_row_plan(st, B, n_heads, n_kv_heads, dim, &G, &nw, fwd, len);
     } else {
-        fwd_kernel_name(fwd, len, dim, dp, bk, fwd_waves(heads_per_wg(n_heads / n_kv_heads)));
+        const int hw = heads_per_wg(n_heads / n_kv_heads);
+        fwd_kernel_name(fwd, len, dim, dp, bk, fwd_waves(hw), fwd_key_split(B, T, n_heads, hw, dp, dim, bk, st->cus));
     }
     BwdArgs a;
     DeviceState *st2 = nullptr;
@@ -1336,10 +1376,13 @@ int zt_attn_plan_train(int B, int T, int n_heads, int n_kv_heads, int dim, char 
     if (zt_attn_plan(B, T, n_heads, n_kv_heads, dim, 64, fwd, dq, dkdv, len)) return 1;
     DeviceState *st = device_state();
     if (!st) return 1;
-    if (T == 1)  // the training forward keeps lse, so one row still takes the forward kernel
-        fwd_kernel_name(fwd, len, dim, pad32(dim), key_tile(Tiled::Forward, pad32(dim), 64, dim),
-                        fwd_waves(heads_per_wg(n_heads / n_kv_heads)));
-    snprintf(dq, len, "zt_gemm_dqds_%d", dqds_tile(B, T, n_heads, dim, st->cus));
+    if (T == 1) {  // the training forward keeps lse, so one row still takes the forward kernel
+        const int hw = heads_per_wg(n_heads / n_kv_heads), dp = pad32(dim);
+        const int bk = key_tile(Tiled::Forward, dp, 64, dim);
+        fwd_kernel_name(fwd, len, dim, dp, bk, fwd_waves(hw), fwd_key_split(B, T, n_heads, hw, dp, dim, bk, st->cus));
+    }
+    const int bt = dqds_tile(B, T, n_heads, dim, st->cus);
+    dqds_name(dq, len, bt, dqds_parts(B, T, n_heads, dim, bt, dim % 4 == 0, st->cus));
     if (scores_path(dim, n_heads, n_kv_heads, st->lds_limit)) {
         const int dp = pad32(dim);
         snprintf(dkdv, len,
