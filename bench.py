@@ -435,6 +435,8 @@ def main():
     ap.add_argument("--cpu-rows", type=int, default=48, help="query rows of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-other", action="store_true", help="skip the C2 / C5 figures (profiling runs)")
+    ap.add_argument("--no-views", action="store_true",
+                    help="skip the reference-shape, sync / end-to-end and seam views (profiling runs)")
     ap.add_argument("--only-other", action="store_true",
                     help="run the C2 / C5 section alone and print its figures (profiling runs)")
     args = ap.parse_args()
@@ -784,12 +786,14 @@ def main():
     del src, dst
 
     # ---------------- The reference's own views: same shapes, sync and end-to-end ----------------
-    norm_sync_e2e = norm_views(torch, zt, dev)
-    ref_shapes = reference_shape_rows(torch, zt, dev)
-    seams = {"GPT-mini T=256 Hq=4 Hkv=2 d=32": seam_e2e(torch, zt, dev, 256, 4, 2, 32, 50),
-             "C3 T=4096 Hq=32 Hkv=8 d=128": seam_e2e(torch, zt, dev, 4096, 32, 8, 128, 5)}
-    for tag, r in seams.items():
-        log(f"seams {tag}: {r}")
+    norm_sync_e2e = ref_shapes = seams = None
+    if not args.no_views:
+        norm_sync_e2e = norm_views(torch, zt, dev)
+        ref_shapes = reference_shape_rows(torch, zt, dev)
+        seams = {"GPT-mini T=256 Hq=4 Hkv=2 d=32": seam_e2e(torch, zt, dev, 256, 4, 2, 32, 50),
+                 "C3 T=4096 Hq=32 Hkv=8 d=128": seam_e2e(torch, zt, dev, 4096, 32, 8, 128, 5)}
+        for tag, r in seams.items():
+            log(f"seams {tag}: {r}")
 
     # ---------------- CPU baseline: the restatement on a bounded sample ----------------
     cpu = None
