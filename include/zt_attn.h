@@ -231,10 +231,13 @@ int zt_attn_backward_train_ws(const float *q, const float *k, const float *v, co
 /* zt_attn_forward_train that also leaves the scaled scores q k log2(e)/sqrt(d)
  * of every causal 16 x 16 tile in the workspace's dS tiles, for
  * zt_attn_backward_train_ws(..., stage | ZT_WS_SCORES, ...).  Scores are kept
- * for the shapes whose dk/dv kernel reads them (an even number of query heads
- * per kv head, and head_dim <= 128 or a multiple of 32); for the others this
- * is zt_attn_forward_train and ZT_WS_SCORES is ignored (so it is for a wide
- * head whose q or dout rows are not 16-byte aligned).  The workspace is the
+ * for the shapes whose dk/dv kernel reads them: an even number of query heads
+ * per kv head with head_dim % 4 == 0 and head_dim <= 128 or a multiple of 32;
+ * and head groups that cannot be halved (MHA, odd groups) with head_dim 32,
+ * 64, 96 or 128 where the grid gives at most one paired dk/dv workgroup per
+ * CU (the row-split kernel's shapes).  For the others this is
+ * zt_attn_forward_train and ZT_WS_SCORES is ignored (so it is for q or dout
+ * rows that are not 16-byte aligned).  The workspace is the
  * backward's (zt_attn_backward_train_workspace bytes).  No reference
  * counterpart. */
 int zt_attn_forward_train_ws(const float *q, const float *k, const float *v, float *out, float *lse, void *workspace,
@@ -330,7 +333,10 @@ int zt_attn_plan(int B, int T, int n_heads, int n_kv_heads, int dim, int max_til
  *   1|2|4|8 and ZT_ROW_W 4|8 (query heads and waves per workgroup of the
  *   one-row forward, T = 1), ZT_ATTN_FKS 1|2 (key parts of the forward for
  *   one query head per workgroup: 2 = the key-split eight-wave kernel),
- *   ZT_DQDS_K 1|2 (key parts of the dq-from-dS product).
+ *   ZT_DQDS_K 1|2 (key parts of the dq-from-dS product), ZT_ATTN_RSCORES
+ *   0|1 (the row-split dk/dv kernel reading the forward's scores for head
+ *   groups that cannot be halved; 0 = it forms S again and the forward keeps
+ *   none).
  * Returns 0, or 1 (reason on stderr) for an unknown name or value.  The
  * process environment is never read.  Not synchronised with launches in
  * flight on other threads: set before launching. */

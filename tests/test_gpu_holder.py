@@ -214,8 +214,8 @@ def test_holder_buffer_pointer_drops_the_saved_state_and_the_read_only_one_keeps
 def test_holder_decode_seam_at_the_c4_sequence_shape(gpu, zt, oracle, threads):
     """decode.zig:462's call on one C4 sequence (8192 cached keys, 32 / 8 heads,
     d = 128) through the holder, which splits the keys over the device with
-    its own chunk partials: against the twin at the full cache and at a
-    partly filled one, and equal to zt_attn_decode bit for bit."""
+    its own chunk partials: against the twin at the full cache and at partly
+    filled ones, and equal to zt_attn_decode bit for bit, call after call."""
     n_ctx, H, Hkv, D = 8192, 32, 8, 128
     p = _holder(zt, n_ctx, H, Hkv, D)
     L = zt.lib()
@@ -228,7 +228,7 @@ def test_holder_decode_seam_at_the_c4_sequence_shape(gpu, zt, oracle, threads):
         qh = _down(zt, p, zt.ZT_BUF_Q, H * D)
         kc = _down(zt, p, zt.ZT_BUF_K, n_ctx * Hkv * D)
         vc = _down(zt, p, zt.ZT_BUF_V, n_ctx * Hkv * D)
-        for n_keys in (n_ctx, 5000, 1):
+        for n_keys in (n_ctx, 5000, 1, 129, n_ctx):
             assert L.zt_holder_forward_at(p, 1, 64, n_keys - 1, n_keys, 1) == 0
             out = _down(zt, p, zt.ZT_BUF_OUT, H * D)
             ref = oracle.attn_step(qh, kc, vc, [n_keys], 1, n_ctx, H, Hkv, D, threads=threads)

@@ -155,7 +155,8 @@ def test_train_ws_stages_and_repeats(gpu, zt):
 
 
 @pytest.mark.parametrize("B,T,H,Hkv,D", [(2, 130, 8, 2, 64), (1, 333, 8, 2, 128), (1, 45, 4, 2, 66),
-                                         (2, 77, 8, 2, 256), (1, 100, 4, 2, 160), (1, 90, 8, 2, 192)])
+                                         (2, 77, 8, 2, 256), (1, 100, 4, 2, 160), (1, 90, 8, 2, 192),
+                                         (1, 333, 4, 4, 64), (2, 200, 6, 2, 128)])
 def test_train_scores_stages_and_repeats(gpu, zt, B, T, H, Hkv, D):
     """The forward that keeps its scores gives the same out and lse bit for bit;
     the backward that reads them back repeats bit for bit, its stages equal the
@@ -185,7 +186,8 @@ def test_train_scores_stages_and_repeats(gpu, zt, B, T, H, Hkv, D):
 def test_train_scores_plan_names_the_score_reading_kernel(gpu, zt):
     assert zt.plan_train(1, 4096, 32, 8, 128) == ("zt_fwd8ps_d128_k32", "zt_gemm_dqds_128", "zt_bwd_dkdv8s_d128_hs2")
     assert "dkdv8s" not in zt.plan_train(1, 256, 8, 8, 128)[2]   # MHA: no score-reading kernel
-    assert zt.plan_train(4, 1024, 8, 8, 64)[2] == "zt_bwd_dkdv_dmar_d64"   # C2: S formed again, rows split
+    assert zt.plan_train(4, 1024, 8, 8, 64)[2] == "zt_bwd_dkdv_dmars_d64"  # C2: the scores read back, rows split
+    assert zt.plan_train(8, 1024, 8, 8, 64)[2] == "zt_bwd_dkdv8pd_d64_hs1"  # past one workgroup per CU: S formed again
     assert zt.plan_train(8, 1024, 8, 8, 64)[0] == "zt_fwdp_d64_k32"   # MHA: four waves, prefetched
     assert zt.plan_train(4, 1024, 8, 8, 64)[0] == "zt_fwdpk_d64_k32"  # C2: one workgroup per CU, keys split
     assert zt.plan_train(1, 300, 4, 4, 66)[0] == "zt_fwd_d96_k32"     # rows not 16-byte chunks: no prefetch
@@ -193,6 +195,28 @@ def test_train_scores_plan_names_the_score_reading_kernel(gpu, zt):
     assert zt.plan_train(1, 256, 8, 2, 192)[2] == "zt_bwd_dkdv8sd_d192_hs2"
     assert zt.plan_train(1, 256, 8, 2, 160)[2] == "zt_bwd_dkdv_dmas_d160_hs2"   # halves not whole 32 columns
     assert "dmas" not in zt.plan_train(1, 256, 8, 2, 250)[2]   # rows not whole 32-float chunks: no scores
+
+
+@pytest.mark.parametrize("B,T,H,Hkv,D", [(1, 333, 4, 4, 32), (2, 130, 8, 8, 64), (1, 200, 6, 2, 96),
+                                         (1, 150, 3, 1, 128), (1, 16, 2, 2, 64)])
+def test_train_row_split_kernel_reads_the_scores(gpu, zt, oracle, tune, B, T, H, Hkv, D):
+    """Head groups that cannot be halved (MHA, odd groups) on small grids: the
+    row-split dk/dv kernel reading the forward's scores and the same kernel
+    forming S again (ZT_ATTN_RSCORES=0) give dq, dk, dv equal to rounding and
+    both hold the oracle's gate; out and lse are bit-identical."""
+    q, k, v, do = _inputs(gpu, zt, B, T, H, Hkv, D)
+    dp = (D + 31) // 32 * 32
+    assert zt.plan_train(B, T, H, Hkv, D)[2] == f"zt_bwd_dkdv_dmars_d{dp}"
+    a = _train(gpu, zt, q, k, v, do, B, T, H, Hkv, D, ws="scores")
+    tune({"ZT_ATTN_RSCORES": 0})
+    assert zt.plan_train(B, T, H, Hkv, D)[2] == f"zt_bwd_dkdv_dmar_d{dp}"
+    b = _train(gpu, zt, q, k, v, do, B, T, H, Hkv, D, ws="scores")
+    for x, y in zip(a[:2], b[:2]):
+        assert np.array_equal(x.view(np.uint32), y.view(np.uint32))
+    for x, y in zip(a[2:5], b[2:5]):
+        assert rel_err(x, y) <= 1e-5
+    rq, rk, rv = oracle.attention_backward(*(host(x) for x in (q, k, v, do)), B, T, H, Hkv, D)
+    assert max(rel_err(a[2], rq), rel_err(a[3], rk), rel_err(a[4], rv)) <= BWD_REL
 
 
 @pytest.mark.parametrize("B,T,H,Hkv,D", [(2, 77, 8, 2, 256), (1, 90, 8, 2, 192)])
@@ -213,7 +237,8 @@ def test_train_scores_wide_kernels_agree(gpu, zt, oracle, tune, B, T, H, Hkv, D)
 
 
 @pytest.mark.parametrize("B,T,H,Hkv,D", [(1, 100, 8, 2, 80), (2, 45, 4, 2, 32), (1, 333, 8, 2, 128),
-                                         (1, 70, 8, 2, 256), (1, 61, 8, 2, 192)])
+                                         (1, 70, 8, 2, 256), (1, 61, 8, 2, 192), (1, 333, 4, 4, 64),
+                                         (1, 100, 6, 2, 96)])
 def test_train_scores_write_nothing_past_the_workspace(gpu, zt, oracle, B, T, H, Hkv, D):
     """Ragged T: the score-reading dk/dv kernel stages 32 rows, so a stage can
     end past the last row; no score or dS tile may be written outside the
@@ -295,10 +320,10 @@ def test_stale_scores_are_refused_not_read(gpu, zt, oracle, capfd, B, T, H, Hkv,
 @pytest.mark.parametrize("ws", MODES, ids=MODE_IDS)
 def test_train_c2_in_full(gpu, zt, oracle, threads, ws):
     """C2 (B=4, T=1024, 8/8 heads, d=64) graded in full on every training path
-    (the key-split forward; MHA keeps no scores, so ZT_WS_SCORES is ignored and
-    the row-split dk/dv kernel forms S again)."""
+    (the key-split forward; with ZT_WS_SCORES it keeps its scores and the
+    row-split dk/dv kernel reads them back instead of forming S again)."""
     B, T, H, Hkv, D = 4, 1024, 8, 8, 64
-    assert zt.plan_train(B, T, H, Hkv, D) == ("zt_fwdpk_d64_k32", "zt_gemm_dqds2_64", "zt_bwd_dkdv_dmar_d64")
+    assert zt.plan_train(B, T, H, Hkv, D) == ("zt_fwdpk_d64_k32", "zt_gemm_dqds2_64", "zt_bwd_dkdv_dmars_d64")
     q, k, v, do = _inputs(gpu, zt, B, T, H, Hkv, D)
     out, lse, dq, dk, dv, delta = _train(gpu, zt, q, k, v, do, B, T, H, Hkv, D, ws=ws)
     qh, kh, vh, dh = (host(x) for x in (q, k, v, do))

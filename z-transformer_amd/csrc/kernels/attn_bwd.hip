@@ -971,7 +971,7 @@ __device__ __forceinline__ void bwd_dkdv_tile(const BwdArgs &a, const int ktile,
 // are summed as the head halves' are.
 template <int DP, int HS, bool SIN = false, bool RS = false>
 __device__ __forceinline__ void bwd_dkdv_dma_tile(const BwdArgs &a, const int ktile) {
-    static_assert(!RS || (HS == 2 && !SIN), "row split: two parts, statistics path");
+    static_assert(!RS || HS == 2, "row split: two parts");
     constexpr int DQ = DP / 4, NT = DP / 16, KW = RS ? 4 : 4 / HS, BQ = 16, NW = KW * HS;
     constexpr int CPR = DP / 4;          // 16-byte chunks per row
     constexpr int TILE = BQ * DP;        // floats per (part, array) tile
@@ -1354,6 +1354,13 @@ ZT_BWD_DKDV(128, 4)
         bwd_dkdv_dma_body<DP, 2, false, true>(a);                                                  \
     }
 ZT_BWD_DKDV_DMAR(32) ZT_BWD_DKDV_DMAR(64) ZT_BWD_DKDV_DMAR(96) ZT_BWD_DKDV_DMAR(128)
+// The same reading the forward's scores: each part's wave loads its own
+// row tile's score tile and writes dS over it.
+#define ZT_BWD_DKDV_DMARS(DP)                                                                      \
+    extern "C" __global__ void __launch_bounds__(512) zt_bwd_dkdv_dmars_d##DP(BwdArgs a) {       \
+        bwd_dkdv_dma_body<DP, 2, true, true>(a);                                                   \
+    }
+ZT_BWD_DKDV_DMARS(32) ZT_BWD_DKDV_DMARS(64) ZT_BWD_DKDV_DMARS(96) ZT_BWD_DKDV_DMARS(128)
 ZT_BWD_DKDV_DMA(32, 4)
 ZT_BWD_DKDV_DMA(64, 4)
 ZT_BWD_DKDV_DMA(96, 4)

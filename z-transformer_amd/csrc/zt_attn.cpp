@@ -166,7 +166,7 @@ int launch(DeviceState *st, const char *name, unsigned blocks, const Args &args,
 enum Tune {
     kTuneBK, kTuneFwdW, kTuneFPF, kTuneFPair, kTuneQPF, kTuneDqW, kTuneHS, kTuneW8, kTunePF, kTuneDMA, kTuneBPair,
     kTuneDSplit, kTuneRSplit, kTuneDecWgs, kTuneGemmTile, kTuneGemmSk, kTuneGemmSkTile, kTuneDqdsTile, kTuneRowG,
-    kTuneRowW, kTuneFKS, kTuneDqdsK, kTuneCount
+    kTuneRowW, kTuneFKS, kTuneDqdsK, kTuneRScores, kTuneCount
 };
 struct TuneSpec {
     const char *name;
@@ -196,6 +196,7 @@ const TuneSpec kTuneSpecs[kTuneCount] = {
     {"ZT_ROW_W", {4, 8}, 2},
     {"ZT_ATTN_FKS", {1, 2}, 2},
     {"ZT_DQDS_K", {1, 2}, 2},
+    {"ZT_ATTN_RSCORES", {0, 1}, 2},
 };
 std::atomic<int> g_tune[kTuneCount] = {};  // 0 = unset (no allowed value is 0 except a flag, stored as value + 1)
 
@@ -473,8 +474,7 @@ int forward_impl(const float *q, const float *k, const float *v, float *out, int
     a.B = B; a.T = T; a.H = n_heads; a.Hkv = n_kv_heads; a.dim = dim;
     a.q_offset = q_offset; a.n_keys = n_keys; a.kv_rows = kv_rows;
     a.HW = heads_per_wg(n_heads / n_kv_heads);
-    // (Not with scores kept: no shape that keeps them has one query head per workgroup.)
-    const int ks = s_out ? 1 : fwd_key_split(B, T, n_heads, a.HW, dp, dim, bk, st->cus);
+    const int ks = fwd_key_split(B, T, n_heads, a.HW, dp, dim, bk, st->cus);
     const int nw = ks > 1 ? 8 : fwd_waves(a.HW);
     const int rows_per_wg = 16 * (nw / ks / a.HW);
     a.n_row_tiles = (T + rows_per_wg - 1) / rows_per_wg;
@@ -813,18 +813,38 @@ size_t zt_attn_backward_train_workspace(int B, int T, int n_heads, int n_kv_head
            (size_t)B * n_heads * (size_t)zt_tri_count(nt) * 256 * sizeof(float);
 }
 
-// Shapes whose dk/dv kernel can take the forward's scores instead of
-// rebuilding them, all with a two-way head split (an even head group) and
-// 16-byte row chunks (d % 4 == 0): up to d = 128 the eight-wave kernel with
-// 32 query rows per stage, above it the asynchronously staged kernel
-// (whole-head rows: d a multiple of 32).  The forward writes scores only for
-// these.  (Groups that cannot be split were measured reading them too, on the
-// row-split kernel at C2: dk/dv 101.7 -> 92.2 us, but the forward's score
-// stores 49.2 -> 56.1 us, the step 0.200 -> 0.207 ms; they form S again.)
-static bool scores_path(int dim, int n_heads, int n_kv_heads, size_t lds_limit) {
+// Which dk/dv kernel takes the forward's scores instead of rebuilding them,
+// if any.  Split: an even head group (two-way head split) with 16-byte row
+// chunks (d % 4 == 0): up to d = 128 the eight-wave kernel with 32 query rows
+// per stage, above it the asynchronously staged kernel (whole-head rows: d a
+// multiple of 32).  RowSplit: a group that cannot be halved (MHA, odd groups)
+// where the statistics path takes the row-split asynchronously staged kernel
+// (whole-head rows up to d = 128, at most one paired workgroup per CU): the
+// same kernel reading the scores (ZT_ATTN_RSCORES=0 keeps it forming S
+// again).  Measured on MI355X (training step, scores against none): C2
+// 179.6 -> 171.8-177.9 us, one 16-head MHA sequence of 2048 rows at d = 128
+// 582 -> 530 us, B = 2, T = 1024, 12 over 4 heads at d = 64 320 -> 291 us,
+// one 8-head sequence of 1024 rows at d = 96 217 -> 202 us; the forward pays
+// 4-5 us for its score stores at each.  The forward writes scores only for
+// these.
+enum class ScoreKernel { None, Split, RowSplit };
+static ScoreKernel score_kernel(int B, int T, int dim, int n_heads, int n_kv_heads, const DeviceState *st) {
     const int dp = pad32(dim);
-    if (n_kv_heads <= 0 || (n_heads / n_kv_heads) % 2 != 0 || dim % 4 != 0) return false;
-    return dp <= 128 ? dkdv_bytes(dp, 2, 4, 32, 2) <= lds_limit : dim == dp && dkdv_dma_bytes(dp, 2) <= lds_limit;
+    if (n_kv_heads <= 0 || n_heads % n_kv_heads != 0 || dim % 4 != 0) return ScoreKernel::None;
+    if ((n_heads / n_kv_heads) % 2 == 0) {
+        const bool fits = dp <= 128 ? dkdv_bytes(dp, 2, 4, 32, 2) <= st->lds_limit
+                                    : dim == dp && dkdv_dma_bytes(dp, 2) <= st->lds_limit;
+        return fits ? ScoreKernel::Split : ScoreKernel::None;
+    }
+    // The statistics path's choice for this shape (backward_prepare, HS = 1).
+    const unsigned long long tiles = (unsigned long long)(T + 63) / 64;
+    const bool dma_pays = (tiles + 1) / 2 * n_kv_heads * B <= (unsigned long long)st->cus;
+    const bool rsplit = dim == dp && dp <= 128 && dkdv_dma_bytes(dp, 2) <= st->lds_limit &&
+                        tuned(kTuneDMA, dma_pays ? 1 : 0) == 1 && tuned(kTuneRSplit, 1) == 1;
+    return rsplit && tuned(kTuneRScores, 1) == 1 ? ScoreKernel::RowSplit : ScoreKernel::None;
+}
+static bool scores_path(int B, int T, int dim, int n_heads, int n_kv_heads, const DeviceState *st) {
+    return score_kernel(B, T, dim, n_heads, n_kv_heads, st) != ScoreKernel::None;
 }
 
 static float *ws_tiles(void *workspace, int B, int T, int n_heads) {
@@ -905,7 +925,7 @@ int zt_attn_forward_train_ws(const float *q, const float *k, const float *v, flo
     }
     if (need != 0 && !workspace_aligned(workspace, "forward_train_ws")) return 1;
     DeviceState *st = need ? device_state() : nullptr;
-    float *s_out = (st && scores_path(dim, n_heads, n_kv_heads, st->lds_limit)) ? ws_tiles(workspace, B, T, n_heads)
+    float *s_out = (st && scores_path(B, T, dim, n_heads, n_kv_heads, st)) ? ws_tiles(workspace, B, T, n_heads)
                                                                                 : nullptr;
     const int rc = forward_impl(q, k, v, out, B, T, n_heads, n_kv_heads, dim, 1, 64, 0, T, T, stream, lse, s_out);
     // (A refused call wrote nothing, so whatever stamp the workspace had still holds.)
@@ -954,8 +974,10 @@ int zt_attn_backward_train_ws(const float *q, const float *k, const float *v, co
     a.ds_out = ds;
     const int dp = pad32(dim);
     const bool qd_aligned = (uintptr_t)q % 16 == 0 && (uintptr_t)dout % 16 == 0;
-    const bool read_scores = scores && (stage & 1) && scores_path(dim, n_heads, n_kv_heads, st->lds_limit) &&
-                             qd_aligned;
+    const ScoreKernel sk = score_kernel(B, T, dim, n_heads, n_kv_heads, st);
+    // (RowSplit reads them on the grid backward_prepare sized for the row-split kernel.)
+    const bool read_scores = scores && (stage & 1) && sk != ScoreKernel::None && qd_aligned &&
+                             (sk != ScoreKernel::RowSplit || strncmp(name_b, "zt_bwd_dkdv_dmar_d", 18) == 0);
     if (read_scores &&
         !stamp_take(ScoreStamp{current_device(), workspace, q, k, B, T, n_heads, n_kv_heads, dim})) {
         fprintf(stderr,
@@ -964,7 +986,11 @@ int zt_attn_backward_train_ws(const float *q, const float *k, const float *v, co
                 "       Refusing rather than reading stale tiles: run the forward again, or drop ZT_WS_SCORES.\n");
         return 1;
     }
-    if (read_scores) {
+    if (read_scores && sk == ScoreKernel::RowSplit) {
+        // The row-split kernel the statistics path chose (backward_prepare
+        // set its grid), reading the scores instead of forming Q K^T.
+        snprintf(name_b, sizeof name_b, "zt_bwd_dkdv_dmars_d%d", dp);
+    } else if (read_scores) {
         // The forward left the scores in the dS tiles: a kernel that reads
         // them, 2 head halves x 64 keys (eight waves, d <= 128) or x 32 keys
         // (wider heads: eight waves splitting the columns, or four waves with
@@ -1383,7 +1409,10 @@ int zt_attn_plan_train(int B, int T, int n_heads, int n_kv_heads, int dim, char 
     }
     const int bt = dqds_tile(B, T, n_heads, dim, st->cus);
     dqds_name(dq, len, bt, dqds_parts(B, T, n_heads, dim, bt, dim % 4 == 0, st->cus));
-    if (scores_path(dim, n_heads, n_kv_heads, st->lds_limit)) {
+    const ScoreKernel sk = score_kernel(B, T, dim, n_heads, n_kv_heads, st);
+    if (sk == ScoreKernel::RowSplit) {
+        snprintf(dkdv, len, "zt_bwd_dkdv_dmars_d%d", pad32(dim));
+    } else if (sk == ScoreKernel::Split) {
         const int dp = pad32(dim);
         snprintf(dkdv, len,
                  dp <= 128                        ? "zt_bwd_dkdv8s_d%d_hs2"
