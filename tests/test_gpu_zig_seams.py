@@ -16,7 +16,8 @@ zt_holder_backward), and the three callers mirror their Zig:
     n_keys - 1, n_keys, 1); download the output row.
 Graded against the CPU restatement with the north_star gates: C1 in full (two
 layers through one cached holder, and a filling cache), and one whole kv group
-of C3 (RoPE'd) after a first call on other inputs."""
+of C3 (RoPE'd) after a first call on other inputs; and model.zig's
+deliberate-corruption control (ATTN_CORRUPT_KEY), which the gate must reject."""
 import ctypes
 
 import numpy as np
@@ -118,9 +119,16 @@ class AutogradDevice:
         self.bwd_dev = None
 
 
-def cuda_forward(a, q, k, v, H, D):
+def cuda_forward(a, q, k, v, H, D, corrupt_key=None):
+    """model.cudaForward; corrupt_key is its ATTN_CORRUPT_KEY (model.zig:452-499):
+    an offset added to the first element of the uploaded keys only."""
     a.upload(a.q, q)
-    a.upload(a.k, k)
+    if corrupt_key:
+        damaged = np.array(k, np.float32, copy=True)
+        damaged[0] += corrupt_key
+        a.upload(a.k, damaged)
+    else:
+        a.upload(a.k, k)
     a.upload(a.v, v)
     a.forward(1, 64)
     out = np.empty(q.size, np.float32)
@@ -188,6 +196,32 @@ def test_seams_at_c1(gpu, zt, oracle):
     finally:
         fwd.deinit()
         auto.deinit()
+
+
+def test_the_model_seam_gate_rejects_a_corrupted_key(gpu, zt, oracle):
+    """model.zig's deliberate-corruption control (ATTN_CORRUPT_KEY=0.05 makes
+    `zig build cuda-attn-check` exit 1): one uploaded key element moved by 0.05
+    on the device side only must fail the forward gate against the clean twin,
+    and only in kv head 0's query heads; the clean upload through the same
+    holder passes it again afterwards."""
+    L = zt.lib()
+    T, H, Hkv, D = 128, 4, 2, 32
+    rng = np.random.default_rng(0xBAD)
+    q, k, v, _ = _host_inputs(rng, T, H, Hkv, D)
+    ref = oracle.attention_forward(q, k, v, 1, T, H, Hkv, D)
+    a = ZigAttn(L, T, H, Hkv, D)
+    try:
+        clean = cuda_forward(a, q, k, v, H, D)
+        assert max_abs(clean, ref) <= FWD_TOL
+        bad = cuda_forward(a, q, k, v, H, D, corrupt_key=0.05)
+        assert max_abs(bad, ref) > FWD_TOL               # the gate fails
+        moved = (bad != clean).reshape(T, H, D)
+        assert not moved[:, H // Hkv:].any()             # kv head 1's query heads never read kv head 0's keys
+        assert not moved[0].any()                        # row 0 sees key 0 alone: its weight stays 1
+        again = cuda_forward(a, q, k, v, H, D)
+        assert np.array_equal(again.view(np.uint32), clean.view(np.uint32))
+    finally:
+        a.deinit()
 
 
 def test_device_backward_seam_on_a_c3_kv_group(gpu, zt, oracle, threads):
