@@ -402,7 +402,7 @@ def other_configs(torch, zt, dev, args, normal, scores):
         # when it reads the forward's scores) and the dq product.
         unit_o = flop_o / 7
         n_fwd, n_dq, n_dkdv = zt.plan_train(Bo, To, Ho, Hkvo, Do)
-        reads_scores = "dkdv8s" in n_dkdv or "dkdv_dmas" in n_dkdv
+        reads_scores = any(t in n_dkdv for t in ("dkdv8s", "dkdv_dmas", "dkdv_dmars"))
         fwd_o = lambda: zt.forward_train_ws(qo, ko, vo, oo, lseo, wo, To, Ho, Hkvo, Do, B=Bo)
         st1 = 1 | (zt.ZT_WS_SCORES if reads_scores else 0)
         dkdv_o = lambda: zt.backward_train_ws(qo, ko, vo, oo, do_, lseo, dqo, dko, dvo, wo, To, Ho, Hkvo, Do, B=Bo,
