@@ -156,6 +156,25 @@ def test_backward_full_size(gpu, zt, oracle, threads, cfg):
     assert rel_err(dq.reshape(qs)[:, :W], rq.reshape(qs)[:, :W]) <= BWD_REL
 
 
+@pytest.mark.parametrize("B,T,H,Hkv,D", [(1, 32768, 2, 1, 64), (1, 20000, 4, 4, 128)])
+def test_backward_long_sequences(gpu, zt, oracle, threads, B, T, H, Hkv, D):
+    """The reference entry point's backward at 5-8x C3's length (2^29 causal
+    pairs per head at T = 32768): invariants at full size, the last and first
+    rows against the twin."""
+    W = 64
+    (q, k, v, do), (dq, dk, dv, *_) = _run(gpu, zt, B, T, H, Hkv, D)
+    for g in (dq, dk, dv):
+        assert np.all(np.isfinite(g))
+    _invariants(dk, dv, do, B, T, H, Hkv, D)
+    qs, ks = (B, T, H * D), (B, T, Hkv * D)
+    rq, rk, rv = oracle.attention_backward(q, k, v, do, B, T, H, Hkv, D, t_begin=T - W, threads=threads)
+    assert rel_err(dq.reshape(qs)[:, T - W:], rq.reshape(qs)[:, T - W:]) <= BWD_REL
+    assert rel_err(dk.reshape(ks)[:, T - W:], rk.reshape(ks)[:, T - W:]) <= BWD_REL
+    assert rel_err(dv.reshape(ks)[:, T - W:], rv.reshape(ks)[:, T - W:]) <= BWD_REL
+    rq, _, _ = oracle.attention_backward(q, k, v, do, B, T, H, Hkv, D, t_begin=0, t_end=W, threads=threads)
+    assert rel_err(dq.reshape(qs)[:, :W], rq.reshape(qs)[:, :W]) <= BWD_REL
+
+
 def test_backward_is_deterministic(gpu, zt):
     B, T, H, Hkv, D = 1, 300, 8, 2, 128
     _, a = _run(gpu, zt, B, T, H, Hkv, D)

@@ -106,6 +106,38 @@ def test_train_path_full_size(gpu, zt, oracle, threads, cfg, ws):
     assert max_abs(out.reshape(qs)[:, T - W:], ro.reshape(qs)[:, T - W:]) <= FWD_TOL
 
 
+@pytest.mark.parametrize("ws", [False, "scores"], ids=["dq-kernel", "scores"])
+@pytest.mark.parametrize("B,T,H,Hkv,D", [(1, 32768, 2, 1, 64), (1, 32768, 1, 1, 64), (1, 20000, 4, 4, 128)])
+def test_train_path_long_sequences(gpu, zt, oracle, threads, B, T, H, Hkv, D, ws):
+    """Sequences 5-8x C3's length, where score / dS tile offsets in the
+    workspace run past 2^31 bytes (4.3 GB of tiles at T = 32768 with two
+    heads, 2.1 GB with one): every
+    path's kernels (the score-reading head-split and row-split dk/dv kernels,
+    and the column-split one past one workgroup per CU) against the twin on
+    the first and last rows, plus the full-size column-sum invariants."""
+    W = 64
+    q, k, v, do = _inputs(gpu, zt, B, T, H, Hkv, D)
+    out, lse, dq, dk, dv, delta = _train(gpu, zt, q, k, v, do, B, T, H, Hkv, D, ws=ws)
+    for g in (out, lse, dq, dk, dv):
+        assert np.all(np.isfinite(g))
+    qh, kh, vh, dh = (host(x) for x in (q, k, v, do))
+    qs, ks = (B, T, H * D), (B, T, Hkv * D)
+    dk4 = dk.reshape(B, T, Hkv, D).astype(np.float64)
+    dv4 = dv.reshape(B, T, Hkv, D).astype(np.float64)
+    want = dh.reshape(B, T, Hkv, H // Hkv, D).astype(np.float64).sum(axis=(1, 3))
+    assert np.max(np.abs(dk4.sum(1))) <= 1e-3 * np.abs(dk4).sum(1).max()
+    assert np.max(np.abs(dv4.sum(1) - want)) <= 1e-3 * np.abs(want).max()
+    rq, rk, rv = oracle.attention_backward(qh, kh, vh, dh, B, T, H, Hkv, D, t_begin=T - W, threads=threads)
+    assert rel_err(dq.reshape(qs)[:, T - W:], rq.reshape(qs)[:, T - W:]) <= BWD_REL
+    assert rel_err(dk.reshape(ks)[:, T - W:], rk.reshape(ks)[:, T - W:]) <= BWD_REL
+    assert rel_err(dv.reshape(ks)[:, T - W:], rv.reshape(ks)[:, T - W:]) <= BWD_REL
+    rq, _, _ = oracle.attention_backward(qh, kh, vh, dh, B, T, H, Hkv, D, t_begin=0, t_end=W, threads=threads)
+    assert rel_err(dq.reshape(qs)[:, :W], rq.reshape(qs)[:, :W]) <= BWD_REL
+    for t0 in (0, T // 2, T - W):
+        ro = oracle.attention_forward(qh, kh, vh, B, T, H, Hkv, D, t_begin=t0, t_end=t0 + W, threads=threads)
+        assert max_abs(out.reshape(qs)[:, t0:t0 + W], ro.reshape(qs)[:, t0:t0 + W]) <= FWD_TOL, t0
+
+
 def test_train_stages_equal_the_whole_and_repeat_bit_for_bit(gpu, zt):
     B, T, H, Hkv, D = 1, 300, 8, 2, 128
     q, k, v, do = _inputs(gpu, zt, B, T, H, Hkv, D)
