@@ -442,8 +442,8 @@ def main():
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print("bench.py measures one GPU: this build's path runs on one MI355X (per-head/batch sharding "
-              "across GPUs is described in DESIGN.md and not built). Run with --gpus 1.", file=sys.stderr)
+        print("bench.py measures one GPU: this build's path runs on one MI355X (sharding by kv head or batch "
+              "across GPUs, which needs no collective, is not built). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     import torch
