@@ -139,12 +139,14 @@ def test_holder_scratch_contract_in_both_modes(gpu, zt, oracle, exact):
         zt.lib().zt_holder_deinit(p)
 
 
-def test_holder_backward_follows_what_the_buffers_hold(gpu, zt, oracle):
+@pytest.mark.parametrize("T,H,Hkv,D", [(150, 4, 2, 128), (150, 4, 4, 64), (120, 6, 2, 96)],
+                         ids=["head-split-scores", "mha-row-split-scores", "group3-row-split-scores"])
+def test_holder_backward_follows_what_the_buffers_hold(gpu, zt, oracle, T, H, Hkv, D):
     """The saved state is used only while it describes the buffers: a second
     backward, a backward after new q was uploaded, after a decode-shaped
     forward_at and after zt_holder_forget all give the twin's gradients for
-    what the buffers hold."""
-    T, H, Hkv, D = 150, 4, 2, 128
+    what the buffers hold; for an even head group and for groups that cannot
+    be halved (whose row-split dk/dv kernel reads the scores too)."""
     p = _holder(zt, T, H, Hkv, D)
     L = zt.lib()
     try:
