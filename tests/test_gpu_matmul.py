@@ -111,10 +111,11 @@ def test_matmul_refusals(gpu, zt):
 
 
 @pytest.mark.parametrize("tile", ["128", "64", "32"])
-@pytest.mark.parametrize("M,K,N", [(200, 70, 150), (33, 129, 65), (128, 64, 256)])
+@pytest.mark.parametrize("M,K,N", [(200, 70, 150), (33, 129, 65), (128, 64, 256), (256, 96, 384), (384, 160, 128)])
 def test_every_tile_size_passes_the_gate(gpu, zt, tune, tile, M, K, N):
     """Each workgroup tile (forced through ZT_GEMM_TILE), for all three
-    products, on ragged shapes."""
+    products, on ragged shapes and on whole tiles (M, N multiples of every
+    tile, K of the 32-deep slab: the unconditional-load path)."""
     tune({"ZT_GEMM_TILE": tile})
     rng = np.random.default_rng(M * K + N)
     a = rng.uniform(-1, 1, (M, K)).astype(np.float32)

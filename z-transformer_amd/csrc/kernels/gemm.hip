@@ -117,9 +117,26 @@ DEVI void operand(f4 (&x)[Tile<BT>::TW], const float *lds, int w0, int l16, int 
 template <int TW, bool KC>
 DEVI int local_index(int t, int j) { return KC ? 16 * t + j : TW * j + t; }
 
+// Offsets (floats, from the operand's base) of a thread's slab chunks when
+// every chunk is inside the matrix: fixed for the kernel apart from the
+// slab's k0, which moves the base (a scalar) by k0 (KC) or k0 rows (else).
+template <int BT, bool KC>
+DEVI void chunk_offsets(unsigned (&off)[Tile<BT>::NCH], int ld, int r0, int tid) {
+#pragma unroll
+    for (int n = 0; n < Tile<BT>::NCH; ++n) {
+        const int e = tid + n * NTHR;
+        off[n] = KC ? (unsigned)((r0 + e / (BK / 4)) * ld + 4 * (e % (BK / 4)))
+                    : (unsigned)((e / (BT / 4)) * ld + r0 + 4 * (e % (BT / 4)));
+    }
+}
+
 // A_KC: A stored M x K (else K x M).  B_KC: B stored N x K (else K x N).
-template <int BT, bool A_KC, bool B_KC>
-DEVI void gemm_body(const GemmArgs &g) {
+// FULL: M and N multiples of BT, K of BK, 16-byte rows: every slab chunk is
+// inside its matrix, so the loads are unconditional 16-byte loads from a
+// scalar slab base plus a fixed per-thread offset (no bounds arithmetic or
+// branches per chunk), and C is stored without bounds checks.
+template <int BT, bool A_KC, bool B_KC, bool FULL>
+DEVI void gemm_tile(const GemmArgs &g) {
     using TL = Tile<BT>;
     constexpr int TW = TL::TW, NCH = TL::NCH;
     __shared__ __attribute__((aligned(16))) float As[A_KC ? BT * LKC : BK * TL::LIC];
@@ -136,16 +153,35 @@ DEVI void gemm_body(const GemmArgs &g) {
         for (int j = 0; j < TW; ++j) acc[i][j] = zero4();
 
     f4 pa[NCH], pb[NCH];
-    fetch<BT, A_KC>(pa, g.a, g.lda, m0, g.M, 0, g.K, g.vec_a, tid);
-    fetch<BT, B_KC>(pb, g.b, g.ldb, n0, g.N, 0, g.K, g.vec_b, tid);
+    unsigned oa[FULL ? NCH : 1], ob[FULL ? NCH : 1];
+    auto fetch_full = [&](f4 (&pf)[NCH], const unsigned (&off)[FULL ? NCH : 1], const float *base) {
+#pragma unroll
+        for (int n = 0; n < NCH; ++n) pf[n] = *reinterpret_cast<const f4 *>(base + off[n]);
+    };
+    // The slab base at k0: k0 columns on (k contiguous) or k0 rows down.
+    auto slab = [](const float *p, int ld, bool kc, int k0) { return kc ? p + k0 : p + (size_t)k0 * ld; };
+    if constexpr (FULL) {
+        chunk_offsets<BT, A_KC>(oa, g.lda, m0, tid);
+        chunk_offsets<BT, B_KC>(ob, g.ldb, n0, tid);
+        fetch_full(pa, oa, g.a);
+        fetch_full(pb, ob, g.b);
+    } else {
+        fetch<BT, A_KC>(pa, g.a, g.lda, m0, g.M, 0, g.K, g.vec_a, tid);
+        fetch<BT, B_KC>(pb, g.b, g.ldb, n0, g.N, 0, g.K, g.vec_b, tid);
+    }
     for (int k0 = 0; k0 < g.K; k0 += BK) {
         __syncthreads();
         put<BT, A_KC>(As, pa, tid);
         put<BT, B_KC>(Bs, pb, tid);
         __syncthreads();
         if (k0 + BK < g.K) {
-            fetch<BT, A_KC>(pa, g.a, g.lda, m0, g.M, k0 + BK, g.K, g.vec_a, tid);
-            fetch<BT, B_KC>(pb, g.b, g.ldb, n0, g.N, k0 + BK, g.K, g.vec_b, tid);
+            if constexpr (FULL) {
+                fetch_full(pa, oa, slab(g.a, g.lda, A_KC, k0 + BK));
+                fetch_full(pb, ob, slab(g.b, g.ldb, B_KC, k0 + BK));
+            } else {
+                fetch<BT, A_KC>(pa, g.a, g.lda, m0, g.M, k0 + BK, g.K, g.vec_a, tid);
+                fetch<BT, B_KC>(pb, g.b, g.ldb, n0, g.N, k0 + BK, g.K, g.vec_b, tid);
+            }
         }
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
@@ -167,14 +203,14 @@ DEVI void gemm_body(const GemmArgs &g) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int m = m0 + wm + local_index<TW, A_KC>(i, 4 * grp + r);
-            if (m >= g.M) continue;
+            if (!FULL && m >= g.M) continue;
             float *crow = g.c + (size_t)m * g.ldc;
             if constexpr (!B_KC && TW == 4) {  // the lane's four columns are consecutive
                 const int n = n0 + wn + 4 * l16;
                 f4 v;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) v[j] = acc[i][j][r];
-                if (g.vec_c && n + 3 < g.N) {
+                if (FULL || (g.vec_c && n + 3 < g.N)) {
                     f4 *p = reinterpret_cast<f4 *>(crow + n);
                     *p = g.accumulate ? *p + v : v;
                 } else {
@@ -186,10 +222,18 @@ DEVI void gemm_body(const GemmArgs &g) {
 #pragma unroll
                 for (int j = 0; j < TW; ++j) {
                     const int n = n0 + wn + local_index<TW, B_KC>(j, l16);
-                    if (n < g.N) crow[n] = g.accumulate ? crow[n] + acc[i][j][r] : acc[i][j][r];
+                    if (FULL || n < g.N) crow[n] = g.accumulate ? crow[n] + acc[i][j][r] : acc[i][j][r];
                 }
             }
         }
+}
+template <int BT, bool A_KC, bool B_KC>
+DEVI void gemm_body(const GemmArgs &g) {
+    // Workgroup-uniform: the whole product is in full tiles (vec_c as well,
+    // so the C rows take 16-byte stores).
+    const bool full = g.vec_a && g.vec_b && g.vec_c && g.M % BT == 0 && g.N % BT == 0 && g.K % BK == 0;
+    if (full) gemm_tile<BT, A_KC, B_KC, true>(g);
+    else gemm_tile<BT, A_KC, B_KC, false>(g);
 }
 
 // Split-K variant for products too small to fill the device with slab tiles
