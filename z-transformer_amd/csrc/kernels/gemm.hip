@@ -125,8 +125,8 @@ DEVI void chunk_offsets(unsigned (&off)[Tile<BT>::NCH], int ld, int r0, int tid)
 #pragma unroll
     for (int n = 0; n < Tile<BT>::NCH; ++n) {
         const int e = tid + n * NTHR;
-        off[n] = KC ? (unsigned)((r0 + e / (BK / 4)) * ld + 4 * (e % (BK / 4)))
-                    : (unsigned)((e / (BT / 4)) * ld + r0 + 4 * (e % (BT / 4)));
+        off[n] = KC ? (unsigned)(r0 + e / (BK / 4)) * (unsigned)ld + 4u * (unsigned)(e % (BK / 4))
+                    : (unsigned)(e / (BT / 4)) * (unsigned)ld + (unsigned)r0 + 4u * (unsigned)(e % (BT / 4));
     }
 }
 
@@ -230,8 +230,12 @@ DEVI void gemm_tile(const GemmArgs &g) {
 template <int BT, bool A_KC, bool B_KC>
 DEVI void gemm_body(const GemmArgs &g) {
     // Workgroup-uniform: the whole product is in full tiles (vec_c as well,
-    // so the C rows take 16-byte stores).
-    const bool full = g.vec_a && g.vec_b && g.vec_c && g.M % BT == 0 && g.N % BT == 0 && g.K % BK == 0;
+    // so the C rows take 16-byte stores), and a k-contiguous operand's chunk
+    // offsets (up to M lda or N ldb floats) fit the 32-bit offsets.
+    constexpr unsigned long long kOff = 1ull << 32;
+    const bool full = g.vec_a && g.vec_b && g.vec_c && g.M % BT == 0 && g.N % BT == 0 && g.K % BK == 0 &&
+                      (!A_KC || (unsigned long long)g.M * (unsigned)g.lda < kOff) &&
+                      (!B_KC || (unsigned long long)g.N * (unsigned)g.ldb < kOff);
     if (full) gemm_tile<BT, A_KC, B_KC, true>(g);
     else gemm_tile<BT, A_KC, B_KC, false>(g);
 }
